@@ -1,0 +1,202 @@
+"""Benchmark of the split-KV paged decode-attention path on one MI355X.
+
+Workload (BASELINE.json metric config): batch 32, context 8192 per sequence, 32 q heads,
+8 kv heads, head_dim 128, fp16, page_size 16, page table a seeded random permutation of
+the 16384-page pool; synthetic N(0,1) data already resident in HBM.
+
+A step is one decode_attention call (pass 1 + pass 2) through the C ABI. Before every
+step a 1 GiB device fill evicts the 4 MB L2s and the 256 MB Infinity Cache, as the
+reference flushes L2 before each timed call (bench/microbench_cuda.py:75-90,140-157);
+HIP events on the launch stream bracket the call itself. The flush is enqueued without a
+host sync, so host launch overhead is hidden behind it and the events measure GPU time.
+
+Prints one JSON line. `value` is achieved algorithmic HBM bandwidth in TB/s
+(bytes of the reference's model, bench/microbench_cuda.py:114-121, plus page tables,
+divided by the p50 per-call time); `us_per_call` is the p50 time.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "decode-kernel_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = ("µs/call + achieved HBM TB/s (% peak), decode B=32 ctx=8k Hq32/Hkv8 d128")
+PEAK_GBPS = 8000.0          # MI355X HBM3E
+FLUSH_BYTES = 1 << 30
+TRAFFIC_FILE = ROOT / "profiles" / "pass1_metric_hbm_traffic.md"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--split", type=int, default=0, help="split_kv (0 = occupancy choice)")
+    ap.add_argument("--qk-path", type=int, default=0, help="0 default, 1 MFMA, 2 VALU")
+    ap.add_argument("--waves", type=int, default=0, help="wavefronts per workgroup (0 = 4)")
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=16,
+                    help="sequences of the workload the CPU baseline computes")
+    return ap.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per pass-1 launch recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(q, kv, indptr, ids, last, out, sample):
+    """The oracle (a numpy restatement of the reference's CPU path, src/reference.py) timed
+    on `sample` sequences of the same workload; also returns its max-abs difference from
+    the GPU output on those sequences."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle.reference import reference_attention_paged
+
+    cores = min(os.cpu_count() or 1, 16)
+    qn, kvn = q.cpu().numpy(), kv.cpu().numpy()
+    ipn, idn, ln = indptr.cpu().numpy(), ids.cpu().numpy(), last.cpu().numpy()
+    subset = list(range(min(sample, q.shape[0])))
+    with threadpool_limits(limits=cores):
+        blas = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            want = reference_attention_paged(qn, kvn, ipn, idn, ln, batch_subset=subset)
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    err = float(np.abs(out[subset].float().cpu().numpy() - want[subset]).max())
+    per_call_us = t / len(subset) * q.shape[0] * 1e6
+    return per_call_us, blas, len(subset), err
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path has no multi-GPU mode here)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import attention
+    import dk_lib
+    import layout
+
+    lib = dk_lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    B, ctx, hq, hkv, d = args.batch, args.ctx, 32, 8, 128
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table="permuted", seed=1)
+    split = attention.resolve_split(q, kv, ids, args.split)
+    nbytes = layout.attention_bytes(B, ctx, hq, hkv, d)
+    out = torch.empty_like(q)
+    ws_bytes = dk_lib.workspace_bytes(B, hq, d, split)
+    o_off, m_off, l_off, p_total = dk_lib.partials_layout(B, hq, d, split)
+    ws = torch.empty(max(ws_bytes, p_total), dtype=torch.uint8, device=dev)
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    strides = attention._strides(q, kv, out)
+    opts = dk_lib.options(args.qk_path, args.waves)
+    stream = torch.cuda.current_stream(dev)
+    code = attention._DTYPE_CODE[dtype]
+    common = (q.data_ptr(), kv.data_ptr(), indptr.data_ptr(), ids.data_ptr(), last.data_ptr())
+    shape = (B, hq, hkv, d, 16, kv.shape[0], ids.shape[0], code, ctypes.byref(strides))
+
+    def full_call():
+        return lib.dk_decode_attention_ex(*common, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          *shape, split, ctypes.byref(opts), stream.cuda_stream)
+
+    def pass1_call():
+        return lib.dk_decode_partials(*common, ws.data_ptr(), ws.numel(), *shape, split,
+                                      ctypes.byref(opts), stream.cuda_stream)
+
+    dk_lib.check(full_call(), "decode_attention")
+    dk_lib.check(pass1_call(), "decode_partials")
+    for _ in range(args.warmup):
+        full_call()
+    torch.cuda.synchronize()
+
+    def timed(fn, steps):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        for e0, e1 in evs:
+            flush.zero_()
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        return [e0.elapsed_time(e1) * 1e3 for e0, e1 in evs]     # microseconds
+
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    call_us = timed(full_call, args.steps)
+    wall = time.perf_counter() - wall0
+    pass1_us = timed(pass1_call, args.steps)
+    call_us.sort()
+    p50 = statistics.median(call_us)
+    p95 = call_us[min(len(call_us) - 1, int(math.ceil(0.95 * len(call_us))) - 1)]
+    p1_avg = statistics.fmean(pass1_us)
+    achieved = nbytes / (p1_avg * 1e-6) / 1e9           # GB/s, pass-1 kernel alone
+    # final correctness of the timed output
+    dk_lib.check(full_call(), "decode_attention")
+    torch.cuda.synchronize()
+    finite = bool(torch.isfinite(out).all())
+
+    rec = {
+        "metric": METRIC, "value": round(nbytes / (p50 * 1e-6) / 1e12, 4), "unit": "TB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
+        "config": {"workload": f"paged decode attention B={B} ctx={ctx} Hq={hq} Hkv={hkv} "
+                               f"D={d} {args.dtype} page_size=16 permuted pages",
+                   "batch": B, "context_length": ctx, "num_q_heads": hq, "num_kv_heads": hkv,
+                   "head_dim": d, "page_size": 16, "split_kv": split,
+                   "qk_path": "valu" if args.qk_path == 2 else "mfma"},
+        "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
+        "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
+        "bytes_per_call": nbytes, "wall_s_timed_loop": round(wall, 3),
+        "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": read_traffic(), "kernel": "dk_pass1 (split-KV pass 1)"},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        us, cores, n, err = cpu_baseline(q, kv, indptr, ids, last, out, args.cpu_sample)
+        rec["cpu_baseline"] = {
+            "value": round(us, 1), "unit": "us/call", "cores": cores, "kind": "port",
+            "tb_s": round(nbytes / (us * 1e-6) / 1e12, 5),
+            "sample": f"numpy fp32 restatement of reference_attention_paged on {n} of {B} "
+                      f"sequences (full ctx), median of 3, scaled to the whole batch"}
+        rec["max_abs_err_vs_fp32"] = err
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

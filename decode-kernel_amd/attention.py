@@ -1,0 +1,262 @@
+"""Decode attention over a FlashInfer-NHD paged KV cache, on MI355X through HIP.
+
+Drop-in for the reference dispatch (src/attention.py:26-58):
+
+    from attention import decode_attention
+    out = decode_attention(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=4)
+
+Same arguments and meaning; the reference's two pybind entry points
+(`decode_attention_naive`, `decode_attention_split_kv`, src/cuda_/attention_ext.cu:613-626)
+are provided too, behind `get_hip_ext()` (the counterpart of `get_cuda_ext()`,
+src/cuda_/build.py:256). Every call goes to libdk_decode.so (HIP, gfx950); there is no
+PyTorch or CPU fallback, and a missing library raises ImportError.
+
+Differences from the reference, all extensions: bf16 as well as fp16; any split_kv >= 1
+(the reference allows 1..32), and split_kv=0 or None picks the split from occupancy;
+work runs on torch's current stream of q's device (the reference used the legacy
+default stream); empty sequences (no pages) produce zeros.
+"""
+from __future__ import annotations
+
+import ctypes
+from types import SimpleNamespace
+from typing import Optional
+
+import torch
+
+import dk_lib
+from dk_lib import DecodeArgumentError
+
+PAGE_SIZE = 16
+SUPPORTED_HEAD_DIMS = (64, 128, 256)
+_DTYPE_CODE = {torch.float16: dk_lib.DK_F16, torch.bfloat16: dk_lib.DK_BF16}
+
+
+def _fail(msg: str) -> None:
+    raise DecodeArgumentError(msg)
+
+
+def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) -> None:
+    """Host-side checks: the reference's TORCH_CHECKs (attention_ext.cu:506-509,549-552)
+    plus the layout invariants that need no device read (src/layout.md:171-178)."""
+    for name, t in (("q", q), ("kv_data", kv_data), ("kv_indptr", kv_indptr),
+                    ("kv_indices", kv_indices), ("kv_last_page_len", kv_last_page_len)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if not q.is_cuda:
+        _fail("q must be on CUDA")
+    if q.dtype not in _DTYPE_CODE:
+        _fail(f"q must be fp16 or bf16, got {q.dtype}")
+    if q.dim() != 3:
+        _fail(f"q must be 3-D (batch, num_q_heads, head_dim), got shape {tuple(q.shape)}")
+    if kv_data.dim() != 5:
+        _fail("kv_data must be 5-D")
+    if kv_data.shape[1] != 2:
+        _fail("kv_data dim-1 must be 2 (K/V)")
+    if kv_data.dtype != q.dtype:
+        _fail(f"kv_data dtype {kv_data.dtype} must match q dtype {q.dtype}")
+    if kv_data.shape[2] != PAGE_SIZE:
+        _fail(f"page_size must be 16 for the HIP kernel, got {kv_data.shape[2]}")
+    if q.shape[2] != kv_data.shape[4]:
+        _fail(f"head_dim mismatch: q has {q.shape[2]}, kv_data has {kv_data.shape[4]}")
+    if q.shape[2] not in SUPPORTED_HEAD_DIMS:
+        _fail(f"head_dim must be 64, 128, or 256; got {q.shape[2]}")
+    if q.shape[1] % kv_data.shape[3] != 0:
+        _fail(f"num_q_heads ({q.shape[1]}) must be divisible by num_kv_heads "
+              f"({kv_data.shape[3]})")
+    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
+                    ("kv_last_page_len", kv_last_page_len)):
+        if t.dtype != torch.int32:
+            _fail(f"{name} must be int32, got {t.dtype}")
+        if t.dim() != 1:
+            _fail(f"{name} must be 1-D")
+        if t.device != q.device:
+            _fail(f"{name} must be on {q.device}, got {t.device}")
+    if kv_data.device != q.device:
+        _fail(f"kv_data must be on {q.device}, got {kv_data.device}")
+    if q.shape[0] != kv_indptr.shape[0] - 1:
+        _fail(f"q.shape[0] ({q.shape[0]}) must equal kv_indptr.shape[0] - 1 "
+              f"({kv_indptr.shape[0] - 1})")
+    if kv_last_page_len.shape[0] != q.shape[0]:
+        _fail("kv_last_page_len must have one entry per sequence")
+    if q.stride(2) != 1 or kv_data.stride(4) != 1:
+        _fail("the head_dim stride of q and kv_data must be 1")
+
+
+def _contig1d(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _strides(q, kv_data, out) -> dk_lib.DkStrides:
+    s = dk_lib.DkStrides()
+    s.q_b, s.q_h = q.stride(0), q.stride(1)
+    s.kv_p, s.kv_r, s.kv_s, s.kv_h = (kv_data.stride(0), kv_data.stride(1), kv_data.stride(2),
+                                      kv_data.stride(3))
+    if out is not None:
+        s.o_b, s.o_h = out.stride(0), out.stride(1)
+    return s
+
+
+def resolve_split(q: torch.Tensor, kv_data: torch.Tensor, kv_indices: torch.Tensor,
+                  split_kv: Optional[int]) -> int:
+    """split_kv as given, or the occupancy-based choice for 0 / None."""
+    if split_kv is None or split_kv == 0:
+        batch = q.shape[0]
+        avg = kv_indices.shape[0] // batch if batch else 0
+        return dk_lib.choose_split(batch, q.shape[1], kv_data.shape[3], q.shape[2],
+                                   _DTYPE_CODE[q.dtype], avg, q.device.index or 0)
+    if isinstance(split_kv, bool) or not isinstance(split_kv, int):
+        raise TypeError(f"split_kv must be an int, got {type(split_kv).__name__}")
+    if split_kv < 1:
+        _fail(f"split_kv must be >= 1 (or 0/None for automatic), got {split_kv}")
+    return split_kv
+
+
+def decode_attention(
+    q: torch.Tensor,
+    kv_data: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    kv_last_page_len: torch.Tensor,
+    split_kv: Optional[int] = 1,
+    *,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+    qk_path: int = 0,
+    waves_per_group: int = 0,
+) -> torch.Tensor:
+    """Decode attention over a paged KV cache (reference src/attention.py:26-58).
+
+    Args:
+        q                : (batch, num_q_heads, head_dim), fp16 or bf16, on a GPU
+        kv_data          : (num_pages, 2, 16, num_kv_heads, head_dim), q's dtype (NHD)
+        kv_indptr        : (batch + 1,) int32 CSR row pointer into kv_indices
+        kv_indices       : (kv_indptr[-1],) int32 physical page ids
+        kv_last_page_len : (batch,) int32 valid tokens in each sequence's last page
+        split_kv         : KV partitions per (sequence, head). 1 -> one pass writing the
+                           output directly; > 1 -> split partials + log-sum-exp merge;
+                           0 / None -> chosen from occupancy.
+        out, workspace   : optional preallocated output (batch, num_q_heads, head_dim) and
+                           uint8 scratch of dk_lib.workspace_bytes(...) bytes
+        qk_path, waves_per_group : tuning knobs (0 = defaults; qk_path 2 = VALU q.k)
+
+    Returns:
+        (batch, num_q_heads, head_dim) tensor, same dtype as q.
+    """
+    _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    lib = dk_lib.load()
+    split = resolve_split(q, kv_data, kv_indices, split_kv)
+    batch, hq, d = q.shape
+    if out is None:
+        out = torch.empty((batch, hq, d), dtype=q.dtype, device=q.device)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or \
+            out.stride(2) != 1:
+        _fail("out must match q's shape, dtype and device with unit head_dim stride")
+    if batch == 0:
+        return out
+    kv_indptr = _contig1d(kv_indptr)
+    kv_indices = _contig1d(kv_indices)
+    kv_last_page_len = _contig1d(kv_last_page_len)
+    ws_need = dk_lib.workspace_bytes(batch, hq, d, split)
+    if ws_need:
+        if workspace is None:
+            workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
+        elif workspace.numel() * workspace.element_size() < ws_need or \
+                workspace.device != q.device:
+            _fail(f"workspace must hold {ws_need} bytes on {q.device}")
+    ws_ptr = workspace.data_ptr() if ws_need else None
+    ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
+    strides = _strides(q, kv_data, out)
+    opts = dk_lib.options(qk_path, waves_per_group)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.dk_decode_attention_ex(
+            q.data_ptr(), kv_data.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+            kv_last_page_len.data_ptr(), out.data_ptr(), ws_ptr, ws_bytes, batch, hq,
+            kv_data.shape[3], d, kv_data.shape[2], kv_data.shape[0], kv_indices.shape[0],
+            _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts), stream)
+    dk_lib.check(rc, "decode_attention")
+    return out
+
+
+def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv: int,
+                    *, qk_path: int = 0, waves_per_group: int = 0):
+    """Pass 1 only. Returns (partial_O (B,Hq,S,D), partial_m (B,Hq,S), partial_l (B,Hq,S)),
+    fp32, with the semantics of the reference partition kernel
+    (src/cuda_/attention_ext.cu:207-349): m is the split's max of q.k*scale (-1e9 when the
+    split is empty), l = sum exp(score - m), O = sum exp(score - m) * V (unnormalised)."""
+    _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    lib = dk_lib.load()
+    split = resolve_split(q, kv_data, kv_indices, split_kv)
+    batch, hq, d = q.shape
+    off_o, off_m, off_l, total = dk_lib.partials_layout(batch, hq, d, split)
+    ws = torch.empty(total, dtype=torch.uint8, device=q.device)
+    strides = _strides(q, kv_data, None)
+    opts = dk_lib.options(qk_path, waves_per_group)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.dk_decode_partials(
+            q.data_ptr(), kv_data.data_ptr(), _contig1d(kv_indptr).data_ptr(),
+            _contig1d(kv_indices).data_ptr(), _contig1d(kv_last_page_len).data_ptr(),
+            ws.data_ptr(), total, batch, hq, kv_data.shape[3], d, kv_data.shape[2],
+            kv_data.shape[0], kv_indices.shape[0], _DTYPE_CODE[q.dtype], ctypes.byref(strides),
+            split, ctypes.byref(opts), stream)
+    dk_lib.check(rc, "decode_partials")
+    rows = batch * hq * split
+    po = ws[off_o:off_o + rows * d * 4].view(torch.float32).view(batch, hq, split, d)
+    pm = ws[off_m:off_m + rows * 4].view(torch.float32).view(batch, hq, split)
+    pl = ws[off_l:off_l + rows * 4].view(torch.float32).view(batch, hq, split)
+    return po, pm, pl
+
+
+def merge_partials(partial_o: torch.Tensor, partial_m: torch.Tensor, partial_l: torch.Tensor,
+                   dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Pass 2 only: log-sum-exp merge of fp32 partials (reference decode_attn_reduce_kernel,
+    src/cuda_/attention_ext.cu:363-406) into a (B, Hq, D) tensor of `dtype`."""
+    if dtype not in _DTYPE_CODE:
+        _fail(f"dtype must be fp16 or bf16, got {dtype}")
+    batch, hq, split, d = partial_o.shape
+    if partial_m.shape != (batch, hq, split) or partial_l.shape != (batch, hq, split):
+        _fail("partial_m / partial_l must be (B, Hq, S)")
+    lib = dk_lib.load()
+    off_o, off_m, off_l, total = dk_lib.partials_layout(batch, hq, d, split)
+    ws = torch.empty(total, dtype=torch.uint8, device=partial_o.device)
+    rows = batch * hq * split
+    ws[off_o:off_o + rows * d * 4].view(torch.float32).copy_(partial_o.reshape(-1))
+    ws[off_m:off_m + rows * 4].view(torch.float32).copy_(partial_m.reshape(-1))
+    ws[off_l:off_l + rows * 4].view(torch.float32).copy_(partial_l.reshape(-1))
+    out = torch.empty((batch, hq, d), dtype=dtype, device=partial_o.device)
+    with torch.cuda.device(partial_o.device):
+        stream = torch.cuda.current_stream(partial_o.device).cuda_stream
+        rc = lib.dk_merge_partials(ws.data_ptr(), total, out.data_ptr(), batch, hq, d,
+                                   _DTYPE_CODE[dtype], out.stride(0), out.stride(1), split,
+                                   stream)
+    dk_lib.check(rc, "merge_partials")
+    return out
+
+
+# ---- the reference's extension-module surface (src/cuda_/attention_ext.cu:613-626)
+
+def decode_attention_naive(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
+    """One pass per (sequence, kv head): the split_kv == 1 route."""
+    return decode_attention(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=1)
+
+
+def decode_attention_split_kv(q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                              split_kv: int = 4):
+    """Split-KV partials + log-sum-exp merge."""
+    return decode_attention(q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                            split_kv=split_kv)
+
+
+_EXT = None
+
+
+def get_hip_ext():
+    """Object with the reference extension's two entry points (cf. get_cuda_ext())."""
+    global _EXT
+    if _EXT is None:
+        dk_lib.load()
+        _EXT = SimpleNamespace(decode_attention_naive=decode_attention_naive,
+                               decode_attention_split_kv=decode_attention_split_kv)
+    return _EXT

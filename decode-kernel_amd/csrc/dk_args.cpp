@@ -1,0 +1,167 @@
+// Host-only argument checking for libdk_decode (compiled with g++, no HIP).
+//
+// The checks mirror the reference's TORCH_CHECKs (src/cuda_/attention_ext.cu:506-509,
+// 549-552: dtype, page_size == 16, split range, head_dim dispatch at :532-535) and the
+// layout invariants that need no device read (src/layout.md:171-178: kv rank / K-V dim,
+// H_q divisible by H_kv, q/kv dtype match is implied by the single `dtype`). Invariants
+// that need device data (kv_indptr[-1] == len(kv_indices), last_page_len in [1, P]) are
+// the Python layer's optional `validate` step; the kernels clamp those values instead.
+#include "dk_args.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+namespace dk {
+
+namespace {
+thread_local std::string g_error;
+}
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+void clear_error() { g_error.clear(); }
+
+const char* last_error() { return g_error.c_str(); }
+
+size_t partials_bytes(int32_t batch, int32_t hq, int32_t head_dim, int32_t split) {
+  if (batch <= 0 || hq <= 0 || head_dim <= 0 || split <= 0) return 0;
+  const size_t rows = (size_t)batch * (size_t)hq * (size_t)split;
+  size_t off_o, off_m, off_l;
+  partials_layout(batch, hq, head_dim, split, &off_o, &off_m, &off_l);
+  return off_l + rows * sizeof(float);
+}
+
+size_t workspace_bytes(int32_t batch, int32_t hq, int32_t head_dim, int32_t split) {
+  return split > 1 ? partials_bytes(batch, hq, head_dim, split) : 0;
+}
+
+void partials_layout(int32_t batch, int32_t hq, int32_t head_dim, int32_t split,
+                     size_t* off_o, size_t* off_m, size_t* off_l) {
+  const size_t rows = (size_t)batch * (size_t)hq * (size_t)split;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  *off_o = 0;
+  *off_m = up(rows * (size_t)head_dim * sizeof(float));
+  *off_l = *off_m + up(rows * sizeof(float));
+}
+
+int heads_per_group(int group, int head_dim) {
+  const int cap = head_dim >= 256 ? 4 : 8;
+  for (int h = cap; h > 1; h >>= 1)
+    if (group % h == 0) return h;
+  return 1;
+}
+
+int choose_split(int64_t units, int64_t slots, int64_t avg_pages_per_seq, int waves) {
+  if (units <= 0) return 1;
+  // Enough workgroups to fill every resident slot once (one round, no tail), but no
+  // split so fine that a wavefront gets fewer than ~4 pages.
+  int64_t s = (slots + units - 1) / units;
+  const int64_t min_pages_per_split = 4 * (int64_t)std::max(waves, 1);
+  const int64_t max_s = std::max<int64_t>(1, avg_pages_per_seq / min_pages_per_split);
+  s = std::min(s, max_s);
+  s = std::max<int64_t>(s, 1);
+  return (int)std::min<int64_t>(s, 4096);
+}
+
+int validate(const Problem& p) {
+  if (p.batch < 0) return set_error(DK_EINVAL, "batch must be >= 0, got %d", p.batch);
+  if (p.hq <= 0 || p.hkv <= 0)
+    return set_error(DK_EINVAL, "num_q_heads and num_kv_heads must be >= 1 (got %d, %d)",
+                     p.hq, p.hkv);
+  if (p.hq % p.hkv != 0)
+    return set_error(DK_EINVAL,
+                     "num_q_heads (%d) must be divisible by num_kv_heads (%d)", p.hq, p.hkv);
+  if (p.head_dim != 64 && p.head_dim != 128 && p.head_dim != 256)
+    return set_error(DK_EINVAL, "head_dim must be 64, 128, or 256; got %d", p.head_dim);
+  if (p.page_size != kPageSize)
+    return set_error(DK_EINVAL, "page_size must be 16 for the HIP kernel; got %d",
+                     p.page_size);
+  if (p.dtype != DK_F16 && p.dtype != DK_BF16)
+    return set_error(DK_EINVAL, "dtype must be DK_F16 (0) or DK_BF16 (1); got %d", p.dtype);
+  if (p.split < 1) return set_error(DK_EINVAL, "split_kv must be >= 1; got %d", p.split);
+  if (p.split > 4096) return set_error(DK_EINVAL, "split_kv must be <= 4096; got %d", p.split);
+  if (p.num_indices < 0 || p.num_indices > INT32_MAX)
+    return set_error(DK_EINVAL, "num_indices must be in [0, 2^31); got %lld",
+                     (long long)p.num_indices);
+  if (p.num_pages < 0) return set_error(DK_EINVAL, "num_pages must be >= 0");
+  if (p.num_indices > 0 && p.num_pages == 0)
+    return set_error(DK_EINVAL, "kv_indices is non-empty but the page pool is empty");
+  const dk_options& o = p.opt;
+  if (o.qk_path < 0 || o.qk_path > 2)
+    return set_error(DK_EINVAL, "options.qk_path must be 0, 1 or 2; got %d", o.qk_path);
+  if (o.waves_per_group != 0 && o.waves_per_group != 1 && o.waves_per_group != 2 &&
+      o.waves_per_group != 4)
+    return set_error(DK_EINVAL, "options.waves_per_group must be 0, 1, 2 or 4; got %d",
+                     o.waves_per_group);
+  for (int r : o.reserved)
+    if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
+  if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything
+
+  if (!p.q || !p.kv || !p.indptr || !p.last_len)
+    return set_error(DK_ENULL, "q, kv_data, kv_indptr and kv_last_page_len must be non-NULL");
+  if (p.num_indices > 0 && !p.indices)
+    return set_error(DK_ENULL, "kv_indices must be non-NULL");
+  if (p.need_out && !p.out) return set_error(DK_ENULL, "out must be non-NULL");
+
+  // Strides: non-negative, and every 16-byte vector access aligned. Row loads of K are
+  // 16 bytes wide (8 elements), so page/row/head strides and the base must be multiples
+  // of 8 elements; q rows are loaded the same way.
+  const dk_strides& s = p.st;
+  const int64_t all[] = {s.q_b, s.q_h, s.kv_p, s.kv_r, s.kv_s, s.kv_h, s.o_b, s.o_h};
+  for (int64_t v : all)
+    if (v < 0) return set_error(DK_EINVAL, "strides must be non-negative");
+  const int64_t esize = 2;
+  auto aligned16 = [](int64_t elems) { return (elems * 2) % 16 == 0; };
+  if (!aligned16(s.q_b) || !aligned16(s.q_h) || !aligned16(s.kv_p) || !aligned16(s.kv_r) ||
+      !aligned16(s.kv_s) || !aligned16(s.kv_h))
+    return set_error(DK_EUNSUPPORTED,
+                     "q and kv_data strides must be multiples of 8 elements (16-byte rows); "
+                     "pass contiguous tensors");
+  if (((uintptr_t)p.q % 16) != 0 || ((uintptr_t)p.kv % 16) != 0)
+    return set_error(DK_EUNSUPPORTED, "q and kv_data must be 16-byte aligned");
+  // Offsets inside one page are carried in 32 bits.
+  const int64_t in_page = (s.kv_r + (int64_t)(kPageSize - 1) * s.kv_s +
+                           (int64_t)(p.hkv - 1) * s.kv_h + p.head_dim) * esize;
+  if (in_page >= ((int64_t)1 << 31))
+    return set_error(DK_EUNSUPPORTED, "kv_data page extent exceeds 2 GiB");
+
+  const Plan plan = make_plan(p);
+  if (plan.pass1_groups > INT32_MAX)
+    return set_error(DK_EINVAL, "grid too large: batch*kv_heads*split = %lld workgroups",
+                     (long long)plan.pass1_groups);
+  // Two passes (split > 1) and the pass-1-only entry point write fp32 partials.
+  if (p.split > 1 || !p.need_out) {
+    const size_t req = partials_bytes(p.batch, p.hq, p.head_dim, p.split);
+    if (!p.workspace || p.workspace_bytes < req)
+      return set_error(DK_EWORKSPACE, "workspace of %zu bytes required, %zu given", req,
+                       p.workspace_bytes);
+    if (((uintptr_t)p.workspace % 256) != 0)
+      return set_error(DK_EWORKSPACE, "workspace must be 256-byte aligned");
+  }
+  return DK_OK;
+}
+
+Plan make_plan(const Problem& p) {
+  Plan pl;
+  pl.group = p.hq / p.hkv;
+  pl.heads = heads_per_group(pl.group, p.head_dim);
+  pl.chunks = pl.group / pl.heads;
+  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : 4;
+  pl.mfma = p.opt.qk_path != 2;
+  pl.pass1_groups = (int64_t)p.batch * p.hkv * pl.chunks * std::max(p.split, 1);
+  return pl;
+}
+
+}  // namespace dk

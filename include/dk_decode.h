@@ -1,0 +1,155 @@
+/*
+ * dk_decode.h — C ABI of the MI355X (gfx950) split-KV paged decode-attention library
+ * (libdk_decode.so).
+ *
+ * One query token per sequence attends over a paged KV cache in the FlashInfer NHD
+ * layout:
+ *   q        (batch, num_q_heads, head_dim)                       fp16 | bf16
+ *   kv_data  (num_pages, 2, page_size, num_kv_heads, head_dim)    same dtype as q
+ *            [:, 0] = K, [:, 1] = V
+ *   kv_indptr (batch + 1) int32, kv_indices (kv_indptr[batch]) int32,
+ *   kv_last_page_len (batch) int32 in [1, page_size]
+ *   out      (batch, num_q_heads, head_dim)                       same dtype as q
+ * GQA: q head h reads kv head h / (num_q_heads / num_kv_heads).
+ * scale = 1/sqrt(head_dim); softmax state and split partials are fp32.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers except `strides`, `opts` and the out-parameters
+ *     of the size/choice helpers, which are host pointers.
+ *   - Strides are in ELEMENTS; the last (head_dim) stride of q, kv_data and out must be 1.
+ *   - Work is enqueued on `hip_stream` (a hipStream_t; NULL = the legacy default stream)
+ *     and is stream-ordered. No entry point allocates device memory: the caller owns
+ *     `out` and `workspace`.
+ *   - Return value: 0 on success; < 0 invalid argument (nothing was launched);
+ *     > 0 a hipError_t from the launch. dk_last_error() then holds a message
+ *     (thread-local, valid until the next call on the same thread).
+ *   - Device-side safety: page ids outside [0, num_pages), kv_indptr entries outside
+ *     [0, num_indices] and kv_last_page_len outside [0, page_size] are clamped inside
+ *     the kernels so that no access leaves the buffers; results for such inputs are
+ *     unspecified (the reference does not check them either).
+ */
+#ifndef DK_DECODE_H
+#define DK_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DK_ABI_VERSION 1
+
+/* Element type of q / kv_data / out. The reference is fp16 only
+ * (src/cuda_/attention_ext.cu:507,550); bf16 is an extension. */
+typedef enum { DK_F16 = 0, DK_BF16 = 1 } dk_dtype;
+
+/* Error codes (< 0). */
+enum {
+  DK_OK = 0,
+  DK_EINVAL = -1,      /* bad shape / size / stride / dtype / split value   */
+  DK_ENULL = -2,       /* required pointer is NULL                           */
+  DK_EWORKSPACE = -3,  /* workspace missing or smaller than dk_workspace_bytes */
+  DK_EUNSUPPORTED = -4 /* valid input this build does not implement           */
+};
+
+/* Element strides. Replaces the int32 stride marshalling of
+ * src/cuda_/attention_ext.cu:577-587 (here int64, so pools > 2^31 elements work). */
+typedef struct {
+  int64_t q_b, q_h;                /* q (batch, num_q_heads, head_dim)            */
+  int64_t kv_p, kv_r, kv_s, kv_h;  /* kv_data (num_pages, 2, page_size, Hkv, D)   */
+  int64_t o_b, o_h;                /* out (batch, num_q_heads, head_dim)          */
+} dk_strides;
+
+/* Optional tuning knobs (NULL = defaults). No counterpart in the reference, which
+ * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
+typedef struct {
+  int32_t qk_path;        /* 0 = default (MFMA), 1 = MFMA q.k, 2 = VALU q.k (A/B baseline) */
+  int32_t waves_per_group;/* 0 = default (4); 1, 2 or 4 wavefronts per workgroup         */
+  int32_t reserved[6];    /* must be 0                                                    */
+} dk_options;
+
+/* ABI version of the loaded library (DK_ABI_VERSION). */
+int dk_abi_version(void);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* dk_last_error(void);
+
+/* Bytes of fp32 scratch that dk_decode_attention needs for `split_kv` splits:
+ * partial_O (batch, Hq, split, D) + partial_m and partial_l (batch, Hq, split),
+ * the scratch of src/cuda_/attention_ext.cu:563-568 / src/layout.md:142-152.
+ * 0 when split_kv == 1 (single pass, no scratch). split_kv must be >= 1. */
+size_t dk_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t head_dim,
+                          int32_t split_kv);
+
+/* Byte offsets of partial_O, partial_m and partial_l inside the workspace and its total
+ * size for split_kv >= 1 (layout of src/layout.md:148-152, all fp32, C-contiguous,
+ * each array 256-byte aligned). dk_decode_partials needs `total` bytes even for
+ * split_kv == 1. Returns 0 or DK_EINVAL. */
+int dk_partials_layout(int32_t batch, int32_t num_q_heads, int32_t head_dim,
+                       int32_t split_kv, size_t* off_o, size_t* off_m, size_t* off_l,
+                       size_t* total);
+
+/* Split count chosen from occupancy over the device's compute units, for an average of
+ * `avg_pages_per_seq` pages per sequence (use num_indices / batch: no device sync).
+ * No counterpart in the reference (split_kv is always caller-given there,
+ * src/attention.py:32). Returns >= 1, or < 0 on a bad argument / HIP error. */
+int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t dtype, int64_t avg_pages_per_seq,
+                    int32_t device);
+
+/* decode_attention: pass 1 (split-KV partials, one workgroup per (sequence, kv head,
+ * split)) then pass 2 (log-sum-exp merge). split_kv == 1 runs one pass that writes
+ * `out` directly (no workspace needed). split_kv == 0 picks the split with
+ * dk_choose_split on the current device.
+ * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
+ * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
+ * functions behind src/attention.py:50-58. Differences: the caller allocates `out`
+ * and the workspace; any split_kv >= 1 (the reference caps it at 32); bf16; int64
+ * page offsets; explicit stream. */
+int dk_decode_attention(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                        const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                        void* out, void* workspace, size_t workspace_bytes,
+                        int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t page_size, int64_t num_pages,
+                        int64_t num_indices, int32_t dtype, const dk_strides* strides,
+                        int32_t split_kv, void* hip_stream);
+
+/* dk_decode_attention with tuning options (NULL = defaults). */
+int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                           const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                           void* out, void* workspace, size_t workspace_bytes,
+                           int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t page_size, int64_t num_pages,
+                           int64_t num_indices, int32_t dtype, const dk_strides* strides,
+                           int32_t split_kv, const dk_options* opts, void* hip_stream);
+
+/* Pass 1 only: writes partial_O / partial_m / partial_l for split_kv >= 1 splits into
+ * the workspace (layout from dk_partials_layout; partial_m is the split's max of
+ * q.k*scale, -1e9 for an empty split, partial_l = sum exp(score - partial_m),
+ * partial_O = sum exp(score - partial_m) * V, unnormalised).
+ * Replaces the partition launch launch_partition_hd (src/cuda_/attention_ext.cu:452-476)
+ * with the semantics of decode_attn_partition_kernel (:207-349). `out`-related strides
+ * are ignored. */
+int dk_decode_partials(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                       void* workspace, size_t workspace_bytes,
+                       int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t page_size, int64_t num_pages,
+                       int64_t num_indices, int32_t dtype, const dk_strides* strides,
+                       int32_t split_kv, const dk_options* opts, void* hip_stream);
+
+/* Pass 2 only: log-sum-exp merge of the workspace partials into `out`
+ * (o_b, o_h element strides). Replaces launch_reduce_hd / decode_attn_reduce_kernel
+ * (src/cuda_/attention_ext.cu:478-495, :363-406). A (sequence, head) whose splits are
+ * all empty gets 0. */
+int dk_merge_partials(const void* workspace, size_t workspace_bytes, void* out,
+                      int32_t batch, int32_t num_q_heads, int32_t head_dim,
+                      int32_t dtype, int64_t o_b, int64_t o_h, int32_t split_kv,
+                      void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DK_DECODE_H */

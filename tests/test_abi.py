@@ -1,0 +1,194 @@
+"""CPU tests of the C ABI (libdk_decode.so) and of the host-side argument checks.
+
+No kernel is launched here: every call below is rejected by argument validation before
+any HIP call, or is a pure size/layout helper.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import attention
+import dk_lib
+import layout
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "dk_decode.h"
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(dk_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_loads_and_reports_abi_version():
+    lib = dk_lib.load()
+    assert lib.dk_abi_version() == dk_lib.ABI_VERSION
+    assert lib.dk_last_error() == b""
+
+
+def test_every_declared_symbol_is_exported():
+    lib = dk_lib.load()
+    names = _declared_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in dk_decode.h but not exported"
+    assert set(names) == set(dk_lib.SIGNATURES), "ctypes signatures out of sync with header"
+
+
+def test_workspace_and_partials_layout():
+    # partial_O (B,Hq,S,D) f32 + partial_m/l (B,Hq,S) f32, each 256-byte aligned
+    assert dk_lib.workspace_bytes(32, 32, 128, 1) == 0
+    o, m, l, total = dk_lib.partials_layout(32, 32, 128, 4)
+    rows = 32 * 32 * 4
+    assert o == 0 and m == rows * 128 * 4 and l == m + rows * 4 and total == l + rows * 4
+    assert dk_lib.workspace_bytes(32, 32, 128, 4) == total
+    assert dk_lib.partials_layout(3, 5, 64, 1)[3] > 0
+    with pytest.raises(dk_lib.DecodeArgumentError):
+        dk_lib.partials_layout(1, 1, 64, 0)
+
+
+def _call(lib, **kw):
+    """dk_decode_attention_ex with a valid metric-shaped problem, overridden by kw.
+    Pointers are fake non-NULL 256-aligned values: validation rejects before any use."""
+    args = dict(q=0x10000, kv=0x20000, indptr=0x30000, indices=0x40000, last=0x50000,
+                out=0x60000, ws=0x70000, ws_bytes=1 << 30, batch=2, hq=32, hkv=8, d=128,
+                page=16, num_pages=64, num_indices=64, dtype=dk_lib.DK_F16, split=4,
+                strides=None, opts=None)
+    args.update(kw)
+    st = args["strides"]
+    if st is None:
+        st = dk_lib.DkStrides(32 * 128, 128, 2 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128, 128,
+                              32 * 128, 128)
+    opts = args["opts"] or dk_lib.options()
+    return lib.dk_decode_attention_ex(
+        args["q"], args["kv"], args["indptr"], args["indices"], args["last"], args["out"],
+        args["ws"], args["ws_bytes"], args["batch"], args["hq"], args["hkv"], args["d"],
+        args["page"], args["num_pages"], args["num_indices"], args["dtype"], ctypes.byref(st),
+        args["split"], ctypes.byref(opts), None)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(d=96), dk_lib.DK_EINVAL, "head_dim"),
+    (dict(page=8), dk_lib.DK_EINVAL, "page_size"),
+    (dict(hq=30), dk_lib.DK_EINVAL, "divisible"),
+    (dict(dtype=7), dk_lib.DK_EINVAL, "dtype"),
+    (dict(split=5000), dk_lib.DK_EINVAL, "split_kv"),
+    (dict(split=-1), dk_lib.DK_EINVAL, "split_kv"),
+    (dict(batch=-1), dk_lib.DK_EINVAL, "batch"),
+    (dict(num_indices=-1), dk_lib.DK_EINVAL, "num_indices"),
+    (dict(num_pages=0), dk_lib.DK_EINVAL, "page pool"),
+    (dict(q=None), dk_lib.DK_ENULL, "non-NULL"),
+    (dict(out=None), dk_lib.DK_ENULL, "out"),
+    (dict(ws=None), dk_lib.DK_EWORKSPACE, "workspace"),
+    (dict(ws_bytes=100), dk_lib.DK_EWORKSPACE, "workspace"),
+    (dict(ws=0x70004), dk_lib.DK_EWORKSPACE, "aligned"),
+    (dict(q=0x10002), dk_lib.DK_EUNSUPPORTED, "aligned"),
+    (dict(strides=dk_lib.DkStrides(32 * 128, 127, 2 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128,
+                                   128, 32 * 128, 128)), dk_lib.DK_EUNSUPPORTED, "strides"),
+    (dict(strides=dk_lib.DkStrides(-1, 128, 0, 0, 0, 0, 0, 0)), dk_lib.DK_EINVAL, "non-negative"),
+    (dict(opts=dk_lib.options(qk_path=3)), dk_lib.DK_EINVAL, "qk_path"),
+    (dict(opts=dk_lib.options(waves_per_group=3)), dk_lib.DK_EINVAL, "waves_per_group"),
+])
+def test_invalid_arguments_are_rejected_before_launch(kw, code, needle):
+    lib = dk_lib.load()
+    rc = _call(lib, **kw)
+    assert rc == code
+    assert needle in lib.dk_last_error().decode()
+
+
+def test_split_one_needs_no_workspace_and_batch_zero_is_a_noop():
+    lib = dk_lib.load()
+    assert _call(lib, batch=0, q=None, kv=None, out=None) == dk_lib.DK_OK
+    # split 1 with no workspace: validation passes (the launch itself is not attempted
+    # here: a zero-sized batch returns before it)
+    assert _call(lib, batch=0, split=1, ws=None, ws_bytes=0) == dk_lib.DK_OK
+
+
+def test_null_strides_and_partials_entry_point():
+    lib = dk_lib.load()
+    rc = lib.dk_decode_attention(0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000, None, 0,
+                                 1, 32, 8, 128, 16, 8, 8, 0, None, 1, None)
+    assert rc == dk_lib.DK_ENULL
+    st = dk_lib.DkStrides()
+    rc = lib.dk_decode_partials(0x10000, 0x20000, 0x30000, 0x40000, 0x50000, None, 0, 1, 32, 8,
+                                128, 16, 8, 8, 0, ctypes.byref(st), 0, None, None)
+    assert rc == dk_lib.DK_EINVAL
+    rc = lib.dk_merge_partials(None, 0, None, 1, 32, 96, 0, 0, 0, 4, None)
+    assert rc == dk_lib.DK_EINVAL
+
+
+# ---------------------------------------------------------------- Python-side checks
+
+def _cpu_inputs(dtype=torch.float16, d=64):
+    q, kv, indptr, ids, last, _ = layout.synthesize(2, 40, 8, 2, d, dtype=dtype, device="cpu")
+    return q, kv, indptr, ids, last
+
+
+def test_python_rejects_cpu_tensors_like_the_reference():
+    q, kv, indptr, ids, last = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="q must be on CUDA"):
+        attention.decode_attention(q, kv, indptr, ids, last, split_kv=4)
+
+
+def test_python_error_type_is_both_value_and_runtime_error():
+    assert issubclass(dk_lib.DecodeArgumentError, ValueError)
+    assert issubclass(dk_lib.DecodeArgumentError, RuntimeError)
+    assert issubclass(layout.LayoutError, ValueError)
+    assert issubclass(layout.LayoutError, AssertionError)
+
+
+def test_layout_validate_catches_each_invariant():
+    q, kv, indptr, ids, last = _cpu_inputs()
+    lay = layout.PagedKVLayout(16, 64, 2, torch.float16)
+    lay.validate(kv, indptr, ids, last)
+    with pytest.raises(layout.LayoutError, match="5-D"):
+        lay.validate(kv[0], indptr, ids, last)
+    with pytest.raises(layout.LayoutError, match="kv_indptr"):
+        lay.validate(kv, indptr, ids[:-1], last)
+    with pytest.raises(layout.LayoutError, match="> 0"):
+        lay.validate(kv, indptr, ids, last * 0)
+    with pytest.raises(layout.LayoutError, match="<= page_size"):
+        lay.validate(kv, indptr, ids, last + 16)
+    with pytest.raises(layout.LayoutError, match="out of range"):
+        lay.validate(kv, indptr, ids + 100, last)
+    with pytest.raises(layout.LayoutError, match="dtype"):
+        lay.validate(kv.float(), indptr, ids, last)
+
+
+def test_build_block_table_matches_reference_semantics():
+    indptr, ids, last = layout.build_block_table(3, 33, 16, device="cpu")
+    assert indptr.tolist() == [0, 3, 6, 9]
+    assert ids.tolist() == list(range(9))
+    assert last.tolist() == [1, 1, 1]
+    _, _, last = layout.build_block_table(2, 32, 16, device="cpu")
+    assert last.tolist() == [16, 16]
+
+
+def test_synthesize_draws_q_first_then_kv():
+    q, kv, *_ = layout.synthesize(2, 20, 4, 2, 64, device="cpu", seed=5)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(5)
+    q2 = torch.randn(2, 4, 64, dtype=torch.float16, generator=g)
+    kv2 = torch.randn(4, 2, 16, 2, 64, dtype=torch.float16, generator=g)
+    assert torch.equal(q, q2) and torch.equal(kv, kv2)
+    with pytest.raises(ValueError):
+        layout.synthesize(1, 16, 6, 4, 64, device="cpu")
+
+
+def test_synthesize_paged_freelist_is_unique_and_ragged():
+    lens = layout.ragged_lengths(64, 128, 8192, seed=3)
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        64, lens, 4, 1, 64, device="cpu", page_table="freelist", pool_pages=20000, seed=3)
+    assert kv.shape[0] == 20000
+    assert len(set(ids.tolist())) == ids.numel()                      # no aliasing
+    assert int(ids.min()) >= 0 and int(ids.max()) < 20000
+    assert layout.seq_lens(indptr, last).tolist() == lens
+    assert ((last >= 1) & (last <= 16)).all()
+
+
+def test_attention_bytes_matches_reference_model():
+    # bench/microbench_cuda.py:114-121 (Q + KV + O) plus the int32 tables
+    b = layout.attention_bytes(32, 8192, 32, 8, 128)
+    assert b == 1_074_266_112 + 4 * 33 + 4 * 32 * 512 + 4 * 32

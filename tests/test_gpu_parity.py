@@ -1,0 +1,322 @@
+"""GPU parity tests: the HIP decode path (through libdk_decode.so's C ABI) against the
+CPU oracle and the brute-force golden fixtures.
+
+Tolerance (north star): max-abs error <= 1e-2 vs the fp32 reference for fp16 / bf16
+outputs; the reference's own gates add mean-abs <= 1e-3 (notebook.ipynb:203-204).
+Results must be bitwise identical on re-runs (notebook.ipynb:258).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import attention
+import layout
+from attention import decode_attention, decode_partials, merge_partials
+from helpers import err_stats, golden_to_torch, load_golden, to_np
+from oracle import reference as ref
+from oracle import split_kv as skv
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MAX_ERR = 1e-2
+MEAN_ERR = 1e-3
+
+
+def _oracle(q, kv, indptr, ids, last, batch_subset=None):
+    return ref.reference_attention_paged(to_np(q), to_np(kv), to_np(indptr), to_np(ids),
+                                         to_np(last), batch_subset=batch_subset)
+
+
+def _check(out, want, rows=None, max_err=MAX_ERR, mean_err=MEAN_ERR, label=""):
+    if rows is not None:
+        out, want = out[rows], want[rows]
+    assert torch.isfinite(out).all(), f"{label}: non-finite output"
+    mx, mean = err_stats(out, want)
+    assert mx <= max_err and mean <= mean_err, f"{label}: max {mx:.3e} mean {mean:.3e}"
+    return mx
+
+
+def _announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+@pytest.mark.parametrize("name", ["gqa4_d64_f16", "gqa8_d128_bf16", "mha_d128_f16"])
+@pytest.mark.parametrize("split", [1, 2, 3, 8, 0])
+@pytest.mark.parametrize("qk_path", [1, 2])
+def test_golden_outputs(name, split, qk_path):
+    _announce(f"golden {name} split={split} qk_path={qk_path}")
+    z, dtype = load_golden(name)
+    q, kv, indptr, ids, last = golden_to_torch(z, dtype, DEV)
+    out = decode_attention(q, kv, indptr, ids, last, split_kv=split, qk_path=qk_path)
+    torch.cuda.synchronize()
+    # output rounding dominates: half an ulp at |out| < 4 is <= 2e-3 (fp16), 8e-3 (bf16)
+    tol = 4e-3 if dtype == "f16" else 1e-2
+    _check(out, z["out"], max_err=tol, label=name)
+
+
+@pytest.mark.parametrize("name", ["gqa4_d64_f16", "gqa8_d128_bf16", "mha_d128_f16"])
+def test_golden_partials(name):
+    z, dtype = load_golden(name)
+    q, kv, indptr, ids, last = golden_to_torch(z, dtype, DEV)
+    for key in [k for k in z if k.startswith("partial_m_s")]:
+        S = int(key[len("partial_m_s"):])
+        _announce(f"golden partials {name} S={S}")
+        po, pm, pl = decode_partials(q, kv, indptr, ids, last, S)
+        torch.cuda.synchronize()
+        m_want, l_want, o_want = z[f"partial_m_s{S}"], z[f"partial_l_s{S}"], z[f"partial_o_s{S}"]
+        np.testing.assert_allclose(pm.cpu().numpy(), m_want, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(pl.cpu().numpy(), l_want, rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(po.cpu().numpy(), o_want, rtol=1e-4, atol=1e-4)
+        # pass 2 alone on the golden partials
+        merged = merge_partials(torch.tensor(o_want, dtype=torch.float32, device=DEV),
+                                torch.tensor(m_want, dtype=torch.float32, device=DEV),
+                                torch.tensor(l_want, dtype=torch.float32, device=DEV),
+                                dtype=q.dtype)
+        torch.cuda.synchronize()
+        _check(merged, z["out"], max_err=1e-2, label=f"merge {name} S={S}")
+
+
+def test_primer_known_answer_on_gpu():
+    # writeup/cuda_primer.md:31-43 embedded in head_dim 64: the four tokens sit on one
+    # page (kv_last_page_len 4) and q = [4,4,0,...] so that q.k / sqrt(64) equals the
+    # primer's q.k / sqrt(4). Every score is 0.5 and all V = 0.5, so out = 0.5 exactly;
+    # the single split has m = 0.5, l = 4 and O = 2 in every dim.
+    K = [[1, 0, 1, 0], [0, 1, 0, 1], [1, 0, 0, 1], [0, 1, 1, 0]]
+    kv = torch.zeros(1, 2, 16, 1, 64, dtype=torch.float16)
+    for t, k in enumerate(K):
+        kv[0, 0, t, 0, :4] = torch.tensor(k, dtype=torch.float16)
+    kv[:, 1] = 0.5
+    q = torch.zeros(1, 1, 64, dtype=torch.float16)
+    q[0, 0, :2] = 4.0
+    args = [t.to(DEV) for t in (q, kv, torch.tensor([0, 1], dtype=torch.int32),
+                                torch.tensor([0], dtype=torch.int32),
+                                torch.tensor([4], dtype=torch.int32))]
+    for path in (1, 2):
+        out = decode_attention(*args, split_kv=1, qk_path=path)
+        po, pm, pl = decode_partials(*args, 1, qk_path=path)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), torch.full((1, 1, 64), 0.5, dtype=torch.float16))
+        assert abs(float(pm[0, 0, 0]) - 0.5) < 1e-6 and abs(float(pl[0, 0, 0]) - 4.0) < 1e-5
+        assert torch.allclose(po[0, 0, 0], torch.full((64,), 2.0, device=DEV), atol=1e-5)
+
+
+# ---------------------------------------------------------------- configs
+
+def test_config1_small_decode():
+    # B=2, ctx=512, 32/8/128, fp16, contiguous pages, split 4
+    _announce("config1")
+    q, kv, indptr, ids, last, _ = layout.synthesize(2, 512, 32, 8, 128, device=DEV, seed=0)
+    out = decode_attention(q, kv, indptr, ids, last, split_kv=4)
+    torch.cuda.synchronize()
+    _check(out, _oracle(q, kv, indptr, ids, last), label="config1")
+
+
+@pytest.mark.parametrize("ctx", [128, 512, 2048])
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gate2_sweep(ctx, batch):
+    # notebook Gate 2: Hq=8, Hkv=2, D=64, fp16, split in {1,2,4,8}
+    q, kv, indptr, ids, last, _ = layout.synthesize(batch, ctx, 8, 2, 64, device=DEV)
+    want = _oracle(q, kv, indptr, ids, last)
+    for s in (1, 2, 4, 8):
+        _announce(f"gate2 ctx={ctx} batch={batch} split={s}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"ctx={ctx} B={batch} S={s}")
+
+
+@pytest.mark.parametrize("label,ctx,batch,hq,hkv,split", [
+    ("ctx=1", 1, 1, 8, 2, 4),
+    ("ctx not divisible by page_size (17)", 17, 1, 8, 2, 4),
+    ("ctx not divisible by split (30)", 30, 1, 8, 2, 4),
+    ("batch=1", 128, 1, 8, 2, 4),
+    ("MHA (group 1)", 128, 1, 4, 4, 4),
+    ("MQA (group 8)", 128, 1, 8, 1, 4),
+])
+def test_gate3_edges_and_determinism(label, ctx, batch, hq, hkv, split):
+    _announce(f"gate3 {label}")
+    q, kv, indptr, ids, last, _ = layout.synthesize(batch, ctx, hq, hkv, 64, device=DEV)
+    out = decode_attention(q, kv, indptr, ids, last, split_kv=split)
+    out2 = decode_attention(q, kv, indptr, ids, last, split_kv=split)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), f"{label}: not deterministic"
+    _check(out, _oracle(q, kv, indptr, ids, last), label=label)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (32, 8), (16, 2), (32, 2)])
+def test_dtypes_head_dims_and_groups(dtype, d, hq, hkv):
+    _announce(f"shape dtype={dtype} d={d} hq={hq} hkv={hkv}")
+    lens = [1, 16, 77, 300]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        4, lens, hq, hkv, d, dtype=dtype, device=DEV, page_table="permuted", pool_pages=40,
+        seed=d + hq)
+    want = _oracle(q, kv, indptr, ids, last)
+    for s in (1, 3, 0):
+        for path in (1, 2):
+            out = decode_attention(q, kv, indptr, ids, last, split_kv=s, qk_path=path)
+            torch.cuda.synchronize()
+            _check(out, want, label=f"{dtype} d={d} {hq}/{hkv} S={s} path={path}")
+
+
+@pytest.mark.parametrize("waves", [1, 2, 4])
+def test_waves_per_group(waves):
+    _announce(f"waves={waves}")
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        3, [5, 200, 1000], 32, 8, 128, device=DEV, page_table="permuted", seed=9)
+    want = _oracle(q, kv, indptr, ids, last)
+    for s in (1, 4):
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s, waves_per_group=waves)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"waves={waves} S={s}")
+
+
+def test_nan_poison_outside_valid_tokens_does_not_leak():
+    # Rows past kv_last_page_len on the last page and pages no sequence uses are NaN/Inf;
+    # the output must be finite and equal to the clean run (select, never 0 * NaN).
+    _announce("nan poison")
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        3, [17, 33, 250], 32, 8, 128, device=DEV, page_table="permuted", pool_pages=40, seed=4)
+    clean = {s: decode_attention(q, kv, indptr, ids, last, split_kv=s) for s in (1, 2, 5)}
+    poisoned = kv.clone()
+    used = set(ids.tolist())
+    for p in range(kv.shape[0]):
+        if p not in used:
+            poisoned[p] = float("nan")
+    ip, lp, idl = indptr.tolist(), last.tolist(), ids.tolist()
+    for b in range(3):
+        lastpage = idl[ip[b + 1] - 1]
+        poisoned[lastpage, :, lp[b]:] = float("inf") if b % 2 else float("nan")
+    for s, ref_out in clean.items():
+        out = decode_attention(q, poisoned, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        assert torch.equal(out, ref_out), f"split {s}"
+
+
+@pytest.mark.parametrize("split", [1, 2, 7, 16, 64, 128])
+def test_split_invariance_long_sequence(split):
+    _announce(f"split invariance {split}")
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        2, [4096, 3001], 32, 8, 128, device=DEV, page_table="permuted", seed=21)
+    want = _oracle(q, kv, indptr, ids, last)
+    out = decode_attention(q, kv, indptr, ids, last, split_kv=split)
+    torch.cuda.synchronize()
+    _check(out, want, label=f"S={split}")
+
+
+def test_empty_sequences_and_more_splits_than_pages():
+    _announce("empty sequences")
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        4, [0, 3, 0, 40], 8, 2, 64, device=DEV, page_table="permuted", pool_pages=8, seed=2)
+    want = _oracle(q, kv, indptr, ids, last)
+    for s in (1, 4, 32):
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"S={s}")
+        assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
+
+
+def test_partials_match_oracle_two_pass():
+    _announce("partials vs oracle")
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        2, [500, 61], 8, 2, 128, device=DEV, page_table="permuted", seed=3)
+    for S in (1, 3, 8, 40):
+        po, pm, pl = decode_partials(q, kv, indptr, ids, last, S)
+        torch.cuda.synchronize()
+        O, m, l = skv.split_partials(to_np(q), to_np(kv), to_np(indptr), to_np(ids),
+                                     to_np(last), S)
+        np.testing.assert_allclose(pm.cpu().numpy(), m, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(pl.cpu().numpy(), l, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(po.cpu().numpy(), O, rtol=1e-4, atol=2e-4)
+
+
+def test_strided_q_out_and_side_stream():
+    _announce("strided q/out, side stream")
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        2, [100, 260], 32, 8, 128, device=DEV, page_table="permuted", seed=8)
+    big = torch.randn(2, 64, 128, dtype=torch.float16, device=DEV)
+    big[:, ::2] = q
+    qv = big[:, ::2]                       # q_h stride 256, non-contiguous
+    out_big = torch.zeros(2, 32, 256, dtype=torch.float16, device=DEV)
+    outv = out_big[:, :, :128]
+    want = _oracle(q, kv, indptr, ids, last)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        decode_attention(qv, kv, indptr, ids, last, split_kv=4, out=outv)
+    s.synchronize()
+    _check(outv, want, label="strided")
+    assert torch.count_nonzero(out_big[:, :, 128:]) == 0
+
+
+def test_reference_extension_surface():
+    ext = attention.get_hip_ext()
+    q, kv, indptr, ids, last, _ = layout.synthesize(2, 64, 8, 2, 64, device=DEV)
+    want = _oracle(q, kv, indptr, ids, last)
+    _check(ext.decode_attention_naive(q, kv, indptr, ids, last), want)
+    _check(ext.decode_attention_split_kv(q, kv, indptr, ids, last), want)
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- benchmark configs
+
+@pytest.mark.parametrize("batch", [1, 4, 16, 32, 64])
+def test_config2_batch_sweep(batch):
+    # ctx=4096, 32/8/128 fp16, pool of batch*256 pages in seeded random order
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, 4096, 32, 8, 128, device=DEV, page_table="permuted", seed=batch)
+    subset = list(range(batch)) if batch <= 16 else [0, batch // 2, batch - 1]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=subset)
+    for s in (1, 2, 4, 8, 16):
+        _announce(f"config2 B={batch} S={s}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        _check(out, want, rows=subset, label=f"B={batch} S={s}")
+
+
+@pytest.mark.parametrize("batch,ctx", [(1, 32768), (4, 32768), (1, 131072), (4, 131072)])
+def test_config3_long_context_bf16(batch, ctx):
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, ctx, 32, 8, 128, dtype=torch.bfloat16, device=DEV, page_table="permuted",
+        seed=ctx + batch)
+    subset = [0] if batch == 1 else [0, batch - 1]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=subset)
+    for s in (16, 32, 64, 128):
+        _announce(f"config3 B={batch} ctx={ctx} S={s}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        _check(out, want, rows=subset, label=f"B={batch} ctx={ctx} S={s}")
+
+
+def test_config4_ragged_freelist():
+    # B=128, ctx ~ U[128, 8192], q scaled by 1/sqrt(d), pages drawn without replacement
+    # from a shuffled free list of 65536 pages (a 4 GiB pool: byte offsets above 2^32)
+    lens = layout.ragged_lengths(128, 128, 8192, seed=4)
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        128, lens, 32, 8, 128, device=DEV, page_table="freelist", pool_pages=65536,
+        q_scale=1 / math.sqrt(128), seed=4)
+    assert int(ids.max()) > 60000
+    subset = list(range(0, 128, 8)) + [int(np.argmax(lens)), int(np.argmin(lens))]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=subset)
+    for s in (1, 4, 0):
+        _announce(f"config4 S={s}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        _check(out, want, rows=subset, label=f"ragged S={s}")
+
+
+def test_metric_config_sample():
+    # B=32, ctx=8192, 32/8/128 fp16, random page permutation; the oracle on 4 sequences
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        32, 8192, 32, 8, 128, device=DEV, page_table="permuted", seed=1)
+    subset = [0, 11, 22, 31]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=subset)
+    for s in (1, 3, 8, 0):
+        _announce(f"metric S={s}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+        torch.cuda.synchronize()
+        _check(out, want, rows=subset, label=f"metric S={s}")

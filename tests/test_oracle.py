@@ -1,0 +1,251 @@
+"""CPU tests that pin the oracle (oracle/) before it is trusted to check the HIP kernels.
+
+Each check is independent of the oracle's own formulas: the reference's hand-worked
+example, closed forms, torch's scaled_dot_product_attention in float64, and brute-force
+float64 fixtures from tests/golden/make_golden.py. The mutation tests plant a plausible
+mistake in a copy of the oracle and show that a check catches it.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import load_golden
+from oracle import reference as ref
+from oracle import split_kv as skv
+
+GOLDEN_CASES = ["tiny_f16", "gqa4_d64_f16", "gqa8_d128_bf16", "mha_d128_f16"]
+
+
+def _paged(lens, Hq, Hkv, D, P, seed, pool=0, dtype=np.float16, permute=True):
+    """Random paged inputs (numpy): q, kv, indptr, indices, last."""
+    rng = np.random.default_rng(seed)
+    pages = [math.ceil(n / P) for n in lens]
+    last = np.array([n - (p - 1) * P if p else P for n, p in zip(lens, pages)], np.int32)
+    need = sum(pages)
+    pool = max(pool, need, 1)
+    ids = (rng.permutation(pool)[:need] if permute else np.arange(need)).astype(np.int32)
+    indptr = np.zeros(len(lens) + 1, np.int32)
+    indptr[1:] = np.cumsum(pages)
+    q = rng.standard_normal((len(lens), Hq, D)).astype(dtype)
+    kv = rng.standard_normal((pool, 2, P, Hkv, D)).astype(dtype)
+    return q, kv, indptr, ids, last
+
+
+def _sdpa(q, K, V):
+    """torch SDPA in float64 with enable_gqa (kv head = q head // G). q (B,Hq,D), K,V (B,S,Hkv,D)."""
+    qt = torch.from_numpy(np.asarray(q, np.float64))[:, :, None, :]
+    kt = torch.from_numpy(np.asarray(K, np.float64)).permute(0, 2, 1, 3)
+    vt = torch.from_numpy(np.asarray(V, np.float64)).permute(0, 2, 1, 3)
+    o = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, enable_gqa=True)
+    return o[:, :, 0, :].numpy()
+
+
+# ---------------------------------------------------------------- known answers
+
+def _primer_inputs():
+    """writeup/cuda_primer.md:31-43: D=4, P=2, one head, tokens
+    K = [1,0,1,0], [0,1,0,1], [1,0,0,1], [0,1,1,0], all V = 0.5, q = [1,1,0,0]."""
+    kv = np.zeros((2, 2, 2, 1, 4), np.float16)
+    K = [[1, 0, 1, 0], [0, 1, 0, 1], [1, 0, 0, 1], [0, 1, 1, 0]]
+    for t, k in enumerate(K):
+        kv[t // 2, 0, t % 2, 0] = k
+        kv[t // 2, 1, t % 2, 0] = 0.5
+    q = np.array([[[1, 1, 0, 0]]], np.float16)
+    return q, kv, np.array([0, 2], np.int32), np.array([0, 1], np.int32), np.array([2], np.int32)
+
+
+def test_primer_known_answer():
+    q, kv, indptr, ids, last = _primer_inputs()
+    out = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    assert np.array_equal(out, np.full((1, 1, 4), 0.5, np.float32))
+
+
+def test_primer_split_partials():
+    # writeup/cuda_primer.md:505-540: two splits, each m=0.5, l=2.0, O=[1,1,1,1]
+    q, kv, indptr, ids, last = _primer_inputs()
+    O, m, l = skv.split_partials(q, kv, indptr, ids, last, 2)
+    np.testing.assert_allclose(m[0, 0], [0.5, 0.5], rtol=0, atol=1e-15)
+    np.testing.assert_allclose(l[0, 0], [2.0, 2.0], rtol=0, atol=1e-15)
+    np.testing.assert_allclose(O[0, 0], np.ones((2, 4)), rtol=0, atol=1e-15)
+    np.testing.assert_allclose(skv.merge_partials(O, m, l), np.full((1, 1, 4), 0.5), atol=1e-15)
+
+
+# ---------------------------------------------------------------- closed forms
+
+def test_single_token_returns_v0_exactly():
+    q, kv, indptr, ids, last = _paged([1, 1, 1], 8, 2, 64, 16, seed=3)
+    out = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    for b in range(3):
+        v0 = kv[ids[indptr[b]], 1, 0].astype(np.float32)        # (Hkv, D)
+        np.testing.assert_array_equal(out[b], np.repeat(v0, 4, axis=0))
+
+
+def test_constant_v_gives_constant():
+    q, kv, indptr, ids, last = _paged([37, 5], 4, 2, 16, 4, seed=4)
+    kv[:, 1] = np.float16(-1.25)
+    out = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    np.testing.assert_allclose(out, -1.25, rtol=0, atol=1e-6)
+
+
+def test_equal_keys_give_mean_of_v():
+    q, kv, indptr, ids, last = _paged([23], 4, 1, 8, 4, seed=5)
+    kv[:, 0] = kv[0, 0, 0]
+    out = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    K, V = ref.gather_paged_to_dense(kv, indptr, ids, last)
+    np.testing.assert_allclose(out[0], np.repeat(V[0].mean(axis=0), 4, axis=0), atol=1e-6)
+
+
+def test_dominant_key_selects_its_value():
+    q, kv, indptr, ids, last = _paged([40], 2, 1, 8, 4, seed=6)
+    q[:] = 0
+    q[0, :, 0] = 1
+    K, V = ref.gather_paged_to_dense(kv, indptr, ids, last)
+    t = 17
+    kv[ids[t // 4], 0, t % 4, 0, 0] = np.float16(400.0)     # score 400/sqrt(8) >> others
+    out = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    np.testing.assert_allclose(out[0, 0], V[0, t, 0], atol=1e-6)
+
+
+# ---------------------------------------------------------------- library cross-check
+
+@pytest.mark.parametrize("lens,Hq,Hkv,D,P", [
+    ([64, 64], 32, 8, 128, 16), ([37, 37, 37], 8, 2, 64, 16), ([5], 4, 4, 32, 4),
+    ([130, 130], 8, 1, 64, 16), ([16], 16, 4, 256, 16),
+])
+def test_against_sdpa_float64(lens, Hq, Hkv, D, P):
+    q, kv, indptr, ids, last = _paged(lens, Hq, Hkv, D, P, seed=sum(lens) + Hq)
+    out = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    K, V = ref.gather_paged_to_dense(kv, indptr, ids, last)
+    np.testing.assert_allclose(out, _sdpa(q.astype(np.float64), K, V), rtol=0, atol=2e-6)
+
+
+def test_gather_identity_table_is_reshape():
+    # with the identity block table, the gather is a reshape truncated to seq_len
+    B, ctx, Hkv, D, P = 3, 45, 2, 8, 16
+    q, kv, indptr, ids, last = _paged([ctx] * B, 4, Hkv, D, P, seed=7, permute=False)
+    K, V = ref.gather_paged_to_dense(kv, indptr, ids, last)
+    Kp = kv[:, 0].reshape(B, -1, Hkv, D)[:, :ctx].astype(np.float32)
+    Vp = kv[:, 1].reshape(B, -1, Hkv, D)[:, :ctx].astype(np.float32)
+    np.testing.assert_array_equal(K, Kp)
+    np.testing.assert_array_equal(V, Vp)
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_oracle_matches_golden(name):
+    z, _ = load_golden(name)
+    out = ref.reference_attention_paged(z["q_f32"], z["kv_f32"], z["kv_indptr"],
+                                        z["kv_indices"], z["kv_last_page_len"])
+    np.testing.assert_allclose(out, z["out"], rtol=0, atol=5e-6)
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_split_partials_match_golden(name):
+    z, _ = load_golden(name)
+    splits = sorted(int(k[len("partial_m_s"):]) for k in z if k.startswith("partial_m_s"))
+    assert splits
+    for S in splits:
+        O, m, l = skv.split_partials(z["q_f32"], z["kv_f32"], z["kv_indptr"], z["kv_indices"],
+                                     z["kv_last_page_len"], S)
+        np.testing.assert_allclose(m, z[f"partial_m_s{S}"], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(l, z[f"partial_l_s{S}"], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(O, z[f"partial_o_s{S}"], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(skv.merge_partials(O, m, l), z["out"], atol=1e-12)
+
+
+# ---------------------------------------------------------------- split semantics
+
+def test_partition_matches_reference_formula():
+    # attention_ext.cu:249-252: pps = ceil(N/S); [s*pps, min(s*pps+pps, N))
+    assert skv.partition(10, 4) == [(0, 3), (3, 6), (6, 9), (9, 10)]
+    assert skv.partition(2, 4) == [(0, 1), (1, 2), (2, 2), (2, 2)]   # empty splits
+    assert skv.partition(9, 3) == [(0, 3), (3, 6), (6, 9)]
+    assert skv.partition(0, 3) == [(0, 0), (0, 0), (0, 0)]
+
+
+@pytest.mark.parametrize("S", [1, 2, 3, 5, 7, 64])
+def test_split_count_does_not_change_result(S):
+    lens = [1, 17, 30, 64, 200, 0]
+    q, kv, indptr, ids, last = _paged(lens, 8, 2, 32, 16, seed=11, pool=40)
+    want = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    got = skv.split_kv_attention(q, kv, indptr, ids, last, S)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_empty_split_sentinel_and_empty_sequence():
+    q, kv, indptr, ids, last = _paged([20, 0], 2, 1, 8, 16, seed=12)
+    O, m, l = skv.split_partials(q, kv, indptr, ids, last, 4)
+    # sequence 0 has 2 pages: splits 2, 3 are empty; sequence 1 has none
+    assert (m[0, :, 2:] == skv.EMPTY_M).all() and (l[0, :, 2:] == 0).all()
+    assert (m[1] == skv.EMPTY_M).all() and (O[1] == 0).all()
+    out = skv.merge_partials(O, m, l)
+    assert np.array_equal(out[1], np.zeros_like(out[1]))
+    np.testing.assert_array_equal(ref.reference_attention_paged(q, kv, indptr, ids, last)[1], 0)
+
+
+# ---------------------------------------------------------------- ragged batches
+
+def test_literal_padding_equals_masked_for_uniform_lengths():
+    q, kv, indptr, ids, last = _paged([48, 48, 48], 8, 2, 64, 16, seed=13)
+    a = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    b = ref.reference_attention_paged(q, kv, indptr, ids, last, literal=True)
+    np.testing.assert_allclose(a, b, rtol=0, atol=1e-6)
+
+
+def test_literal_padding_is_wrong_for_ragged_batches():
+    # The reference pads short sequences with zero keys and softmaxes over them
+    # (src/reference.py:40-43,91-94). With small scores the padding takes most of the
+    # weight: the short sequence's output shrinks far beyond the 1e-2 tolerance.
+    q, kv, indptr, ids, last = _paged([16, 1024], 8, 2, 64, 16, seed=14)
+    q = (q.astype(np.float32) / 8).astype(np.float16)
+    masked = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    literal = ref.reference_attention_paged(q, kv, indptr, ids, last, literal=True)
+    assert np.abs(masked[0] - literal[0]).max() > 1e-1
+    np.testing.assert_allclose(masked[1], literal[1], atol=1e-6)   # the longest is unaffected
+
+
+# ---------------------------------------------------------------- planted mistakes
+
+def _oracle_with_modulo_gqa(q, kv, indptr, ids, last):
+    """Copy of the oracle with a plausible bug: kv head = q head % Hkv (not // G)."""
+    B, Hq, D = q.shape
+    Hkv = kv.shape[3]
+    perm = [h % Hkv for h in range(Hq)]
+    out = np.zeros((B, Hq, D), np.float32)
+    for b in range(B):
+        k, v = ref._sequence_kv(kv, indptr, ids, last, b)
+        for h in range(Hq):
+            qs = (q[b, h].astype(np.float32) * np.float32(D ** -0.5))[None, None]
+            out[b, h] = ref._softmax_attend(qs, k[:, perm[h]:perm[h] + 1],
+                                            v[:, perm[h]:perm[h] + 1])[0, 0]
+    return out
+
+
+def test_planted_gqa_mistake_is_caught_by_sdpa():
+    q, kv, indptr, ids, last = _paged([40, 40], 8, 2, 32, 16, seed=15)
+    K, V = ref.gather_paged_to_dense(kv, indptr, ids, last)
+    want = _sdpa(q.astype(np.float64), K, V)
+    good = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    bad = _oracle_with_modulo_gqa(q, kv, indptr, ids, last)
+    assert np.abs(good - want).max() < 2e-6
+    assert np.abs(bad - want).max() > 1e-2
+
+
+def test_planted_scale_mistake_is_caught_by_primer():
+    # scaling by 1/D instead of 1/sqrt(D) breaks the primer's partial m = 0.5
+    q, kv, indptr, ids, last = _primer_inputs()
+    _, m_good, _ = skv.split_partials(q, kv, indptr, ids, last, 2)
+    _, m_bad, _ = skv.split_partials(q, kv, indptr, ids, last, 2, scale=1 / 4)
+    assert np.allclose(m_good, 0.5) and not np.allclose(m_bad, 0.5)
+
+
+def test_planted_last_page_mistake_is_caught_by_golden():
+    # using page_size tokens on the last page (ignoring kv_last_page_len) changes results
+    z, _ = load_golden("gqa4_d64_f16")
+    full = np.full_like(z["kv_last_page_len"], 16)
+    bad = ref.reference_attention_paged(z["q_f32"], z["kv_f32"], z["kv_indptr"],
+                                        z["kv_indices"], full)
+    assert np.abs(bad - z["out"]).max() > 1e-2
