@@ -42,9 +42,11 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--split", type=int, default=0, help="split_kv (0 = occupancy choice)")
+    ap.add_argument("--split", type=int, default=0, help="split_kv (0 = balanced mode)")
     ap.add_argument("--qk-path", type=int, default=0, help="0 default, 1 MFMA, 2 VALU")
     ap.add_argument("--waves", type=int, default=0, help="wavefronts per workgroup (0 = 4)")
+    ap.add_argument("--waves-per-cu", type=int, default=0,
+                    help="balanced mode: persistent wavefronts per CU (0 = default)")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
@@ -113,15 +115,15 @@ def main():
     B, ctx, hq, hkv, d = args.batch, args.ctx, 32, 8, 128
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table="permuted", seed=1)
-    split = attention.resolve_split(q, kv, ids, args.split)
+    split = attention.resolve_split(args.split)
     nbytes = layout.attention_bytes(B, ctx, hq, hkv, d)
     out = torch.empty_like(q)
-    ws_bytes = dk_lib.workspace_bytes(B, hq, d, split)
-    o_off, m_off, l_off, p_total = dk_lib.partials_layout(B, hq, d, split)
+    ws_bytes = dk_lib.workspace_bytes(B, hq, hkv, d, split)
+    p_total = dk_lib.partials_layout(B, hq, d, split)[3] if split else ws_bytes
     ws = torch.empty(max(ws_bytes, p_total), dtype=torch.uint8, device=dev)
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
     strides = attention._strides(q, kv, out)
-    opts = dk_lib.options(args.qk_path, args.waves)
+    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu)
     stream = torch.cuda.current_stream(dev)
     code = attention._DTYPE_CODE[dtype]
     common = (q.data_ptr(), kv.data_ptr(), indptr.data_ptr(), ids.data_ptr(), last.data_ptr())
@@ -175,15 +177,17 @@ def main():
         "config": {"workload": f"paged decode attention B={B} ctx={ctx} Hq={hq} Hkv={hkv} "
                                f"D={d} {args.dtype} page_size=16 permuted pages",
                    "batch": B, "context_length": ctx, "num_q_heads": hq, "num_kv_heads": hkv,
-                   "head_dim": d, "page_size": 16, "split_kv": split,
-                   "qk_path": "valu" if args.qk_path == 2 else "mfma"},
+                   "head_dim": d, "page_size": 16,
+                   "split_kv": split if split else "balanced",
+                   "qk_path": "mfma" if args.qk_path == 1 else "valu"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
         "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
         "bytes_per_call": nbytes, "wall_s_timed_loop": round(wall, 3),
         "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": read_traffic(), "kernel": "dk_pass1 (split-KV pass 1)"},
+                     "traffic": read_traffic(),
+                     "kernel": "dk_pass1_balanced" if split == 0 else "dk_pass1_split"},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -12,9 +12,10 @@ src/cuda_/build.py:256). Every call goes to libdk_decode.so (HIP, gfx950); there
 PyTorch or CPU fallback, and a missing library raises ImportError.
 
 Differences from the reference, all extensions: bf16 as well as fp16; any split_kv >= 1
-(the reference allows 1..32), and split_kv=0 or None picks the split from occupancy;
-work runs on torch's current stream of q's device (the reference used the legacy
-default stream); empty sequences (no pages) produce zeros.
+(the reference allows 1..32), and split_kv=0 or None selects the balanced mode, in which
+a persistent grid gives every wavefront an equal share of all (sequence, kv head, page)
+work whatever the sequence lengths; work runs on torch's current stream of q's device
+(the reference used the legacy default stream); empty sequences (no pages) produce zeros.
 """
 from __future__ import annotations
 
@@ -97,19 +98,23 @@ def _strides(q, kv_data, out) -> dk_lib.DkStrides:
     return s
 
 
-def resolve_split(q: torch.Tensor, kv_data: torch.Tensor, kv_indices: torch.Tensor,
-                  split_kv: Optional[int]) -> int:
-    """split_kv as given, or the occupancy-based choice for 0 / None."""
-    if split_kv is None or split_kv == 0:
-        batch = q.shape[0]
-        avg = kv_indices.shape[0] // batch if batch else 0
-        return dk_lib.choose_split(batch, q.shape[1], kv_data.shape[3], q.shape[2],
-                                   _DTYPE_CODE[q.dtype], avg, q.device.index or 0)
+def resolve_split(split_kv: Optional[int]) -> int:
+    """split_kv as the C ABI takes it: 0 for the balanced mode (None or 0), else >= 1."""
+    if split_kv is None:
+        return 0
     if isinstance(split_kv, bool) or not isinstance(split_kv, int):
         raise TypeError(f"split_kv must be an int, got {type(split_kv).__name__}")
-    if split_kv < 1:
-        _fail(f"split_kv must be >= 1 (or 0/None for automatic), got {split_kv}")
+    if split_kv < 0:
+        _fail(f"split_kv must be >= 1 (or 0/None for the balanced mode), got {split_kv}")
     return split_kv
+
+
+def choose_split(q: torch.Tensor, kv_data: torch.Tensor, kv_indices: torch.Tensor) -> int:
+    """An explicit split count chosen from occupancy (for callers that want one)."""
+    batch = q.shape[0]
+    avg = kv_indices.shape[0] // batch if batch else 0
+    return dk_lib.choose_split(batch, q.shape[1], kv_data.shape[3], q.shape[2],
+                               _DTYPE_CODE[q.dtype], avg, q.device.index or 0)
 
 
 def decode_attention(
@@ -124,6 +129,7 @@ def decode_attention(
     workspace: Optional[torch.Tensor] = None,
     qk_path: int = 0,
     waves_per_group: int = 0,
+    waves_per_cu: int = 0,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
@@ -134,18 +140,20 @@ def decode_attention(
         kv_indices       : (kv_indptr[-1],) int32 physical page ids
         kv_last_page_len : (batch,) int32 valid tokens in each sequence's last page
         split_kv         : KV partitions per (sequence, head). 1 -> one pass writing the
-                           output directly; > 1 -> split partials + log-sum-exp merge;
-                           0 / None -> chosen from occupancy.
+                           output directly; > 1 -> the reference's ceil(N/S)-page split
+                           partials + log-sum-exp merge; 0 / None -> balanced mode
+                           (equal work per wavefront) + merge.
         out, workspace   : optional preallocated output (batch, num_q_heads, head_dim) and
                            uint8 scratch of dk_lib.workspace_bytes(...) bytes
-        qk_path, waves_per_group : tuning knobs (0 = defaults; qk_path 2 = VALU q.k)
+        qk_path, waves_per_group, waves_per_cu : tuning knobs (0 = defaults;
+                           qk_path 1 = MFMA q.k, 2 = VALU q.k)
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
     """
     _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
     lib = dk_lib.load()
-    split = resolve_split(q, kv_data, kv_indices, split_kv)
+    split = resolve_split(split_kv)
     batch, hq, d = q.shape
     if out is None:
         out = torch.empty((batch, hq, d), dtype=q.dtype, device=q.device)
@@ -157,7 +165,7 @@ def decode_attention(
     kv_indptr = _contig1d(kv_indptr)
     kv_indices = _contig1d(kv_indices)
     kv_last_page_len = _contig1d(kv_last_page_len)
-    ws_need = dk_lib.workspace_bytes(batch, hq, d, split)
+    ws_need = dk_lib.workspace_bytes(batch, hq, kv_data.shape[3], d, split)
     if ws_need:
         if workspace is None:
             workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
@@ -167,7 +175,7 @@ def decode_attention(
     ws_ptr = workspace.data_ptr() if ws_need else None
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
-    opts = dk_lib.options(qk_path, waves_per_group)
+    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.dk_decode_attention_ex(
@@ -187,7 +195,8 @@ def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_k
     split is empty), l = sum exp(score - m), O = sum exp(score - m) * V (unnormalised)."""
     _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
     lib = dk_lib.load()
-    split = resolve_split(q, kv_data, kv_indices, split_kv)
+    split = choose_split(q, kv_data, kv_indices) if split_kv in (None, 0) else \
+        resolve_split(split_kv)
     batch, hq, d = q.shape
     off_o, off_m, off_l, total = dk_lib.partials_layout(batch, hq, d, split)
     ws = torch.empty(total, dtype=torch.uint8, device=q.device)

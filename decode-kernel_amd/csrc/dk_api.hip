@@ -1,0 +1,316 @@
+// dk_api.hip — the C ABI of libdk_decode (include/dk_decode.h): argument validation,
+// launch planning and the two passes.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "dk_args.h"
+#include "dk_decode.h"
+#include "dk_launch.h"
+
+namespace dk {
+namespace {
+
+int hip_fail(hipError_t e, const char* what) {
+  return set_error((int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+int current_device(int device) {
+  if (device >= 0) return device;
+  int d = 0;
+  return hipGetDevice(&d) == hipSuccess ? d : -1;
+}
+
+// Compute units of `device` (cached; the count never changes for a device).
+int cu_count(int device) {
+  static int cached[64] = {0};
+  if (device < 0) return -1;
+  if (device < 64 && cached[device] > 0) return cached[device];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return -1;
+  if (device < 64) cached[device] = n;
+  return n;
+}
+
+const void* pass1_fn(int dtype, const Plan& pl, int d) {
+  return dtype == DK_F16 ? pass1_symbol<F16>(d, pl.heads, pl.waves, pl.mfma, pl.balanced)
+                         : pass1_symbol<BF16>(d, pl.heads, pl.waves, pl.mfma, pl.balanced);
+}
+
+// Resident pass-1 workgroups per compute unit (occupancy calculator).
+int resident_groups(int dtype, const Plan& pl, int d) {
+  const void* fn = pass1_fn(dtype, pl, d);
+  int blocks = 0;
+  if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, pl.waves * 64, 0) !=
+                 hipSuccess || blocks <= 0)
+    blocks = 1;
+  return blocks;
+}
+
+int explicit_split(const Problem& p, int device) {
+  Problem q = p;
+  q.split = 1;
+  const Plan pl = make_plan(q);
+  const int cus = cu_count(device);
+  if (cus <= 0) return hip_fail(hipErrorNoDevice, "compute-unit count");
+  const int64_t units = (int64_t)p.batch * pl.pairs_per_seq;
+  const int64_t avg = p.batch > 0 ? p.num_indices / p.batch : 0;
+  return choose_split(units, (int64_t)cus * resident_groups(p.dtype, pl, p.head_dim), avg,
+                      pl.waves);
+}
+
+}  // namespace
+
+// Validation, planning and both passes; shared by the extern "C" entry points.
+int run(Problem p, bool do_merge, void* stream) {
+  clear_error();
+  const int rc = validate(p);
+  if (rc != DK_OK || p.batch == 0) return rc;
+  Plan pl = make_plan(p);
+  const bool direct = p.need_out && p.split == 1;
+  const int64_t esize = 2;
+
+  if (pl.balanced) {
+    const int dev = current_device(-1);
+    const int cus = cu_count(dev);
+    if (cus <= 0) return hip_fail(hipErrorNoDevice, "compute-unit count");
+    const int per_cu = p.opt.waves_per_cu ? p.opt.waves_per_cu : kDefaultWavesPerCU;
+    int64_t waves = std::min<int64_t>(kMaxWaves, (int64_t)cus * per_cu);
+    waves = std::max<int64_t>(pl.waves, waves / pl.waves * pl.waves);
+    pl.grid = waves / pl.waves;
+  }
+
+  Pass1Args a{};
+  a.q = static_cast<const uint8_t*>(p.q);
+  a.kv = static_cast<const uint8_t*>(p.kv);
+  a.indptr = p.indptr;
+  a.indices = p.indices;
+  a.last_len = p.last_len;
+  if (!direct) {
+    const int64_t rows = pl.balanced ? balanced_rows(p.batch, p.hq, p.hkv, p.head_dim)
+                                     : split_rows(p.batch, p.hq, p.split);
+    size_t off_o, off_m, off_l, total;
+    partials_layout_rows(rows, p.head_dim, &off_o, &off_m, &off_l, &total);
+    uint8_t* ws = static_cast<uint8_t*>(p.workspace);
+    a.part_o = reinterpret_cast<float*>(ws + off_o);
+    a.part_m = reinterpret_cast<float*>(ws + off_m);
+    a.part_l = reinterpret_cast<float*>(ws + off_l);
+  }
+  a.out = static_cast<uint8_t*>(p.out);
+  a.q_b = p.st.q_b * esize;
+  a.q_h = p.st.q_h * esize;
+  a.kv_p = p.st.kv_p * esize;
+  a.o_b = p.st.o_b * esize;
+  a.o_h = p.st.o_h * esize;
+  a.kv_r = (int32_t)(p.st.kv_r * esize);
+  a.kv_s = (int32_t)(p.st.kv_s * esize);
+  a.kv_h = (int32_t)(p.st.kv_h * esize);
+  a.batch = p.batch;
+  a.hq = p.hq;
+  a.hkv = p.hkv;
+  a.group = pl.group;
+  a.chunks = pl.chunks;
+  a.split = std::max(p.split, 1);
+  a.num_indices = (int32_t)p.num_indices;
+  a.num_pages = (uint32_t)std::min<int64_t>(p.num_pages, (int64_t)1 << 31);
+  // bytes from a kv head's slice base that its K and V rows reach (validated < 2^31)
+  a.page_extent = (uint32_t)((p.st.kv_r + (int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * esize);
+  a.direct = direct ? 1 : 0;
+  a.kscale = kLog2e / sqrtf((float)p.head_dim);
+
+  Pass1Launch L;
+  L.d = p.head_dim;
+  L.heads = pl.heads;
+  L.waves = pl.waves;
+  L.mfma = pl.mfma;
+  L.balanced = pl.balanced;
+  L.grid = (int)pl.grid;
+  L.stream = static_cast<hipStream_t>(stream);
+  hipError_t e = p.dtype == DK_F16 ? launch_pass1<F16>(a, L) : launch_pass1<BF16>(a, L);
+  if (e != hipSuccess) return hip_fail(e, "pass-1 launch");
+
+  if (do_merge && !direct) {
+    MergeArgs m{};
+    m.po = a.part_o;
+    m.pm = a.part_m;
+    m.pl = a.part_l;
+    m.out = a.out;
+    m.o_b = a.o_b;
+    m.o_h = a.o_h;
+    m.batch = p.batch;
+    m.hq = p.hq;
+    m.split = a.split;
+    m.indptr = p.indptr;
+    m.num_indices = a.num_indices;
+    m.pairs_per_seq = pl.pairs_per_seq;
+    m.heads = pl.heads;
+    m.total_waves = (int)pl.grid * pl.waves;
+    e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)
+                          : launch_merge<BF16>(m, p.head_dim, pl.balanced, L.stream);
+    if (e != hipSuccess) return hip_fail(e, "merge launch");
+  }
+  return DK_OK;
+}
+
+}  // namespace dk
+
+// ---------------------------------------------------------------- C ABI
+using dk::Problem;
+
+static Problem make_problem(const void* q, const void* kv, const int32_t* indptr,
+                            const int32_t* indices, const int32_t* last_len, void* out,
+                            void* ws, size_t ws_bytes, int32_t batch, int32_t hq, int32_t hkv,
+                            int32_t d, int32_t page, int64_t num_pages, int64_t num_indices,
+                            int32_t dtype, const dk_strides* st, int32_t split,
+                            const dk_options* opts, bool need_out) {
+  Problem p;
+  p.q = q;
+  p.kv = kv;
+  p.indptr = indptr;
+  p.indices = indices;
+  p.last_len = last_len;
+  p.out = out;
+  p.workspace = ws;
+  p.workspace_bytes = ws_bytes;
+  p.batch = batch;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.head_dim = d;
+  p.page_size = page;
+  p.num_pages = num_pages;
+  p.num_indices = num_indices;
+  p.dtype = dtype;
+  if (st) p.st = *st;
+  p.split = split;
+  if (opts) p.opt = *opts;
+  p.need_out = need_out;
+  return p;
+}
+
+extern "C" {
+
+int dk_abi_version(void) { return DK_ABI_VERSION; }
+
+const char* dk_last_error(void) { return dk::last_error(); }
+
+size_t dk_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t split_kv) {
+  return dk::workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, split_kv);
+}
+
+int dk_partials_layout(int32_t batch, int32_t num_q_heads, int32_t head_dim, int32_t split_kv,
+                       size_t* off_o, size_t* off_m, size_t* off_l, size_t* total) {
+  dk::clear_error();
+  if (batch < 0 || num_q_heads <= 0 || head_dim <= 0 || split_kv <= 0 || !off_o || !off_m ||
+      !off_l || !total)
+    return dk::set_error(DK_EINVAL, "dk_partials_layout: bad argument");
+  dk::partials_layout_rows(dk::split_rows(batch, num_q_heads, split_kv), head_dim, off_o, off_m,
+                           off_l, total);
+  return DK_OK;
+}
+
+int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                    int32_t dtype, int64_t avg_pages_per_seq, int32_t device) {
+  dk::clear_error();
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
+      (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+      (dtype != DK_F16 && dtype != DK_BF16) || avg_pages_per_seq < 0)
+    return dk::set_error(DK_EINVAL, "dk_choose_split: bad argument");
+  Problem p;
+  p.batch = batch;
+  p.hq = num_q_heads;
+  p.hkv = num_kv_heads;
+  p.head_dim = head_dim;
+  p.dtype = dtype;
+  p.num_indices = avg_pages_per_seq * (int64_t)batch;
+  p.split = 1;
+  const int dev = dk::current_device(device);
+  if (dev < 0) return dk::hip_fail(hipErrorNoDevice, "dk_choose_split");
+  return dk::explicit_split(p, dev);
+}
+
+int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                           const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                           void* out, void* workspace, size_t workspace_bytes, int32_t batch,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t page_size, int64_t num_pages, int64_t num_indices,
+                           int32_t dtype, const dk_strides* strides, int32_t split_kv,
+                           const dk_options* opts, void* hip_stream) {
+  dk::clear_error();
+  if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
+  Problem p = make_problem(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out, workspace,
+                           workspace_bytes, batch, num_q_heads, num_kv_heads, head_dim,
+                           page_size, num_pages, num_indices, dtype, strides, split_kv, opts,
+                           true);
+  return dk::run(p, true, hip_stream);
+}
+
+int dk_decode_attention(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                        const int32_t* kv_indices, const int32_t* kv_last_page_len, void* out,
+                        void* workspace, size_t workspace_bytes, int32_t batch,
+                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t page_size, int64_t num_pages, int64_t num_indices,
+                        int32_t dtype, const dk_strides* strides, int32_t split_kv,
+                        void* hip_stream) {
+  return dk_decode_attention_ex(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out,
+                                workspace, workspace_bytes, batch, num_q_heads, num_kv_heads,
+                                head_dim, page_size, num_pages, num_indices, dtype, strides,
+                                split_kv, nullptr, hip_stream);
+}
+
+int dk_decode_partials(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                       void* workspace, size_t workspace_bytes, int32_t batch,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t page_size, int64_t num_pages, int64_t num_indices, int32_t dtype,
+                       const dk_strides* strides, int32_t split_kv, const dk_options* opts,
+                       void* hip_stream) {
+  dk::clear_error();
+  if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
+  Problem p = make_problem(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, nullptr,
+                           workspace, workspace_bytes, batch, num_q_heads, num_kv_heads,
+                           head_dim, page_size, num_pages, num_indices, dtype, strides,
+                           split_kv, opts, false);
+  return dk::run(p, false, hip_stream);
+}
+
+int dk_merge_partials(const void* workspace, size_t workspace_bytes, void* out, int32_t batch,
+                      int32_t num_q_heads, int32_t head_dim, int32_t dtype, int64_t o_b,
+                      int64_t o_h, int32_t split_kv, void* hip_stream) {
+  dk::clear_error();
+  if (batch < 0 || num_q_heads <= 0 || split_kv < 1 || split_kv > 4096 ||
+      (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
+      (dtype != DK_F16 && dtype != DK_BF16) || o_b < 0 || o_h < 0)
+    return dk::set_error(DK_EINVAL, "dk_merge_partials: bad argument");
+  if (batch == 0) return DK_OK;
+  if (!workspace || !out) return dk::set_error(DK_ENULL, "workspace and out must be non-NULL");
+  if ((int64_t)batch * num_q_heads > INT32_MAX / 4)
+    return dk::set_error(DK_EINVAL, "dk_merge_partials: batch*num_q_heads too large");
+  size_t off_o, off_m, off_l, need;
+  dk::partials_layout_rows(dk::split_rows(batch, num_q_heads, split_kv), head_dim, &off_o,
+                           &off_m, &off_l, &need);
+  if (workspace_bytes < need)
+    return dk::set_error(DK_EWORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                         workspace_bytes);
+  const uint8_t* ws = static_cast<const uint8_t*>(workspace);
+  dk::MergeArgs m{};
+  m.po = reinterpret_cast<const float*>(ws + off_o);
+  m.pm = reinterpret_cast<const float*>(ws + off_m);
+  m.pl = reinterpret_cast<const float*>(ws + off_l);
+  m.out = static_cast<uint8_t*>(out);
+  m.o_b = o_b * 2;
+  m.o_h = o_h * 2;
+  m.batch = batch;
+  m.hq = num_q_heads;
+  m.split = split_kv;
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  hipError_t e = dtype == DK_F16 ? dk::launch_merge<dk::F16>(m, head_dim, false, st)
+                                 : dk::launch_merge<dk::BF16>(m, head_dim, false, st);
+  if (e != hipSuccess) return dk::hip_fail(e, "merge launch");
+  return DK_OK;
+}
+
+}  // extern "C"

@@ -2,15 +2,14 @@
 //
 // The checks mirror the reference's TORCH_CHECKs (src/cuda_/attention_ext.cu:506-509,
 // 549-552: dtype, page_size == 16, split range, head_dim dispatch at :532-535) and the
-// layout invariants that need no device read (src/layout.md:171-178: kv rank / K-V dim,
-// H_q divisible by H_kv, q/kv dtype match is implied by the single `dtype`). Invariants
-// that need device data (kv_indptr[-1] == len(kv_indices), last_page_len in [1, P]) are
-// the Python layer's optional `validate` step; the kernels clamp those values instead.
+// layout invariants that need no device read (src/layout.md:171-178: H_q divisible by
+// H_kv; q/kv dtype agreement is implied by the single `dtype`). Invariants that need
+// device data (kv_indptr[-1] == len(kv_indices), last_page_len in [1, P]) are the Python
+// layer's optional `validate` step; the kernels clamp those values instead.
 #include "dk_args.h"
 
 #include <stdarg.h>
 #include <stdio.h>
-#include <string.h>
 
 #include <algorithm>
 #include <string>
@@ -19,7 +18,11 @@ namespace dk {
 
 namespace {
 thread_local std::string g_error;
+
+bool valid_shape(int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
+  return batch >= 0 && hq > 0 && hkv > 0 && hq % hkv == 0 && (d == 64 || d == 128 || d == 256);
 }
+}  // namespace
 
 int set_error(int code, const char* fmt, ...) {
   char buf[512];
@@ -35,27 +38,6 @@ void clear_error() { g_error.clear(); }
 
 const char* last_error() { return g_error.c_str(); }
 
-size_t partials_bytes(int32_t batch, int32_t hq, int32_t head_dim, int32_t split) {
-  if (batch <= 0 || hq <= 0 || head_dim <= 0 || split <= 0) return 0;
-  const size_t rows = (size_t)batch * (size_t)hq * (size_t)split;
-  size_t off_o, off_m, off_l;
-  partials_layout(batch, hq, head_dim, split, &off_o, &off_m, &off_l);
-  return off_l + rows * sizeof(float);
-}
-
-size_t workspace_bytes(int32_t batch, int32_t hq, int32_t head_dim, int32_t split) {
-  return split > 1 ? partials_bytes(batch, hq, head_dim, split) : 0;
-}
-
-void partials_layout(int32_t batch, int32_t hq, int32_t head_dim, int32_t split,
-                     size_t* off_o, size_t* off_m, size_t* off_l) {
-  const size_t rows = (size_t)batch * (size_t)hq * (size_t)split;
-  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  *off_o = 0;
-  *off_m = up(rows * (size_t)head_dim * sizeof(float));
-  *off_l = *off_m + up(rows * sizeof(float));
-}
-
 int heads_per_group(int group, int head_dim) {
   const int cap = head_dim >= 256 ? 4 : 8;
   for (int h = cap; h > 1; h >>= 1)
@@ -63,16 +45,56 @@ int heads_per_group(int group, int head_dim) {
   return 1;
 }
 
+void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,
+                          size_t* off_l, size_t* total) {
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  *off_o = 0;
+  *off_m = up((size_t)rows * (size_t)head_dim * sizeof(float));
+  *off_l = *off_m + up((size_t)rows * sizeof(float));
+  *total = *off_l + (size_t)rows * sizeof(float);
+}
+
+int64_t split_rows(int32_t batch, int32_t hq, int32_t split) {
+  return (int64_t)batch * hq * split;
+}
+
+int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) {
+  const int group = hq / hkv;
+  const int heads = heads_per_group(group, head_dim);
+  const int64_t pairs = (int64_t)batch * hkv * (group / heads);
+  return (kMaxWaves + pairs) * heads;
+}
+
+size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split) {
+  if (!valid_shape(batch, hq, hkv, head_dim) || split < 0 || batch == 0 || split == 1) return 0;
+  const int64_t rows = split == 0 ? balanced_rows(batch, hq, hkv, head_dim)
+                                  : split_rows(batch, hq, split);
+  size_t o, m, l, total;
+  partials_layout_rows(rows, head_dim, &o, &m, &l, &total);
+  return total;
+}
+
 int choose_split(int64_t units, int64_t slots, int64_t avg_pages_per_seq, int waves) {
   if (units <= 0) return 1;
-  // Enough workgroups to fill every resident slot once (one round, no tail), but no
-  // split so fine that a wavefront gets fewer than ~4 pages.
+  // Enough workgroups to fill every resident slot once (one round), but no split so fine
+  // that a wavefront gets fewer than ~4 pages.
   int64_t s = (slots + units - 1) / units;
-  const int64_t min_pages_per_split = 4 * (int64_t)std::max(waves, 1);
-  const int64_t max_s = std::max<int64_t>(1, avg_pages_per_seq / min_pages_per_split);
-  s = std::min(s, max_s);
-  s = std::max<int64_t>(s, 1);
+  const int64_t max_s = std::max<int64_t>(1, avg_pages_per_seq / (4 * (int64_t)std::max(waves, 1)));
+  s = std::max<int64_t>(1, std::min(s, max_s));
   return (int)std::min<int64_t>(s, 4096);
+}
+
+Plan make_plan(const Problem& p) {
+  Plan pl;
+  pl.group = p.hq / p.hkv;
+  pl.heads = heads_per_group(pl.group, p.head_dim);
+  pl.chunks = pl.group / pl.heads;
+  pl.pairs_per_seq = p.hkv * pl.chunks;
+  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : 4;
+  pl.mfma = p.opt.qk_path == 1;
+  pl.balanced = p.split == 0;
+  pl.grid = pl.balanced ? 0 : (int64_t)p.batch * pl.pairs_per_seq * std::max(p.split, 1);
+  return pl;
 }
 
 int validate(const Problem& p) {
@@ -90,7 +112,7 @@ int validate(const Problem& p) {
                      p.page_size);
   if (p.dtype != DK_F16 && p.dtype != DK_BF16)
     return set_error(DK_EINVAL, "dtype must be DK_F16 (0) or DK_BF16 (1); got %d", p.dtype);
-  if (p.split < 1) return set_error(DK_EINVAL, "split_kv must be >= 1; got %d", p.split);
+  if (p.split < 0) return set_error(DK_EINVAL, "split_kv must be >= 0; got %d", p.split);
   if (p.split > 4096) return set_error(DK_EINVAL, "split_kv must be <= 4096; got %d", p.split);
   if (p.num_indices < 0 || p.num_indices > INT32_MAX)
     return set_error(DK_EINVAL, "num_indices must be in [0, 2^31); got %lld",
@@ -105,6 +127,8 @@ int validate(const Problem& p) {
       o.waves_per_group != 4)
     return set_error(DK_EINVAL, "options.waves_per_group must be 0, 1, 2 or 4; got %d",
                      o.waves_per_group);
+  if (o.waves_per_cu < 0 || o.waves_per_cu > 32)
+    return set_error(DK_EINVAL, "options.waves_per_cu must be in [0, 32]; got %d", o.waves_per_cu);
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything
@@ -115,9 +139,9 @@ int validate(const Problem& p) {
     return set_error(DK_ENULL, "kv_indices must be non-NULL");
   if (p.need_out && !p.out) return set_error(DK_ENULL, "out must be non-NULL");
 
-  // Strides: non-negative, and every 16-byte vector access aligned. Row loads of K are
-  // 16 bytes wide (8 elements), so page/row/head strides and the base must be multiples
-  // of 8 elements; q rows are loaded the same way.
+  // Strides: non-negative, and every 16-byte vector access aligned. Row loads of K/V are
+  // up to 16 bytes wide (8 elements), so page/row/head strides and the base must be
+  // multiples of 8 elements; q rows are loaded the same way.
   const dk_strides& s = p.st;
   const int64_t all[] = {s.q_b, s.q_h, s.kv_p, s.kv_r, s.kv_s, s.kv_h, s.o_b, s.o_h};
   for (int64_t v : all)
@@ -138,12 +162,17 @@ int validate(const Problem& p) {
     return set_error(DK_EUNSUPPORTED, "kv_data page extent exceeds 2 GiB");
 
   const Plan plan = make_plan(p);
-  if (plan.pass1_groups > INT32_MAX)
+  if (plan.grid > INT32_MAX)
     return set_error(DK_EINVAL, "grid too large: batch*kv_heads*split = %lld workgroups",
-                     (long long)plan.pass1_groups);
-  // Two passes (split > 1) and the pass-1-only entry point write fp32 partials.
-  if (p.split > 1 || !p.need_out) {
-    const size_t req = partials_bytes(p.batch, p.hq, p.head_dim, p.split);
+                     (long long)plan.grid);
+  if ((int64_t)p.batch * p.hq > INT32_MAX / 4)
+    return set_error(DK_EINVAL, "batch*num_q_heads too large");
+  // Two passes and the pass-1-only entry point write fp32 partials.
+  if (p.split != 1 || !p.need_out) {
+    const int64_t rows = p.split == 0 ? balanced_rows(p.batch, p.hq, p.hkv, p.head_dim)
+                                      : split_rows(p.batch, p.hq, p.split);
+    size_t o, m, l, req;
+    partials_layout_rows(rows, p.head_dim, &o, &m, &l, &req);
     if (!p.workspace || p.workspace_bytes < req)
       return set_error(DK_EWORKSPACE, "workspace of %zu bytes required, %zu given", req,
                        p.workspace_bytes);
@@ -151,17 +180,6 @@ int validate(const Problem& p) {
       return set_error(DK_EWORKSPACE, "workspace must be 256-byte aligned");
   }
   return DK_OK;
-}
-
-Plan make_plan(const Problem& p) {
-  Plan pl;
-  pl.group = p.hq / p.hkv;
-  pl.heads = heads_per_group(pl.group, p.head_dim);
-  pl.chunks = pl.group / pl.heads;
-  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : 4;
-  pl.mfma = p.opt.qk_path != 2;
-  pl.pass1_groups = (int64_t)p.batch * p.hkv * pl.chunks * std::max(p.split, 1);
-  return pl;
 }
 
 }  // namespace dk

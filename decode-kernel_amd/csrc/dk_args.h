@@ -1,4 +1,4 @@
-// Host-only argument checking, workspace layout and split choice for libdk_decode.
+// Host-only argument checking, workspace layout and launch planning for libdk_decode.
 // No HIP in this header or in dk_args.cpp: it is compiled with g++ and exercised on
 // machines without a GPU.
 #pragma once
@@ -10,7 +10,9 @@
 
 namespace dk {
 
-constexpr int kPageSize = 16;   // tokens per page (reference: PAGE_SIZE=16, attention_ext.cu:509)
+constexpr int kPageSize = 16;        // tokens per page (reference: PAGE_SIZE=16, attention_ext.cu:509)
+constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid (wavefronts)
+constexpr int kDefaultWavesPerCU = 4;
 
 // Everything a launch needs that is known on the host.
 struct Problem {
@@ -25,19 +27,21 @@ struct Problem {
   int32_t batch = 0, hq = 0, hkv = 0, head_dim = 0, page_size = 0, dtype = 0;
   int64_t num_pages = 0, num_indices = 0;
   dk_strides st{};
-  int32_t split = 0;
+  int32_t split = 0;          // 0: balanced persistent mode; >= 1: explicit split
   bool need_out = true;       // false for the pass-1-only entry point
   dk_options opt{};
 };
 
-// Derived launch shape.
+// Launch shape derived from a problem.
 struct Plan {
   int group = 0;       // hq / hkv
-  int heads = 0;       // q heads handled by one workgroup (1, 2, 4 or 8)
+  int heads = 0;       // q heads handled by one wavefront (1, 2, 4 or 8)
   int chunks = 0;      // group / heads
+  int pairs_per_seq = 0;   // hkv * chunks
   int waves = 0;       // wavefronts per workgroup
-  bool mfma = true;    // q.k on MFMA (false: VALU dot2)
-  int64_t pass1_groups = 0;
+  bool mfma = false;   // q.k on MFMA (default: VALU dot2)
+  bool balanced = false;
+  int64_t grid = 0;    // workgroups of pass 1 (balanced: filled in from the device)
 };
 
 // Records a message for dk_last_error() and returns `code`.
@@ -49,22 +53,24 @@ const char* last_error();
 // split) without touching device memory. Returns DK_OK or a negative code.
 int validate(const Problem& p);
 
-// Plan for a validated problem with split >= 1.
 Plan make_plan(const Problem& p);
 
-// Bytes of the fp32 partials for `split` >= 1 splits; workspace_bytes is that for
-// split > 1 and 0 for the single-pass split == 1.
-size_t partials_bytes(int32_t batch, int32_t hq, int32_t head_dim, int32_t split);
-size_t workspace_bytes(int32_t batch, int32_t hq, int32_t head_dim, int32_t split);
-void partials_layout(int32_t batch, int32_t hq, int32_t head_dim, int32_t split,
-                     size_t* off_o, size_t* off_m, size_t* off_l);
-
-// Split count for `units` = batch * hkv * chunks workgroups per split, given
-// `slots` = compute units * resident workgroups per unit.
-int choose_split(int64_t units, int64_t slots, int64_t avg_pages_per_seq, int waves);
-
-// Heads per workgroup for a GQA group size (largest power of two <= 8, or <= 4 for
+// Heads per wavefront for a GQA group size (largest power of two <= 8, or <= 4 for
 // head_dim 256, that divides the group).
 int heads_per_group(int group, int head_dim);
+
+// fp32 partials: `rows` rows of head_dim floats + m + l, each array 256-byte aligned.
+void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,
+                          size_t* off_l, size_t* total);
+// Rows of partials each mode writes: explicit split S -> batch*hq*S; balanced ->
+// (kMaxWaves + batch*pairs_per_seq) * heads.
+int64_t split_rows(int32_t batch, int32_t hq, int32_t split);
+int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim);
+// Workspace of dk_decode_attention: split 1 -> 0, split > 1 -> explicit partials,
+// split 0 -> balanced partials. 0 on invalid shapes.
+size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split);
+
+// Explicit split count for `units` workgroups per split and `slots` resident workgroups.
+int choose_split(int64_t units, int64_t slots, int64_t avg_pages_per_seq, int waves);
 
 }  // namespace dk

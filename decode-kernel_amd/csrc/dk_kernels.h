@@ -1,0 +1,930 @@
+// dk_kernels.h — device code of the split-KV paged decode attention (gfx950, wave64).
+//
+// A wavefront owns one 16-token page of one kv head at a time. Lane (r, c) with
+// r = lane/16, c = lane%16:
+//   * V rows: tokens 4r..4r+3, dims c*D/16 .. +D/16-1 (each 16-lane row of the wave reads
+//     whole rows: four 256-byte rows per 16-byte load instruction at D = 128).
+//   * K rows, VALU q.k path: the same layout as V; each lane forms dot2 partial scores over
+//     its dims for its 4 tokens and the G heads of the GQA group, and a reduce-scatter
+//     over the row's 16 lanes leaves lane (r, c) with the scores of tokens 4r..4r+3 for
+//     q head c mod 4.
+//   * K rows, MFMA q.k path: lane l holds token l%16 with 8 dims per
+//     v_mfma_f32_16x16x32_{f16,bf16}, so S^T = K.Q^T lands in the same score layout.
+//     Its loads read 64 bytes per row per instruction; the VALU path's full-row loads
+//     measured faster on MI355X, so VALU is the default.
+//   Every K/V element is read once and serves all G heads of its kv head.
+//   Online softmax is fp32 in the log2 domain (v_exp_f32); the reference max only moves
+//   when a score exceeds it by more than 2^8, so accumulators are rescaled a handful of
+//   times per split instead of every page. P.V: fp16 pairs tokens with v_dot2_f32_f16
+//   (p rounded to nearest fp16, and l summed from the same rounded p, so the output is an
+//   exact weighted mean under weights perturbed by <= 2^-11); bf16 uses fp32 fma. The p
+//   of the other heads of a quad come through DPP quad_perm. The next page's loads are
+//   in flight while the current page is computed.
+//
+// Pass 1, explicit split (dk_pass1_split): one workgroup per (sequence, kv head, split)
+//   over ceil(N/S)-page ranges as in the reference partition kernel
+//   (src/cuda_/attention_ext.cu:207-349); NW wavefronts take the split's pages round-robin
+//   and merge through LDS. With one split it writes the normalised output.
+// Pass 1, balanced (dk_pass1_balanced): a persistent grid of W wavefronts splits the
+//   linear (sequence, kv head, page) space into W equal ranges; a wavefront writes one
+//   partial per (sequence, kv head) segment it crosses, at slot wave + pair (unique,
+//   < W + pairs). Uniform or ragged, every wavefront streams the same number of pages.
+// Pass 2 (dk_merge_split / dk_merge_balanced): one wavefront per (sequence, q head)
+//   merges its partials with the log-sum-exp identity (reference decode_attn_reduce_kernel,
+//   src/cuda_/attention_ext.cu:363-406; contract src/layout.md:142-167).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dk {
+
+using u32 = uint32_t;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kPage = 16;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kEmptyM = -1e9f;        // partial_m of an empty split (attention_ext.cu:254)
+constexpr float kMinit = -1e30f;        // running reference before the first score
+constexpr float kSlack = 8.0f;          // log2 headroom before the reference max moves
+constexpr float kNegInf = -__builtin_inff();
+constexpr u32 kOnesF16x2 = 0x3C003C00u; // (1.0h, 1.0h)
+
+// ---------------------------------------------------------------- launch arguments
+struct Pass1Args {
+  const uint8_t* q;
+  const uint8_t* kv;
+  const int32_t* indptr;
+  const int32_t* indices;
+  const int32_t* last_len;
+  float* part_o;
+  float* part_m;
+  float* part_l;
+  uint8_t* out;
+  int64_t q_b, q_h, kv_p, o_b, o_h;   // bytes
+  int32_t kv_r, kv_s, kv_h;           // bytes
+  int32_t batch, hq, hkv, group, chunks, split;
+  int32_t num_indices;
+  uint32_t num_pages;                 // clamp bound for page ids (min(num_pages, 2^31))
+  uint32_t page_extent;               // bytes of a page a kv head's loads may touch (< 2^31)
+  int32_t direct;                     // explicit split 1: write the normalised output
+  float kscale;                       // log2(e) / sqrt(head_dim)
+};
+
+struct MergeArgs {
+  const float* po;
+  const float* pm;
+  const float* pl;
+  uint8_t* out;
+  int64_t o_b, o_h;                   // bytes
+  int32_t batch, hq, split;           // explicit split
+  const int32_t* indptr;              // balanced: recompute each pair's slots
+  int32_t num_indices, pairs_per_seq, heads, total_waves;
+};
+
+// ---------------------------------------------------------------- element types
+struct F16 {
+  static constexpr bool kDotPV = true;
+  static __device__ __forceinline__ float lo(u32 w) { return (float)__builtin_bit_cast(f16x2, w)[0]; }
+  static __device__ __forceinline__ float hi(u32 w) { return (float)__builtin_bit_cast(f16x2, w)[1]; }
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float dot2(u32 a, u32 b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b),
+                                  c, false);
+  }
+  static __device__ __forceinline__ void store(uint8_t* p, float x) {
+    *reinterpret_cast<_Float16*>(p) = (_Float16)x;
+  }
+};
+
+struct BF16 {
+  static constexpr bool kDotPV = false;
+  static __device__ __forceinline__ float lo(u32 w) { return __builtin_bit_cast(float, w << 16); }
+  static __device__ __forceinline__ float hi(u32 w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float dot2(u32 a, u32 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  static __device__ __forceinline__ void store(uint8_t* p, float x) {
+    *reinterpret_cast<__bf16*>(p) = (__bf16)x;
+  }
+};
+
+// ---------------------------------------------------------------- cross-lane helpers
+template <int CTRL>
+__device__ __forceinline__ u32 dpp_u(u32 x) {
+  // bound_ctrl: every pattern used here reads an existing lane, so no "old" value is
+  // needed (and no zeroing move is emitted for it).
+  return (u32)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xf, 0xf, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, dpp_u<CTRL>(__builtin_bit_cast(u32, x)));
+}
+// Value of lane 4*(l/4) + Q: DPP quad_perm [Q,Q,Q,Q].
+template <int Q>
+__device__ __forceinline__ float quad_bcast(float x) { return dpp<Q * 0x55>(x); }
+template <int Q>
+__device__ __forceinline__ u32 quad_bcast_u(u32 x) { return dpp_u<Q * 0x55>(x); }
+// Runtime-indexed (but compile-time unrolled) quad broadcast.
+__device__ __forceinline__ float quad_bcast_i(float x, int q) {
+  return q == 0 ? quad_bcast<0>(x) : q == 1 ? quad_bcast<1>(x) : q == 2 ? quad_bcast<2>(x)
+                                                                        : quad_bcast<3>(x);
+}
+__device__ __forceinline__ u32 quad_bcast_iu(u32 x, int q) {
+  return q == 0 ? quad_bcast_u<0>(x) : q == 1 ? quad_bcast_u<1>(x)
+                                              : q == 2 ? quad_bcast_u<2>(x) : quad_bcast_u<3>(x);
+}
+template <int N>
+__device__ __forceinline__ float row_ror(float x) { return dpp<0x120 + N>(x); }
+__device__ __forceinline__ float xor1(float x) { return dpp<0xB1>(x); }   // quad_perm [1,0,3,2]
+__device__ __forceinline__ float xor2(float x) { return dpp<0x4E>(x); }   // quad_perm [2,3,0,1]
+
+// (v[l], v[l ^ 16]) and (v[l], v[l ^ 32]) through the gfx950 permlane swaps; both lanes
+// of a pair get the operands in the same order, so sums are bitwise identical.
+__device__ __forceinline__ float sum_xor16(float x) {
+  const u32 v = __builtin_bit_cast(u32, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return __builtin_bit_cast(float, (u32)r[0]) + __builtin_bit_cast(float, (u32)r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const u32 v = __builtin_bit_cast(u32, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __builtin_bit_cast(float, (u32)r[0]) + __builtin_bit_cast(float, (u32)r[1]);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  const u32 v = __builtin_bit_cast(u32, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return fmaxf(__builtin_bit_cast(float, (u32)r[0]), __builtin_bit_cast(float, (u32)r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const u32 v = __builtin_bit_cast(u32, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__builtin_bit_cast(float, (u32)r[0]), __builtin_bit_cast(float, (u32)r[1]));
+}
+// Max over all lanes whose column c = l%16 agrees modulo GQ (the lanes holding one q head
+// of a head set), result in all of them.
+template <int GQ>
+__device__ __forceinline__ float allmax_head(float x) {
+  if constexpr (GQ == 1) {
+    x = fmaxf(x, xor1(x));
+    x = fmaxf(x, xor2(x));
+  } else if constexpr (GQ == 2) {
+    x = fmaxf(x, xor2(x));
+  }
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<8>(x));
+  return max_xor32(max_xor16(x));
+}
+__device__ __forceinline__ float row_sum(float x) {
+  x += xor1(x);
+  x += xor2(x);
+  x += row_ror<4>(x);
+  x += row_ror<8>(x);
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) { return sum_xor32(sum_xor16(row_sum(x))); }
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, xor1(x));
+  x = fmaxf(x, xor2(x));
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<8>(x));
+  return max_xor32(max_xor16(x));
+}
+__device__ __forceinline__ float readlane_f(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// ---------------------------------------------------------------- memory helpers
+// Page tables are read through the constant address space: the kernels never write
+// them, and this lets every uniform read stay a scalar load even after stores.
+template <class X>
+__device__ __forceinline__ X ld_const(const X* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) X*)p)[i];
+}
+
+// Buffer resource of one page slice: base address, no stride, `extent` bytes in range
+// (out-of-range lanes read 0). gfx9-family descriptor word 3.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* base, u32 extent) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)extent, 0x00020000);
+}
+constexpr int kBufNT = 2;   // buffer-load cache policy: non-temporal (streamed once)
+
+// NWORDS consecutive words at base + voff + soff (NWORDS in {2, 4, 8}), streaming.
+template <int NWORDS>
+__device__ __forceinline__ void ld_buf(u32* dst, __amdgpu_buffer_rsrc_t r, u32 voff, u32 soff) {
+  if constexpr (NWORDS == 2) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, kBufNT));
+    dst[0] = v[0];
+    dst[1] = v[1];
+  } else {
+#pragma unroll
+    for (int k = 0; k < NWORDS / 4; ++k) {
+      const u32x4 v = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(voff + 16 * k), (int)soff, kBufNT));
+      dst[4 * k + 0] = v[0];
+      dst[4 * k + 1] = v[1];
+      dst[4 * k + 2] = v[2];
+      dst[4 * k + 3] = v[3];
+    }
+  }
+}
+template <int NWORDS>
+__device__ __forceinline__ void ld_words_cached(u32* dst, const uint8_t* p) {
+#pragma unroll
+  for (int k = 0; k < NWORDS; ++k) dst[k] = reinterpret_cast<const u32*>(p)[k];
+}
+template <int N>
+__device__ __forceinline__ void st_floats(float* p, const float* v) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k)
+      reinterpret_cast<f32x4*>(p)[k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; ++k) p[k] = v[k];
+  }
+}
+
+// Clamped CSR range of sequence b (so that no access leaves kv_indices).
+__device__ __forceinline__ int seq_begin(const Pass1Args& a, int b) {
+  return min(max(ld_const(a.indptr, b), 0), a.num_indices);
+}
+
+// ---------------------------------------------------------------- per-wavefront decoder
+template <class T, int D, int G, bool MFMA>
+struct Wave {
+  static constexpr int GQ = G < 4 ? G : 4;   // heads per column set
+  static constexpr int NS = G / GQ;          // column sets (G = 8 -> 2)
+  static constexpr int DPL = D / 16;         // V (and VALU-path K) dims per lane
+  static constexpr int VWT = DPL / 2;        // words per token per lane
+  static constexpr int KW = D / 8;           // K words per lane per page (both paths)
+  static constexpr int VW = 4 * VWT;         // V words per lane per page
+  static constexpr int NMF = D / 32;         // MFMAs per head set per page
+
+  int r16, c;
+  u32 koff, voff, tok_s, extent;
+  float kscale;
+  u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, dims 32i+8r16..
+  u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
+  float acc[G][DPL];
+  float mref[NS], mtrue[NS], lsum[NS];
+
+  __device__ __forceinline__ void init(const Pass1Args& a) {
+    const int lane = threadIdx.x & 63;
+    r16 = lane >> 4;
+    c = lane & 15;
+    tok_s = (u32)a.kv_s;
+    koff = MFMA ? (u32)(c * a.kv_s + 16 * r16) : (u32)(4 * r16 * a.kv_s + 2 * DPL * c);
+    voff = (u32)(a.kv_r + 4 * r16 * a.kv_s + 2 * DPL * c);
+    extent = a.page_extent;
+    kscale = a.kscale;
+  }
+
+  // q rows of the G heads starting at qbase (q_h bytes apart).
+  __device__ __forceinline__ void load_q(const uint8_t* qbase, int64_t q_h) {
+    if constexpr (MFMA) {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        const uint8_t* qp = qbase + (int64_t)(ss * GQ + c % GQ) * q_h + 16 * r16;
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) ld_words_cached<4>(&qw[ss][4 * i], qp + 64 * i);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < G; ++h) ld_words_cached<VWT>(qv[h], qbase + (int64_t)h * q_h + 2 * DPL * c);
+    }
+  }
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[h][j] = 0.f;
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss) {
+      mref[ss] = kMinit;
+      mtrue[ss] = kNegInf;
+      lsum[ss] = 0.f;
+    }
+  }
+
+  // pg: base of this kv head's slice of a page (page base + kvh * kv_h). Buffer loads:
+  // the address is the page base (scalar) + a per-lane offset + a per-row scalar offset.
+  __device__ __forceinline__ void load_page(u32 (&kb)[KW], u32 (&vb)[VW], const uint8_t* pg) const {
+    const __amdgpu_buffer_rsrc_t rs = page_rsrc(pg, extent);
+    if constexpr (MFMA) {
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) ld_buf<4>(&kb[4 * i], rs, koff, 64 * i);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ld_buf<VWT>(&kb[r * VWT], rs, koff, r * tok_s);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ld_buf<VWT>(&vb[r * VWT], rs, voff, r * tok_s);
+  }
+
+  // Scores of tokens 4*r16 + r for head ss*GQ + c%GQ from per-lane partials of the G
+  // heads over this lane's dims: reduce-scatter over the low column bits (the head),
+  // all-reduce over the rest.
+  __device__ __forceinline__ float scatter_scores(const float (&part)[GQ], int r) const {
+    (void)r;
+    if constexpr (GQ == 4) {
+      const bool b0 = c & 1, b1 = c & 2;
+      const float k0 = b0 ? part[1] : part[0], s0 = b0 ? part[0] : part[1];
+      const float k1 = b0 ? part[3] : part[2], s1 = b0 ? part[2] : part[3];
+      const float w0 = k0 + xor1(s0), w1 = k1 + xor1(s1);   // heads {b0, 2+b0}
+      float x = (b1 ? w1 : w0) + xor2(b1 ? w0 : w1);        // head 2*b1 + b0
+      x += row_ror<4>(x);
+      x += row_ror<8>(x);
+      return x;
+    } else if constexpr (GQ == 2) {
+      const bool b0 = c & 1;
+      float x = (b0 ? part[1] : part[0]) + xor1(b0 ? part[0] : part[1]);
+      x += xor2(x);
+      x += row_ror<4>(x);
+      x += row_ror<8>(x);
+      return x;
+    } else {
+      return row_sum(part[0]);
+    }
+  }
+
+  // One page: scores, online softmax, P.V. valid < 16 masks tokens >= valid.
+  __device__ __forceinline__ void compute_page(const u32 (&kb)[KW], u32 (&vb)[VW], int valid) {
+    float sc[NS][4];
+    if constexpr (MFMA) {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+          const u32x4 av = {kb[4 * i], kb[4 * i + 1], kb[4 * i + 2], kb[4 * i + 3]};
+          const u32x4 bv = {qw[ss][4 * i], qw[ss][4 * i + 1], qw[ss][4 * i + 2],
+                            qw[ss][4 * i + 3]};
+          d = T::mfma(av, bv, d);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[ss][r] = d[r];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int ss = 0; ss < NS; ++ss) {
+          float part[GQ];
+#pragma unroll
+          for (int g = 0; g < GQ; ++g) {
+            float x = 0.f;
+#pragma unroll
+            for (int q = 0; q < VWT; ++q) x = T::dot2(kb[r * VWT + q], qv[ss * GQ + g][q], x);
+            part[g] = x;
+          }
+          sc[ss][r] = scatter_scores(part, r);
+        }
+      }
+    }
+    // last page of a sequence: tokens >= valid are masked by selection (never by
+    // multiplying), so stale or NaN bytes in the page tail cannot reach the output
+    if (valid < kPage) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool dead = 4 * r16 + r >= valid;
+#pragma unroll
+        for (int ss = 0; ss < NS; ++ss) sc[ss][r] = dead ? kNegInf : sc[ss][r];
+#pragma unroll
+        for (int q = 0; q < VWT; ++q) vb[r * VWT + q] = dead ? 0u : vb[r * VWT + q];
+      }
+    }
+    // online softmax (log2 domain)
+    float x[NS][4], mx[NS];
+    bool need = false;
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[ss][r] = sc[ss][r] * kscale;
+      mx[ss] = fmaxf(fmaxf(x[ss][0], x[ss][1]), fmaxf(x[ss][2], x[ss][3]));
+      mtrue[ss] = fmaxf(mtrue[ss], mx[ss]);
+      need |= mx[ss] > mref[ss] + kSlack;
+    }
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        const float mn = allmax_head<GQ>(fmaxf(mref[ss], mx[ss]));
+        const float al = __builtin_amdgcn_exp2f(mref[ss] - mn);
+        lsum[ss] *= al;
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+          const float ab = GQ > 1 ? quad_bcast_i(al, g) : al;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] *= ab;
+        }
+        mref[ss] = mn;
+      }
+    }
+    float p[NS][4];
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[ss][r] = __builtin_amdgcn_exp2f(x[ss][r] - mref[ss]);
+
+    if constexpr (T::kDotPV) {
+      // fp16: p rounded to fp16 pairs (tokens 0,1 and 2,3); l from the same rounded p
+      u32 pk[NS][2], pb[NS][GQ][2];
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        // round to nearest even (v_cvt_pk_f16_f32)
+        pk[ss][0] = __builtin_bit_cast(u32, __builtin_convertvector(f32x2{p[ss][0], p[ss][1]}, f16x2));
+        pk[ss][1] = __builtin_bit_cast(u32, __builtin_convertvector(f32x2{p[ss][2], p[ss][3]}, f16x2));
+        lsum[ss] = T::dot2(pk[ss][0], kOnesF16x2, T::dot2(pk[ss][1], kOnesF16x2, lsum[ss]));
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+          pb[ss][g][0] = GQ > 1 ? quad_bcast_iu(pk[ss][0], g) : pk[ss][0];
+          pb[ss][g][1] = GQ > 1 ? quad_bcast_iu(pk[ss][1], g) : pk[ss][1];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < VWT; ++q) {
+        const u32 v0 = vb[q], v1 = vb[VWT + q], v2 = vb[2 * VWT + q], v3 = vb[3 * VWT + q];
+        const u32 lo01 = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
+        const u32 hi01 = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
+        const u32 lo23 = __builtin_amdgcn_perm(v3, v2, 0x05040100u);
+        const u32 hi23 = __builtin_amdgcn_perm(v3, v2, 0x07060302u);
+#pragma unroll
+        for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+          for (int g = 0; g < GQ; ++g) {
+            float& a0 = acc[ss * GQ + g][2 * q];
+            float& a1 = acc[ss * GQ + g][2 * q + 1];
+            a0 = T::dot2(lo01, pb[ss][g][0], T::dot2(lo23, pb[ss][g][1], a0));
+            a1 = T::dot2(hi01, pb[ss][g][0], T::dot2(hi23, pb[ss][g][1], a1));
+          }
+      }
+    } else {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss)
+        lsum[ss] += (p[ss][0] + p[ss][1]) + (p[ss][2] + p[ss][3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float vf[DPL];
+#pragma unroll
+        for (int q = 0; q < VWT; ++q) {
+          vf[2 * q] = T::lo(vb[r * VWT + q]);
+          vf[2 * q + 1] = T::hi(vb[r * VWT + q]);
+        }
+#pragma unroll
+        for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+          for (int g = 0; g < GQ; ++g) {
+            const float pbv = GQ > 1 ? quad_bcast_i(p[ss][r], g) : p[ss][r];
+#pragma unroll
+            for (int j = 0; j < DPL; ++j)
+              acc[ss * GQ + g][j] = fmaf(pbv, vf[j], acc[ss * GQ + g][j]);
+          }
+      }
+    }
+  }
+
+  // Sum acc and lsum over the four lane rows; exact max over the lanes of each head.
+  __device__ __forceinline__ void reduce_rows() {
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss) {
+      lsum[ss] = sum_xor32(sum_xor16(lsum[ss]));
+      mtrue[ss] = allmax_head<GQ>(mtrue[ss]);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[h][j] = sum_xor32(sum_xor16(acc[h][j]));
+  }
+
+  // After reduce_rows: rescale to the exact maximum and store the partial of the G
+  // heads: O (G, D) row-major at po, m and l (G) at pm / pl (reference semantics:
+  // m = max score in natural units or -1e9 if nothing was seen, l = sum exp(s - m),
+  // O = sum exp(s - m) V). Rows of lanes split the heads between them.
+  __device__ __forceinline__ void store_partial(float* po, float* pm, float* pl) {
+    float f[NS];
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss)
+      f[ss] = mtrue[ss] > kNegInf ? __builtin_amdgcn_exp2f(mref[ss] - mtrue[ss]) : 0.f;
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) {
+        const int h = ss * GQ + g;
+        const float fh = GQ > 1 ? quad_bcast_i(f[ss], g) : f[ss];
+        if (h % 4 == r16) {
+          float v[DPL];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) v[j] = acc[h][j] * fh;
+          st_floats<DPL>(po + h * D + c * DPL, v);
+        }
+      }
+    if (r16 == 0 && c < GQ) {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        const bool seen = mtrue[ss] > kNegInf;
+        pm[ss * GQ + c] = seen ? mtrue[ss] * kLn2 : kEmptyM;
+        pl[ss * GQ + c] = lsum[ss] * f[ss];
+      }
+    }
+  }
+
+  // After reduce_rows: normalised output of the G heads (q head h at out + h * o_h).
+  __device__ __forceinline__ void store_output(uint8_t* out, int64_t o_h) {
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) {
+        const int h = ss * GQ + g;
+        const float L = GQ > 1 ? quad_bcast_i(lsum[ss], g) : lsum[ss];
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        if (h % 4 == r16) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j)
+            T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), acc[h][j] * inv);
+        }
+      }
+  }
+};
+
+// Resident wavefronts per SIMD the register allocator is held to: the page buffers
+// (D/4 words each), G*D/16 accumulators and the q operand must fit without spilling.
+template <int D, int G>
+constexpr int min_waves_per_simd() {
+  return D >= 256 ? 1 : (D * G >= 1024 ? 1 : 2);
+}
+
+// Pages [first, first + n) of one (sequence, kv head), streamed through register buffers:
+// while page k is computed, the loads of the next DEPTH pages are in flight. The
+// steady-state loop has no early exit and issues its loads unconditionally, so the wait
+// counters at its head see the same pending loads on every path and only wait for the
+// page about to be used; the last pages are peeled off after it. Buffer 0 must already
+// hold (or be loading) page 0; page(i) is the base address of page i, valid(i) its valid
+// token count.
+template <int DEPTH, class W, class PageFn, class ValidFn>
+__device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KW], u32 (&va)[W::VW],
+                                             int n, PageFn page, ValidFn valid) {
+  u32 kb[W::KW], vb[W::VW];
+  if constexpr (DEPTH == 1) {
+    int k = 0;
+    for (; k + 2 < n; k += 2) {
+      wv.load_page(kb, vb, page(k + 1));
+      wv.compute_page(ka, va, valid(k));
+      wv.load_page(ka, va, page(k + 2));
+      wv.compute_page(kb, vb, valid(k + 1));
+    }
+    if (k + 1 < n) {
+      wv.load_page(kb, vb, page(k + 1));
+      wv.compute_page(ka, va, valid(k));
+      wv.compute_page(kb, vb, valid(k + 1));
+    } else if (k < n) {
+      wv.compute_page(ka, va, valid(k));
+    }
+  } else {
+    u32 kc[W::KW], vc[W::VW];
+    if (n > 1) wv.load_page(kb, vb, page(1));
+    int k = 0;
+    for (; k + 4 < n; k += 3) {
+      wv.load_page(kc, vc, page(k + 2));
+      wv.compute_page(ka, va, valid(k));
+      wv.load_page(ka, va, page(k + 3));
+      wv.compute_page(kb, vb, valid(k + 1));
+      wv.load_page(kb, vb, page(k + 4));
+      wv.compute_page(kc, vc, valid(k + 2));
+    }
+    const int r = n - k;   // 1..4 pages left; buffers a, b hold pages k, k+1
+    if (r >= 3) wv.load_page(kc, vc, page(k + 2));
+    if (r >= 1) wv.compute_page(ka, va, valid(k));
+    if (r >= 4) wv.load_page(ka, va, page(k + 3));
+    if (r >= 2) wv.compute_page(kb, vb, valid(k + 1));
+    if (r >= 3) wv.compute_page(kc, vc, valid(k + 2));
+    if (r >= 4) wv.compute_page(ka, va, valid(k + 3));
+  }
+}
+
+// Pages kept in flight ahead of the one being computed: two for head_dim <= 128, one for
+// 256 (whose page buffers are twice as large).
+template <int D>
+constexpr int prefetch_depth() { return D <= 128 ? 2 : 1; }
+
+// ---------------------------------------------------------------- pass 1, explicit split
+template <class T, int D, int G, int NW, bool MFMA>
+__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_split(Pass1Args a) {
+  using WV = Wave<T, D, G, MFMA>;
+  constexpr int DPL = WV::DPL;
+  constexpr int NS = WV::NS, GQ = WV::GQ;
+  __shared__ float sm_acc[NW > 1 ? NW : 1][G][D];
+  __shared__ float sm_m[NW > 1 ? NW : 1][G], sm_mt[NW > 1 ? NW : 1][G], sm_l[NW > 1 ? NW : 1][G];
+
+  WV wv;
+  wv.init(a);
+  const int w = uniform(threadIdx.x >> 6);
+
+  int t = blockIdx.x;
+  const int hc = t % a.chunks;
+  t /= a.chunks;
+  const int kvh = t % a.hkv;
+  t /= a.hkv;
+  const int s = t % a.split;
+  const int b = t / a.split;
+
+  const int seq0 = seq_begin(a, b);
+  const int seq1 = max(seq_begin(a, b + 1), seq0);
+  const int npages = seq1 - seq0;
+  const int pps = (npages + a.split - 1) / a.split;          // attention_ext.cu:249-252
+  const int p0 = min(s * pps, npages);
+  const int n = max(min(p0 + pps, npages) - p0, 0);
+  const int valid_last = min(max(ld_const(a.last_len, b), 0), kPage);
+  const int qh0 = kvh * a.group + hc * G;
+
+  wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+  wv.reset();
+
+  // pages of this wavefront: p0 + w + NW*k, k < nk
+  const int nk = n > w ? (n - w + NW - 1) / NW : 0;
+  const int32_t* ids = a.indices + seq0 + p0 + w;
+  const int last_k = (npages - 1 - p0 - w) % NW == 0 ? (npages - 1 - p0 - w) / NW : -1;
+  const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
+  auto page = [&](int k) -> const uint8_t* {
+    u32 pid = (u32)uniform(ld_const(ids, NW * k));
+    pid = pid < a.num_pages ? pid : 0u;
+    return kvh_base + (int64_t)pid * a.kv_p;
+  };
+  auto valid = [&](int k) -> int { return k == last_k ? valid_last : kPage; };
+
+  u32 ka[WV::KW], va[WV::VW];
+  if (nk > 0) {
+    wv.load_page(ka, va, page(0));
+    stream_pages<prefetch_depth<D>()>(wv, ka, va, nk, page, valid);
+  }
+  wv.reduce_rows();
+
+  if constexpr (NW == 1) {
+    if (a.direct) {
+      wv.store_output(a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h);
+    } else {
+      // partial rows of consecutive heads are split rows apart
+      const int64_t row = ((int64_t)b * a.hq + qh0) * a.split + s;
+      float f[NS];
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss)
+        f[ss] = wv.mtrue[ss] > kNegInf ? __builtin_amdgcn_exp2f(wv.mref[ss] - wv.mtrue[ss]) : 0.f;
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+          const int h = ss * GQ + g;
+          const float fh = GQ > 1 ? quad_bcast_i(f[ss], g) : f[ss];
+          if (h % 4 == wv.r16) {
+            float v[DPL];
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) v[j] = wv.acc[h][j] * fh;
+            st_floats<DPL>(a.part_o + (row + (int64_t)h * a.split) * D + wv.c * DPL, v);
+          }
+        }
+      if (wv.r16 == 0 && wv.c < GQ) {
+#pragma unroll
+        for (int ss = 0; ss < NS; ++ss) {
+          const int64_t rr = row + (int64_t)(ss * GQ + wv.c) * a.split;
+          const bool seen = wv.mtrue[ss] > kNegInf;
+          a.part_m[rr] = seen ? wv.mtrue[ss] * kLn2 : kEmptyM;
+          a.part_l[rr] = wv.lsum[ss] * f[ss];
+        }
+      }
+    }
+  } else {
+    // merge the NW wavefronts through LDS
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      if (h % 4 == wv.r16) {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) sm_acc[w][h][wv.c * DPL + j] = wv.acc[h][j];
+      }
+    }
+    if (wv.r16 == 0 && wv.c < GQ) {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        sm_m[w][ss * GQ + wv.c] = wv.mref[ss];
+        sm_mt[w][ss * GQ + wv.c] = wv.mtrue[ss];
+        sm_l[w][ss * GQ + wv.c] = wv.lsum[ss];
+      }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
+      const int h = idx / D, d = idx % D;
+      float mt = kNegInf;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) mt = fmaxf(mt, sm_mt[ww][h]);
+      float L = 0.f, O = 0.f;
+      const bool empty = !(mt > kNegInf);
+      if (!empty) {
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) {
+          const float f = __builtin_amdgcn_exp2f(sm_m[ww][h] - mt);
+          L += sm_l[ww][h] * f;
+          O += sm_acc[ww][h][d] * f;
+        }
+      }
+      const int qh = qh0 + h;
+      if (a.direct) {
+        T::store(a.out + (int64_t)b * a.o_b + (int64_t)qh * a.o_h + 2 * d, L > 0.f ? O / L : 0.f);
+      } else {
+        const int64_t row = ((int64_t)b * a.hq + qh) * a.split + s;
+        a.part_o[row * D + d] = empty ? 0.f : O;
+        if (d == 0) {
+          a.part_m[row] = empty ? kEmptyM : mt * kLn2;
+          a.part_l[row] = L;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pass 1, balanced
+// Linear unit u of pair p = b * HC + hc (HC = hkv * chunks) and page i of sequence b is
+// (seq_begin(b) - seq_begin(0)) * HC + hc * npages(b) + i. Wavefront w covers
+// [w * L, (w + 1) * L) with L = ceil(U / W); each maximal run of its range inside one pair
+// is a segment, stored at partial slot w + p.
+template <class T, int D, int G, int NW, bool MFMA>
+__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_balanced(Pass1Args a) {
+  using WV = Wave<T, D, G, MFMA>;
+  WV wv;
+  wv.init(a);
+  const int HC = a.hkv * a.chunks;
+  const int W = gridDim.x * NW;
+  const int wid = uniform(blockIdx.x * NW + (threadIdx.x >> 6));
+  const int base = seq_begin(a, 0);
+  const int64_t U = (int64_t)max(seq_begin(a, a.batch) - base, 0) * HC;
+  const int64_t L = (U + W - 1) / W;
+  int64_t u = (int64_t)wid * L;
+  const int64_t u_end = min(u + L, U);
+  if (u >= u_end) return;
+
+  // sequence containing u: the largest b with start(b) <= u (binary search)
+  int lo = 0, hi = a.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)(seq_begin(a, mid) - base) * HC <= u) lo = mid; else hi = mid - 1;
+  }
+  int b = lo;
+  int seq0 = seq_begin(a, b);
+  int np = max(seq_begin(a, b + 1), seq0) - seq0;
+  if (np <= 0) return;   // only for a decreasing kv_indptr (invalid input): stay in bounds
+  const int64_t rel = u - (int64_t)(seq0 - base) * HC;
+  if (rel < 0 || rel >= (int64_t)np * HC) return;
+  int hc = (int)(rel / np);
+  int pg = (int)(rel % np);
+
+  auto page_ptr = [&](int bb, int hcc, int i) -> const uint8_t* {
+      u32 pid = (u32)uniform(ld_const(a.indices, seq_begin(a, bb) + i));
+    pid = pid < a.num_pages ? pid : 0u;
+    return a.kv + (int64_t)(hcc / a.chunks) * a.kv_h + (int64_t)pid * a.kv_p;
+  };
+
+  u32 ka[WV::KW], va[WV::VW];
+  wv.load_page(ka, va, page_ptr(b, hc, pg));
+  while (true) {
+    const int n = (int)min((int64_t)(np - pg), u_end - u);   // pages in this segment (>= 1)
+    // the pair after this segment (if the range continues)
+    int nb = b, nhc = hc, nseq0 = seq0, nnp = np;
+    bool more = u + n < u_end;
+    if (more && pg + n == np) {
+      if (++nhc == HC) {
+        nhc = 0;
+        do {
+          ++nb;
+          nseq0 = seq_begin(a, nb);
+          nnp = max(seq_begin(a, nb + 1), nseq0) - nseq0;
+        } while (nnp == 0 && nb < a.batch - 1);
+        more = nnp > 0;   // false only for an invalid kv_indptr
+      }
+    }
+    const int kvh = hc / a.chunks;
+    const int qh0 = kvh * a.group + (hc % a.chunks) * G;
+    wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+    wv.reset();
+    const int valid_last = min(max(ld_const(a.last_len, b), 0), kPage);
+    const int first = pg;
+    const int cur_b = b, cur_hc = hc;
+    auto page = [&](int k) -> const uint8_t* { return page_ptr(cur_b, cur_hc, first + k); };
+    auto valid = [&](int k) -> int { return first + k == np - 1 ? valid_last : kPage; };
+    stream_pages<prefetch_depth<D>()>(wv, ka, va, n, page, valid);
+    wv.reduce_rows();
+    const int64_t slot = (int64_t)wid + (int64_t)b * HC + hc;
+    wv.store_partial(a.part_o + slot * G * D, a.part_m + slot * G, a.part_l + slot * G);
+    if (!more) break;
+    u += n;
+    if (pg + n == np) {
+      b = nb;
+      hc = nhc;
+      seq0 = nseq0;
+      np = nnp;
+      pg = 0;
+    } else {
+      pg += n;
+    }
+    wv.load_page(ka, va, page_ptr(b, hc, pg));
+  }
+}
+
+// ---------------------------------------------------------------- pass 2
+template <class T, int D>
+__device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const float* po,
+                                          const float* pm, const float* pl, int nslots,
+                                          int64_t stride_rows) {
+  // row's partial k sits at po + k * stride_rows * D, pm/pl + k * stride_rows
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  float M = kNegInf;
+  for (int k = lane; k < nslots; k += 64) M = fmaxf(M, pm[(int64_t)k * stride_rows]);
+  M = wave_max(M);
+  float accv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) accv[e] = 0.f;
+  float L = 0.f;
+  for (int k0 = 0; k0 < nslots; k0 += 64) {
+    const int k = k0 + lane;
+    float wgt = 0.f;
+    if (k < nslots) {
+      wgt = __builtin_amdgcn_exp2f((pm[(int64_t)k * stride_rows] - M) * kLog2e);
+      L += wgt * pl[(int64_t)k * stride_rows];
+    }
+    const int cnt = min(64, nslots - k0);
+    for (int j = 0; j < cnt; ++j) {
+      const float wk = readlane_f(wgt, j);
+      const float* o = po + ((int64_t)(k0 + j) * stride_rows) * D + lane * E;
+      if constexpr (E == 1) {
+        accv[0] = fmaf(wk, o[0], accv[0]);
+      } else if constexpr (E == 2) {
+        const f32x2 v = *reinterpret_cast<const f32x2*>(o);
+        accv[0] = fmaf(wk, v[0], accv[0]);
+        accv[1] = fmaf(wk, v[1], accv[1]);
+      } else {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accv[e] = fmaf(wk, v[e], accv[e]);
+      }
+    }
+  }
+  L = wave_sum(L);
+  const int b = row / m.hq, qh = row % m.hq;
+  uint8_t* op = m.out + (int64_t)b * m.o_b + (int64_t)qh * m.o_h + 2 * lane * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e) T::store(op + 2 * e, L > 0.f ? accv[e] / L : 0.f);
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(256) void dk_merge_split(MergeArgs m) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m.batch * m.hq) return;
+  const int64_t r0 = (int64_t)row * m.split;
+  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, m.split, 1);
+}
+
+template <class T, int D>
+__global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m.batch * m.hq) return;
+  const int b = row / m.hq, qh = row % m.hq;
+  const int HC = m.pairs_per_seq, G = m.heads;
+  auto sb = [&](int bb) { return min(max(ld_const(m.indptr, bb), 0), m.num_indices); };
+  const int base = sb(0);
+  const int64_t U = (int64_t)max(sb(m.batch) - base, 0) * HC;
+  const int W = m.total_waves;
+  const int64_t L = (U + W - 1) / W;
+  const int seq0 = sb(b);
+  const int np = max(sb(b + 1), seq0) - seq0;
+  const int hc = qh / G, g = qh % G;
+  int nslots = 0;
+  int64_t first_slot = 0;
+  if (np > 0 && L > 0) {
+    const int64_t start = (int64_t)(seq0 - base) * HC + (int64_t)hc * np;
+    const int64_t w0 = start / L, w1 = (start + np - 1) / L;
+    nslots = (int)(w1 - w0 + 1);
+    first_slot = w0 + (int64_t)b * HC + hc;
+  }
+  // slot k of this pair is first_slot + k; head g of slot s is row s * G + g
+  const int64_t r0 = first_slot * G + g;
+  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, G);
+}
+
+}  // namespace dk

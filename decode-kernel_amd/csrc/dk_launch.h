@@ -1,0 +1,103 @@
+// dk_launch.h — host-side selection and launch of the decode kernels for one element type.
+// dk_f16.hip and dk_bf16.hip instantiate these templates (compiled in parallel);
+// dk_api.hip calls them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "dk_kernels.h"
+
+namespace dk {
+
+struct Pass1Launch {
+  int d = 128, heads = 4, waves = 4;   // head_dim, q heads per workgroup, waves per workgroup
+  bool mfma = false, balanced = false;
+  int grid = 0;
+  hipStream_t stream = nullptr;
+};
+
+// Kernel symbol for (head_dim, heads, waves, path, mode); nullptr if not instantiated.
+template <class T>
+const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool balanced);
+template <class T>
+const void* merge_symbol(int d, bool balanced);
+
+template <class T>
+hipError_t launch_pass1(const Pass1Args& a, const Pass1Launch& L) {
+  const void* fn = pass1_symbol<T>(L.d, L.heads, L.waves, L.mfma, L.balanced);
+  if (!fn) return hipErrorInvalidDeviceFunction;
+  Pass1Args arg = a;
+  void* args[] = {&arg};
+  return hipLaunchKernel(fn, dim3(L.grid), dim3(L.waves * 64), args, 0, L.stream);
+}
+
+template <class T>
+hipError_t launch_merge(const MergeArgs& m, int d, bool balanced, hipStream_t stream) {
+  const void* fn = merge_symbol<T>(d, balanced);
+  if (!fn) return hipErrorInvalidDeviceFunction;
+  MergeArgs arg = m;
+  void* args[] = {&arg};
+  const int rows = m.batch * m.hq;
+  return hipLaunchKernel(fn, dim3((rows + 3) / 4), dim3(256), args, 0, stream);
+}
+
+// ---- symbol tables (instantiated per element type)
+template <class T, int D, int G, int NW, bool M>
+const void* pass1_sym(bool balanced) {
+  return balanced ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M>)
+                  : reinterpret_cast<const void*>(&dk_pass1_split<T, D, G, NW, M>);
+}
+
+template <class T, int D, int G>
+const void* pass1_sym_w(int waves, bool mfma, bool balanced) {
+  switch (waves) {
+    case 1: return mfma ? pass1_sym<T, D, G, 1, true>(balanced) : pass1_sym<T, D, G, 1, false>(balanced);
+    case 2: return mfma ? pass1_sym<T, D, G, 2, true>(balanced) : pass1_sym<T, D, G, 2, false>(balanced);
+    case 4: return mfma ? pass1_sym<T, D, G, 4, true>(balanced) : pass1_sym<T, D, G, 4, false>(balanced);
+    default: return nullptr;
+  }
+}
+
+template <class T, int D>
+const void* pass1_sym_g(int heads, int waves, bool mfma, bool balanced) {
+  switch (heads) {
+    case 1: return pass1_sym_w<T, D, 1>(waves, mfma, balanced);
+    case 2: return pass1_sym_w<T, D, 2>(waves, mfma, balanced);
+    case 4: return pass1_sym_w<T, D, 4>(waves, mfma, balanced);
+    case 8:
+      if constexpr (D <= 128) return pass1_sym_w<T, D, 8>(waves, mfma, balanced);
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template <class T>
+const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool balanced) {
+  switch (d) {
+    case 64: return pass1_sym_g<T, 64>(heads, waves, mfma, balanced);
+    case 128: return pass1_sym_g<T, 128>(heads, waves, mfma, balanced);
+    case 256: return pass1_sym_g<T, 256>(heads, waves, mfma, balanced);
+    default: return nullptr;
+  }
+}
+
+template <class T>
+const void* merge_symbol(int d, bool balanced) {
+  switch (d) {
+    case 64: return balanced ? reinterpret_cast<const void*>(&dk_merge_balanced<T, 64>)
+                             : reinterpret_cast<const void*>(&dk_merge_split<T, 64>);
+    case 128: return balanced ? reinterpret_cast<const void*>(&dk_merge_balanced<T, 128>)
+                              : reinterpret_cast<const void*>(&dk_merge_split<T, 128>);
+    case 256: return balanced ? reinterpret_cast<const void*>(&dk_merge_balanced<T, 256>)
+                              : reinterpret_cast<const void*>(&dk_merge_split<T, 256>);
+    default: return nullptr;
+  }
+}
+
+// Explicit instantiation declarations (definitions in dk_f16.hip / dk_bf16.hip).
+extern template const void* pass1_symbol<F16>(int, int, int, bool, bool);
+extern template const void* pass1_symbol<BF16>(int, int, int, bool, bool);
+extern template const void* merge_symbol<F16>(int, bool);
+extern template const void* merge_symbol<BF16>(int, bool);
+
+}  // namespace dk

@@ -35,28 +35,44 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def _run(cmd: list[str]) -> None:
-    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+HIP_SOURCES = ("dk_api.hip", "dk_f16.hip", "dk_bf16.hip")
+
+
+def _filter(out: str) -> str:
     # hipcc's host pass reports the device-only feature flag as unknown; drop that noise.
-    out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
-    if proc.returncode != 0:
-        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
-    if out.strip():
-        print(out, file=sys.stderr)
+    return "\n".join(l for l in out.splitlines() if "packed-fp32-ops" not in l)
+
+
+def _run_all(cmds: list[list[str]]) -> None:
+    """Run compile commands in parallel; raise with the output of the first failure."""
+    procs = [(c, subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True))
+             for c in cmds]
+    failed = None
+    for cmd, proc in procs:
+        out = _filter(proc.communicate()[0])
+        if proc.returncode != 0 and failed is None:
+            failed = f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}"
+        elif out.strip():
+            print(out, file=sys.stderr)
+    if failed:
+        raise RuntimeError(failed)
 
 
 def build(verbose: bool = False) -> Path:
     """Compile csrc/ into libdk_decode.so (always rebuilds). Returns the library path."""
     BUILD_DIR.mkdir(exist_ok=True)
-    args_o = BUILD_DIR / "dk_args.o"
-    dec_o = BUILD_DIR / "dk_decode.o"
-    _run(["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}",
-          "-c", str(CSRC / "dk_args.cpp"), "-o", str(args_o)])
     hipcc = _hipcc()
-    _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / "dk_decode.hip"), "-o", str(dec_o)])
+    objs = [BUILD_DIR / "dk_args.o"]
+    cmds = [["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}",
+             "-c", str(CSRC / "dk_args.cpp"), "-o", str(objs[0])]]
+    for src in HIP_SOURCES:
+        obj = BUILD_DIR / (Path(src).stem + ".o")
+        objs.append(obj)
+        cmds.append([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)])
+    _run_all(cmds)
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", str(dec_o), str(args_o),
-          "-o", str(tmp)])
+    _run_all([[hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs),
+               "-o", str(tmp)]])
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")

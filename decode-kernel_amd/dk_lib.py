@@ -46,7 +46,7 @@ class DkStrides(ctypes.Structure):
 
 class DkOptions(ctypes.Structure):
     _fields_ = [("qk_path", ctypes.c_int32), ("waves_per_group", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 6)]
+                ("waves_per_cu", ctypes.c_int32), ("reserved", ctypes.c_int32 * 5)]
 
 
 _P = ctypes.c_void_p
@@ -58,7 +58,7 @@ _SZ = ctypes.c_size_t
 SIGNATURES = {
     "dk_abi_version": (ctypes.c_int, []),
     "dk_last_error": (ctypes.c_char_p, []),
-    "dk_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "dk_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
     "dk_partials_layout": (ctypes.c_int, [_I32, _I32, _I32, _I32, ctypes.POINTER(_SZ),
                                           ctypes.POINTER(_SZ), ctypes.POINTER(_SZ),
                                           ctypes.POINTER(_SZ)]),
@@ -111,8 +111,10 @@ def check(rc: int, what: str) -> None:
     raise DecodeLaunchError(f"{what}: HIP error {rc}: {msg}")
 
 
-def workspace_bytes(batch: int, num_q_heads: int, head_dim: int, split_kv: int) -> int:
-    return int(load().dk_workspace_bytes(batch, num_q_heads, head_dim, split_kv))
+def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                    split_kv: int) -> int:
+    """Scratch bytes for split_kv (0 = balanced mode, 1 = none, > 1 = explicit partials)."""
+    return int(load().dk_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, split_kv))
 
 
 def partials_layout(batch: int, num_q_heads: int, head_dim: int, split_kv: int):
@@ -133,8 +135,9 @@ def choose_split(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
     return int(rc)
 
 
-def options(qk_path: int = 0, waves_per_group: int = 0) -> DkOptions:
+def options(qk_path: int = 0, waves_per_group: int = 0, waves_per_cu: int = 0) -> DkOptions:
     o = DkOptions()
     o.qk_path = qk_path
     o.waves_per_group = waves_per_group
+    o.waves_per_cu = waves_per_cu
     return o

@@ -64,9 +64,11 @@ typedef struct {
 /* Optional tuning knobs (NULL = defaults). No counterpart in the reference, which
  * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
 typedef struct {
-  int32_t qk_path;        /* 0 = default (MFMA), 1 = MFMA q.k, 2 = VALU q.k (A/B baseline) */
-  int32_t waves_per_group;/* 0 = default (4); 1, 2 or 4 wavefronts per workgroup         */
-  int32_t reserved[6];    /* must be 0                                                    */
+  int32_t qk_path;         /* 0 = default (VALU dot2), 1 = MFMA q.k, 2 = VALU q.k          */
+  int32_t waves_per_group; /* 0 = default (4); 1, 2 or 4 wavefronts per workgroup          */
+  int32_t waves_per_cu;    /* split_kv == 0 only: persistent wavefronts per compute unit
+                              (0 = default); the grid is min(2048, CUs * waves_per_cu)     */
+  int32_t reserved[5];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */
@@ -75,12 +77,15 @@ int dk_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
 const char* dk_last_error(void);
 
-/* Bytes of fp32 scratch that dk_decode_attention needs for `split_kv` splits:
- * partial_O (batch, Hq, split, D) + partial_m and partial_l (batch, Hq, split),
- * the scratch of src/cuda_/attention_ext.cu:563-568 / src/layout.md:142-152.
- * 0 when split_kv == 1 (single pass, no scratch). split_kv must be >= 1. */
-size_t dk_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t head_dim,
-                          int32_t split_kv);
+/* Bytes of fp32 scratch that dk_decode_attention needs for `split_kv`:
+ *   split_kv == 1: 0 (single pass, no scratch);
+ *   split_kv  > 1: partial_O (batch, Hq, split, D) + partial_m and partial_l
+ *                  (batch, Hq, split), the scratch of src/cuda_/attention_ext.cu:563-568 /
+ *                  src/layout.md:142-152;
+ *   split_kv == 0: the partials of the balanced mode (one per wavefront segment).
+ * 0 for an invalid shape. */
+size_t dk_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t split_kv);
 
 /* Byte offsets of partial_O, partial_m and partial_l inside the workspace and its total
  * size for split_kv >= 1 (layout of src/layout.md:148-152, all fp32, C-contiguous,
@@ -90,22 +95,27 @@ int dk_partials_layout(int32_t batch, int32_t num_q_heads, int32_t head_dim,
                        int32_t split_kv, size_t* off_o, size_t* off_m, size_t* off_l,
                        size_t* total);
 
-/* Split count chosen from occupancy over the device's compute units, for an average of
- * `avg_pages_per_seq` pages per sequence (use num_indices / batch: no device sync).
- * No counterpart in the reference (split_kv is always caller-given there,
+/* An explicit split count (for split_kv > 1 callers) chosen from occupancy over the
+ * device's compute units, for an average of `avg_pages_per_seq` pages per sequence (use
+ * num_indices / batch: no device sync). split_kv == 0 needs no choice: it balances work
+ * itself. No counterpart in the reference (split_kv is always caller-given there,
  * src/attention.py:32). Returns >= 1, or < 0 on a bad argument / HIP error. */
 int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t dtype, int64_t avg_pages_per_seq,
                     int32_t device);
 
-/* decode_attention: pass 1 (split-KV partials, one workgroup per (sequence, kv head,
- * split)) then pass 2 (log-sum-exp merge). split_kv == 1 runs one pass that writes
- * `out` directly (no workspace needed). split_kv == 0 picks the split with
- * dk_choose_split on the current device.
+/* decode_attention: pass 1 (split-KV partials) then pass 2 (log-sum-exp merge).
+ *   split_kv == 1: one pass, one workgroup per (sequence, kv head) writing `out` directly
+ *                  (no workspace needed);
+ *   split_kv  > 1: the reference's partition: one workgroup per (sequence, kv head,
+ *                  split) over ceil(pages/split)-page ranges, then the merge;
+ *   split_kv == 0: balanced mode: a persistent grid whose wavefronts each stream an equal
+ *                  share of all (sequence, kv head, page) units, whatever the lengths,
+ *                  then the merge.
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
  * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
  * functions behind src/attention.py:50-58. Differences: the caller allocates `out`
- * and the workspace; any split_kv >= 1 (the reference caps it at 32); bf16; int64
+ * and the workspace; any split_kv >= 0 (the reference allows 1..32); bf16; int64
  * page offsets; explicit stream. */
 int dk_decode_attention(const void* q, const void* kv_data, const int32_t* kv_indptr,
                         const int32_t* kv_indices, const int32_t* kv_last_page_len,
@@ -127,7 +137,9 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
 /* Pass 1 only: writes partial_O / partial_m / partial_l for split_kv >= 1 splits into
  * the workspace (layout from dk_partials_layout; partial_m is the split's max of
  * q.k*scale, -1e9 for an empty split, partial_l = sum exp(score - partial_m),
- * partial_O = sum exp(score - partial_m) * V, unnormalised).
+ * partial_O = sum exp(score - partial_m) * V, unnormalised). split_kv == 0 runs the
+ * balanced pass 1 into a workspace of dk_workspace_bytes(..., 0) bytes; its partials
+ * (one per wavefront segment) have no public layout (this is for timing pass 1).
  * Replaces the partition launch launch_partition_hd (src/cuda_/attention_ext.cu:452-476)
  * with the semantics of decode_attn_partition_kernel (:207-349). `out`-related strides
  * are ignored. */

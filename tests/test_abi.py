@@ -39,11 +39,16 @@ def test_every_declared_symbol_is_exported():
 
 def test_workspace_and_partials_layout():
     # partial_O (B,Hq,S,D) f32 + partial_m/l (B,Hq,S) f32, each 256-byte aligned
-    assert dk_lib.workspace_bytes(32, 32, 128, 1) == 0
+    assert dk_lib.workspace_bytes(32, 32, 8, 128, 1) == 0
     o, m, l, total = dk_lib.partials_layout(32, 32, 128, 4)
     rows = 32 * 32 * 4
     assert o == 0 and m == rows * 128 * 4 and l == m + rows * 4 and total == l + rows * 4
-    assert dk_lib.workspace_bytes(32, 32, 128, 4) == total
+    assert dk_lib.workspace_bytes(32, 32, 8, 128, 4) == total
+    # balanced mode: (2048 wavefront slots + batch * kv_heads pairs) * 4 heads rows
+    rows_b = (2048 + 32 * 8) * 4
+    assert dk_lib.workspace_bytes(32, 32, 8, 128, 0) == \
+        ((rows_b * 128 * 4 + 255) // 256 * 256) + ((rows_b * 4 + 255) // 256 * 256) + rows_b * 4
+    assert dk_lib.workspace_bytes(32, 30, 8, 128, 4) == 0      # invalid shape
     assert dk_lib.partials_layout(3, 5, 64, 1)[3] > 0
     with pytest.raises(dk_lib.DecodeArgumentError):
         dk_lib.partials_layout(1, 1, 64, 0)
@@ -76,6 +81,7 @@ def _call(lib, **kw):
     (dict(dtype=7), dk_lib.DK_EINVAL, "dtype"),
     (dict(split=5000), dk_lib.DK_EINVAL, "split_kv"),
     (dict(split=-1), dk_lib.DK_EINVAL, "split_kv"),
+    (dict(split=0, ws_bytes=4096), dk_lib.DK_EWORKSPACE, "workspace"),
     (dict(batch=-1), dk_lib.DK_EINVAL, "batch"),
     (dict(num_indices=-1), dk_lib.DK_EINVAL, "num_indices"),
     (dict(num_pages=0), dk_lib.DK_EINVAL, "page pool"),
@@ -90,6 +96,7 @@ def _call(lib, **kw):
     (dict(strides=dk_lib.DkStrides(-1, 128, 0, 0, 0, 0, 0, 0)), dk_lib.DK_EINVAL, "non-negative"),
     (dict(opts=dk_lib.options(qk_path=3)), dk_lib.DK_EINVAL, "qk_path"),
     (dict(opts=dk_lib.options(waves_per_group=3)), dk_lib.DK_EINVAL, "waves_per_group"),
+    (dict(opts=dk_lib.options(waves_per_cu=40)), dk_lib.DK_EINVAL, "waves_per_cu"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(kw, code, needle):
     lib = dk_lib.load()
@@ -114,7 +121,7 @@ def test_null_strides_and_partials_entry_point():
     st = dk_lib.DkStrides()
     rc = lib.dk_decode_partials(0x10000, 0x20000, 0x30000, 0x40000, 0x50000, None, 0, 1, 32, 8,
                                 128, 16, 8, 8, 0, ctypes.byref(st), 0, None, None)
-    assert rc == dk_lib.DK_EINVAL
+    assert rc == dk_lib.DK_EWORKSPACE
     rc = lib.dk_merge_partials(None, 0, None, 1, 32, 96, 0, 0, 0, 4, None)
     assert rc == dk_lib.DK_EINVAL
 

@@ -13,6 +13,20 @@ import torch
 
 import attention
 import layout
+
+
+def _check_partials(po, pm, pl, O, m, l, dtype):
+    """Pass-1 partials vs the exact ones. m is the split max of the scaled scores. For
+    fp16, P.V uses p rounded to fp16 (relative error <= 2^-11 per weight, the same
+    rounded p in l), so l is compared to 1e-3 and O through the normalised O / l."""
+    pm, pl, po = pm.cpu().numpy(), pl.cpu().numpy(), po.cpu().numpy()
+    np.testing.assert_allclose(pm, m, rtol=1e-5, atol=1e-5)
+    l_rtol = 1e-3 if dtype == torch.float16 else 1e-5
+    np.testing.assert_allclose(pl, l, rtol=l_rtol, atol=1e-6)
+    live = l > 0
+    np.testing.assert_allclose(po[live] / pl[live][:, None], O[live] / l[live][:, None],
+                               rtol=0, atol=2e-3 if dtype == torch.float16 else 1e-4)
+    assert (po[~live] == 0).all()
 from attention import decode_attention, decode_partials, merge_partials
 from helpers import err_stats, golden_to_torch, load_golden, to_np
 from oracle import reference as ref
@@ -68,9 +82,7 @@ def test_golden_partials(name):
         po, pm, pl = decode_partials(q, kv, indptr, ids, last, S)
         torch.cuda.synchronize()
         m_want, l_want, o_want = z[f"partial_m_s{S}"], z[f"partial_l_s{S}"], z[f"partial_o_s{S}"]
-        np.testing.assert_allclose(pm.cpu().numpy(), m_want, rtol=1e-5, atol=1e-5)
-        np.testing.assert_allclose(pl.cpu().numpy(), l_want, rtol=1e-5, atol=1e-6)
-        np.testing.assert_allclose(po.cpu().numpy(), o_want, rtol=1e-4, atol=1e-4)
+        _check_partials(po, pm, pl, o_want, m_want, l_want, q.dtype)
         # pass 2 alone on the golden partials
         merged = merge_partials(torch.tensor(o_want, dtype=torch.float32, device=DEV),
                                 torch.tensor(m_want, dtype=torch.float32, device=DEV),
@@ -221,18 +233,17 @@ def test_empty_sequences_and_more_splits_than_pages():
         assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
 
 
-def test_partials_match_oracle_two_pass():
-    _announce("partials vs oracle")
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_partials_match_oracle_two_pass(dtype):
+    _announce(f"partials vs oracle {dtype}")
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-        2, [500, 61], 8, 2, 128, device=DEV, page_table="permuted", seed=3)
+        2, [500, 61], 8, 2, 128, dtype=dtype, device=DEV, page_table="permuted", seed=3)
     for S in (1, 3, 8, 40):
         po, pm, pl = decode_partials(q, kv, indptr, ids, last, S)
         torch.cuda.synchronize()
         O, m, l = skv.split_partials(to_np(q), to_np(kv), to_np(indptr), to_np(ids),
                                      to_np(last), S)
-        np.testing.assert_allclose(pm.cpu().numpy(), m, rtol=1e-5, atol=1e-5)
-        np.testing.assert_allclose(pl.cpu().numpy(), l, rtol=1e-4, atol=1e-5)
-        np.testing.assert_allclose(po.cpu().numpy(), O, rtol=1e-4, atol=2e-4)
+        _check_partials(po, pm, pl, O, m, l, q.dtype)
 
 
 def test_strided_q_out_and_side_stream():
@@ -320,3 +331,59 @@ def test_metric_config_sample():
         out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
         torch.cuda.synchronize()
         _check(out, want, rows=subset, label=f"metric S={s}")
+
+
+# ---------------------------------------------------------------- balanced mode
+
+@pytest.mark.parametrize("waves_per_cu", [1, 2, 5, 16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_balanced_ragged_with_empty_sequences(waves_per_cu, dtype):
+    # lengths chosen so that wavefront ranges start and end inside pairs, on pair
+    # boundaries, and span several short sequences; two sequences have no pages
+    lens = [0, 1, 17, 16, 4000, 0, 33, 2, 900, 1023, 1024, 1025, 5]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        len(lens), lens, 32, 8, 128, dtype=dtype, device=DEV, page_table="permuted",
+        pool_pages=1200, seed=waves_per_cu)
+    want = _oracle(q, kv, indptr, ids, last)
+    for path in (0, 1):
+        for wpg in (1, 4):
+            _announce(f"balanced wpc={waves_per_cu} {dtype} path={path} wpg={wpg}")
+            out = decode_attention(q, kv, indptr, ids, last, split_kv=0, qk_path=path,
+                                   waves_per_group=wpg, waves_per_cu=waves_per_cu)
+            out2 = decode_attention(q, kv, indptr, ids, last, split_kv=0, qk_path=path,
+                                    waves_per_group=wpg, waves_per_cu=waves_per_cu)
+            torch.cuda.synchronize()
+            assert torch.equal(out, out2)
+            _check(out, want, label=f"wpc={waves_per_cu} path={path} wpg={wpg}")
+            assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[5]) == 0
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(64, 32, 8), (64, 8, 1), (128, 64, 4), (256, 16, 4),
+                                      (128, 6, 2)])
+def test_balanced_head_layouts(d, hq, hkv):
+    # group 8 and 16 (head chunks), group 3 (1 head per wavefront), head_dim 64 / 256
+    lens = [300, 7, 129]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        3, lens, hq, hkv, d, device=DEV, page_table="permuted", pool_pages=60, seed=d + hq)
+    want = _oracle(q, kv, indptr, ids, last)
+    for wpc in (1, 8):
+        _announce(f"balanced heads d={d} {hq}/{hkv} wpc={wpc}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=0, waves_per_cu=wpc)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"d={d} {hq}/{hkv} wpc={wpc}")
+
+
+def test_balanced_pass1_alone_runs():
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        4, 1000, 32, 8, 128, device=DEV, page_table="permuted", seed=5)
+    import ctypes
+    import dk_lib
+    lib = dk_lib.load()
+    ws = torch.empty(dk_lib.workspace_bytes(4, 32, 8, 128, 0), dtype=torch.uint8, device=DEV)
+    st = attention._strides(q, kv, None)
+    rc = lib.dk_decode_partials(q.data_ptr(), kv.data_ptr(), indptr.data_ptr(), ids.data_ptr(),
+                                last.data_ptr(), ws.data_ptr(), ws.numel(), 4, 32, 8, 128, 16,
+                                kv.shape[0], ids.shape[0], 0, ctypes.byref(st), 0, None,
+                                torch.cuda.current_stream().cuda_stream)
+    dk_lib.check(rc, "partials")
+    torch.cuda.synchronize()
