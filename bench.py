@@ -42,11 +42,13 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--split", type=int, default=0, help="split_kv (0 = balanced mode)")
+    ap.add_argument("--split", type=int, default=0, help="split_kv (0 = automatic)")
+    ap.add_argument("--schedule", type=int, default=0,
+                    help="split_kv 0: 0 automatic, 1 balanced, 2 one pass")
     ap.add_argument("--qk-path", type=int, default=0, help="0 default, 1 MFMA, 2 VALU")
-    ap.add_argument("--waves", type=int, default=0, help="wavefronts per workgroup (0 = 4)")
+    ap.add_argument("--waves", type=int, default=0, help="wavefronts per workgroup (0 = 1)")
     ap.add_argument("--waves-per-cu", type=int, default=0,
-                    help="balanced mode: persistent wavefronts per CU (0 = default)")
+                    help="balanced schedule: wavefronts per CU (0 = default)")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
@@ -123,7 +125,9 @@ def main():
     ws = torch.empty(max(ws_bytes, p_total), dtype=torch.uint8, device=dev)
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
     strides = attention._strides(q, kv, out)
-    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu)
+    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule)
+    # the schedule the full call runs (split_kv 0 resolves on the device's CU count)
+    eff = dk_lib.plan_schedule(B, hq, hkv, d, split, opts)
     stream = torch.cuda.current_stream(dev)
     code = attention._DTYPE_CODE[dtype]
     common = (q.data_ptr(), kv.data_ptr(), indptr.data_ptr(), ids.data_ptr(), last.data_ptr())
@@ -133,9 +137,12 @@ def main():
         return lib.dk_decode_attention_ex(*common, out.data_ptr(), ws.data_ptr(), ws.numel(),
                                           *shape, split, ctypes.byref(opts), stream.cuda_stream)
 
-    def pass1_call():
+    def pass1_only():
         return lib.dk_decode_partials(*common, ws.data_ptr(), ws.numel(), *shape, split,
                                       ctypes.byref(opts), stream.cuda_stream)
+
+    # The dominant kernel: with one pass it is the whole call; otherwise pass 1 alone.
+    pass1_call = full_call if eff == 1 else pass1_only
 
     dk_lib.check(full_call(), "decode_attention")
     dk_lib.check(pass1_call(), "decode_partials")
@@ -178,7 +185,9 @@ def main():
                                f"D={d} {args.dtype} page_size=16 permuted pages",
                    "batch": B, "context_length": ctx, "num_q_heads": hq, "num_kv_heads": hkv,
                    "head_dim": d, "page_size": 16,
-                   "split_kv": split if split else "balanced",
+                   "split_kv": split,
+                   "schedule": {1: "one pass"}.get(eff, "balanced + merge" if eff == 0
+                                                   else f"split {eff} + merge"),
                    "qk_path": "mfma" if args.qk_path == 1 else "valu"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
         "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
@@ -187,7 +196,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
                      "traffic": read_traffic(),
-                     "kernel": "dk_pass1_balanced" if split == 0 else "dk_pass1_split"},
+                     "kernel": "dk_pass1_balanced" if eff == 0 else "dk_pass1_split"},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -130,6 +130,7 @@ def decode_attention(
     qk_path: int = 0,
     waves_per_group: int = 0,
     waves_per_cu: int = 0,
+    schedule: int = 0,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
@@ -141,12 +142,14 @@ def decode_attention(
         kv_last_page_len : (batch,) int32 valid tokens in each sequence's last page
         split_kv         : KV partitions per (sequence, head). 1 -> one pass writing the
                            output directly; > 1 -> the reference's ceil(N/S)-page split
-                           partials + log-sum-exp merge; 0 / None -> balanced mode
-                           (equal work per wavefront) + merge.
+                           partials + log-sum-exp merge; 0 / None -> automatic: the
+                           one-pass kernel when batch * kv heads fills the device, else the
+                           balanced schedule (equal pages per workgroup) + merge.
         out, workspace   : optional preallocated output (batch, num_q_heads, head_dim) and
                            uint8 scratch of dk_lib.workspace_bytes(...) bytes
-        qk_path, waves_per_group, waves_per_cu : tuning knobs (0 = defaults;
-                           qk_path 1 = MFMA q.k, 2 = VALU q.k)
+        qk_path, waves_per_group, waves_per_cu, schedule : tuning knobs (0 =
+                           defaults; qk_path 1 = MFMA q.k, 2 = VALU q.k; schedule (for
+                           split_kv 0) 1 = always balanced, 2 = always one pass)
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
@@ -175,7 +178,7 @@ def decode_attention(
     ws_ptr = workspace.data_ptr() if ws_need else None
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
-    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu)
+    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.dk_decode_attention_ex(

@@ -62,6 +62,21 @@ int explicit_split(const Problem& p, int device) {
                       pl.waves);
 }
 
+// Wavefronts per compute unit the balanced schedule keeps resident. Two measured best on
+// MI355X at every decode shape tried (each wavefront keeps two pages of loads in flight).
+int waves_per_cu(const Problem& p) {
+  return p.opt.waves_per_cu ? p.opt.waves_per_cu : kDefaultWavesPerCU;
+}
+
+// Whether split_kv == 0 runs the one-pass kernel: forced by options.schedule, else when
+// the (sequence, head chunk) pairs alone give every compute unit its wavefronts.
+// Pass-1-only calls always take the balanced schedule (they return partials).
+bool auto_one_pass(const Problem& p, const Plan& pl, int cus) {
+  if (!p.need_out || p.opt.schedule == 1) return false;
+  return p.opt.schedule == 2 ||
+         (int64_t)p.batch * pl.pairs_per_seq * pl.waves >= (int64_t)cus * waves_per_cu(p);
+}
+
 }  // namespace
 
 // Validation, planning and both passes; shared by the extern "C" entry points.
@@ -70,18 +85,28 @@ int run(Problem p, bool do_merge, void* stream) {
   const int rc = validate(p);
   if (rc != DK_OK || p.batch == 0) return rc;
   Plan pl = make_plan(p);
-  const bool direct = p.need_out && p.split == 1;
-  const int64_t esize = 2;
-
+  int waves_per_pair = 0;   // balanced: workgroups per head chunk
   if (pl.balanced) {
     const int dev = current_device(-1);
     const int cus = cu_count(dev);
     if (cus <= 0) return hip_fail(hipErrorNoDevice, "compute-unit count");
-    const int per_cu = p.opt.waves_per_cu ? p.opt.waves_per_cu : kDefaultWavesPerCU;
-    int64_t waves = std::min<int64_t>(kMaxWaves, (int64_t)cus * per_cu);
-    waves = std::max<int64_t>(pl.waves, waves / pl.waves * pl.waves);
-    pl.grid = waves / pl.waves;
+    if (auto_one_pass(p, pl, cus)) {
+      p.split = 1;
+      pl.balanced = false;
+      pl.grid = (int64_t)p.batch * pl.pairs_per_seq;
+    } else {
+      // a whole number of workgroups per head chunk
+      const int per_cu = waves_per_cu(p);
+      const int64_t hc = pl.pairs_per_seq;
+      const int64_t max_groups = std::max<int64_t>(hc, kMaxWaves / pl.waves / hc * hc);
+      int64_t groups = std::max<int64_t>(1, (int64_t)cus * per_cu / pl.waves);
+      groups = std::min(max_groups, std::max(hc, (groups + hc / 2) / hc * hc));
+      pl.grid = groups;
+      waves_per_pair = (int)(groups / hc);
+    }
   }
+  const bool direct = p.need_out && (p.split == 1 || pl.balanced);
+  const int64_t esize = 2;
 
   Pass1Args a{};
   a.q = static_cast<const uint8_t*>(p.q);
@@ -89,7 +114,11 @@ int run(Problem p, bool do_merge, void* stream) {
   a.indptr = p.indptr;
   a.indices = p.indices;
   a.last_len = p.last_len;
-  if (!direct) {
+  // Partials: every call but a full one-pass call (the balanced schedule writes them for
+  // the sequences that span several workgroups even when it writes `out` directly; the
+  // pass-1-only entry point writes them for split_kv == 1 too).
+  const bool need_partials = !(p.need_out && p.split == 1);
+  if (need_partials) {
     const int64_t rows = pl.balanced ? balanced_rows(p.batch, p.hq, p.hkv, p.head_dim)
                                      : split_rows(p.batch, p.hq, p.split);
     size_t off_o, off_m, off_l, total;
@@ -120,6 +149,9 @@ int run(Problem p, bool do_merge, void* stream) {
   a.page_extent = (uint32_t)((p.st.kv_r + (int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * esize);
   a.direct = direct ? 1 : 0;
   a.kscale = kLog2e / sqrtf((float)p.head_dim);
+  // every launch that can store partials has them (or the library is inconsistent)
+  if ((pl.balanced || !direct) && (!a.part_o || !a.part_m || !a.part_l))
+    return set_error(DK_EWORKSPACE, "internal: partials not assigned for this schedule");
 
   Pass1Launch L;
   L.d = p.head_dim;
@@ -132,7 +164,7 @@ int run(Problem p, bool do_merge, void* stream) {
   hipError_t e = p.dtype == DK_F16 ? launch_pass1<F16>(a, L) : launch_pass1<BF16>(a, L);
   if (e != hipSuccess) return hip_fail(e, "pass-1 launch");
 
-  if (do_merge && !direct) {
+  if (do_merge && p.split != 1) {
     MergeArgs m{};
     m.po = a.part_o;
     m.pm = a.part_m;
@@ -147,7 +179,7 @@ int run(Problem p, bool do_merge, void* stream) {
     m.num_indices = a.num_indices;
     m.pairs_per_seq = pl.pairs_per_seq;
     m.heads = pl.heads;
-    m.total_waves = (int)pl.grid * pl.waves;
+    m.waves_per_pair = waves_per_pair;
     e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)
                           : launch_merge<BF16>(m, p.head_dim, pl.balanced, L.stream);
     if (e != hipSuccess) return hip_fail(e, "merge launch");
@@ -230,6 +262,27 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, in
   const int dev = dk::current_device(device);
   if (dev < 0) return dk::hip_fail(hipErrorNoDevice, "dk_choose_split");
   return dk::explicit_split(p, dev);
+}
+
+int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t split_kv, const dk_options* opts, int32_t device) {
+  dk::clear_error();
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
+      (head_dim != 64 && head_dim != 128 && head_dim != 256) || split_kv < 0 || split_kv > 4096)
+    return dk::set_error(DK_EINVAL, "dk_plan_schedule: bad argument");
+  if (split_kv != 0) return split_kv;
+  Problem p;
+  p.batch = batch;
+  p.hq = num_q_heads;
+  p.hkv = num_kv_heads;
+  p.head_dim = head_dim;
+  if (opts) p.opt = *opts;
+  if (p.opt.schedule < 0 || p.opt.schedule > 2)
+    return dk::set_error(DK_EINVAL, "options.schedule must be 0, 1 or 2; got %d", p.opt.schedule);
+  const int dev = dk::current_device(device);
+  const int cus = dk::cu_count(dev);
+  if (cus <= 0) return dk::hip_fail(hipErrorNoDevice, "dk_plan_schedule");
+  return dk::auto_one_pass(p, dk::make_plan(p), cus) ? 1 : 0;
 }
 
 int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv_indptr,

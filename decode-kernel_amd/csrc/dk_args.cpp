@@ -90,7 +90,7 @@ Plan make_plan(const Problem& p) {
   pl.heads = heads_per_group(pl.group, p.head_dim);
   pl.chunks = pl.group / pl.heads;
   pl.pairs_per_seq = p.hkv * pl.chunks;
-  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : 4;
+  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : kDefaultWavesPerGroup;
   pl.mfma = p.opt.qk_path == 1;
   pl.balanced = p.split == 0;
   pl.grid = pl.balanced ? 0 : (int64_t)p.batch * pl.pairs_per_seq * std::max(p.split, 1);
@@ -129,6 +129,8 @@ int validate(const Problem& p) {
                      o.waves_per_group);
   if (o.waves_per_cu < 0 || o.waves_per_cu > 32)
     return set_error(DK_EINVAL, "options.waves_per_cu must be in [0, 32]; got %d", o.waves_per_cu);
+  if (o.schedule < 0 || o.schedule > 2)
+    return set_error(DK_EINVAL, "options.schedule must be 0, 1 or 2; got %d", o.schedule);
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything
@@ -169,10 +171,10 @@ int validate(const Problem& p) {
     return set_error(DK_EINVAL, "batch*num_q_heads too large");
   // Two passes and the pass-1-only entry point write fp32 partials.
   if (p.split != 1 || !p.need_out) {
-    const int64_t rows = p.split == 0 ? balanced_rows(p.batch, p.hq, p.hkv, p.head_dim)
-                                      : split_rows(p.batch, p.hq, p.split);
-    size_t o, m, l, req;
-    partials_layout_rows(rows, p.head_dim, &o, &m, &l, &req);
+    size_t req, o, m, l;
+    partials_layout_rows(p.split == 0 ? balanced_rows(p.batch, p.hq, p.hkv, p.head_dim)
+                                      : split_rows(p.batch, p.hq, p.split),
+                         p.head_dim, &o, &m, &l, &req);
     if (!p.workspace || p.workspace_bytes < req)
       return set_error(DK_EWORKSPACE, "workspace of %zu bytes required, %zu given", req,
                        p.workspace_bytes);

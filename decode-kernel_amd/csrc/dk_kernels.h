@@ -75,7 +75,8 @@ struct Pass1Args {
   int32_t num_indices;
   uint32_t num_pages;                 // clamp bound for page ids (min(num_pages, 2^31))
   uint32_t page_extent;               // bytes of a page a kv head's loads may touch (< 2^31)
-  int32_t direct;                     // explicit split 1: write the normalised output
+  int32_t direct;                     // explicit split 1 / balanced: may write the
+                                      // normalised output (0: partials only)
   float kscale;                       // log2(e) / sqrt(head_dim)
 };
 
@@ -87,7 +88,7 @@ struct MergeArgs {
   int64_t o_b, o_h;                   // bytes
   int32_t batch, hq, split;           // explicit split
   const int32_t* indptr;              // balanced: recompute each pair's slots
-  int32_t num_indices, pairs_per_seq, heads, total_waves;
+  int32_t num_indices, pairs_per_seq, heads, waves_per_pair;
 };
 
 // ---------------------------------------------------------------- element types
@@ -517,10 +518,10 @@ struct Wave {
   }
 
   // After reduce_rows: rescale to the exact maximum and store the partial of the G
-  // heads: O (G, D) row-major at po, m and l (G) at pm / pl (reference semantics:
-  // m = max score in natural units or -1e9 if nothing was seen, l = sum exp(s - m),
-  // O = sum exp(s - m) V). Rows of lanes split the heads between them.
-  __device__ __forceinline__ void store_partial(float* po, float* pm, float* pl) {
+  // heads, head h at row row0 + h * hstride of part_o (D floats) / part_m / part_l
+  // (reference semantics: m = max score in natural units or -1e9 if nothing was seen,
+  // l = sum exp(s - m), O = sum exp(s - m) V). Rows of lanes split the heads between them.
+  __device__ __forceinline__ void store_partial(const Pass1Args& a, int64_t row0, int64_t hstride) {
     float f[NS];
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss)
@@ -535,15 +536,16 @@ struct Wave {
           float v[DPL];
 #pragma unroll
           for (int j = 0; j < DPL; ++j) v[j] = acc[h][j] * fh;
-          st_floats<DPL>(po + h * D + c * DPL, v);
+          st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
         }
       }
     if (r16 == 0 && c < GQ) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
+        const int64_t r = row0 + (int64_t)(ss * GQ + c) * hstride;
         const bool seen = mtrue[ss] > kNegInf;
-        pm[ss * GQ + c] = seen ? mtrue[ss] * kLn2 : kEmptyM;
-        pl[ss * GQ + c] = lsum[ss] * f[ss];
+        a.part_m[r] = seen ? mtrue[ss] * kLn2 : kEmptyM;
+        a.part_l[r] = lsum[ss] * f[ss];
       }
     }
   }
@@ -626,15 +628,92 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KW], u32 (&va)[
 template <int D>
 constexpr int prefetch_depth() { return D <= 128 ? 2 : 1; }
 
+// ---------------------------------------------------------------- workgroup combine
+// LDS scratch for merging the NW wavefronts of a workgroup.
+template <int G, int D, int NW>
+struct CombineSmem {
+  float acc[NW][G][D];
+  float m[NW][G], mt[NW][G], l[NW][G];
+};
+
+// After every wavefront's reduce_rows: the workgroup's result for its G heads, written
+// normalised to out (head h at out + h * o_h) when `direct`, otherwise as a partial with
+// head h at row prow0 + h * phstride.
+template <class T, int D, int G, int NW, class WV>
+__device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 ? NW : 1)>& sm,
+                                              const Pass1Args& a, bool direct, uint8_t* out,
+                                              int64_t o_h, int64_t prow0, int64_t phstride) {
+  constexpr int DPL = WV::DPL, NS = WV::NS, GQ = WV::GQ;
+  if constexpr (NW == 1) {
+    if (direct) wv.store_output(out, o_h);
+    else wv.store_partial(a, prow0, phstride);
+  } else {
+    const int w = uniform(threadIdx.x >> 6);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      if (h % 4 == wv.r16) {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) sm.acc[w][h][wv.c * DPL + j] = wv.acc[h][j];
+      }
+    }
+    if (wv.r16 == 0 && wv.c < GQ) {
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss) {
+        sm.m[w][ss * GQ + wv.c] = wv.mref[ss];
+        sm.mt[w][ss * GQ + wv.c] = wv.mtrue[ss];
+        sm.l[w][ss * GQ + wv.c] = wv.lsum[ss];
+      }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
+      const int h = idx / D, d = idx % D;
+      float mt = kNegInf;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) mt = fmaxf(mt, sm.mt[ww][h]);
+      float L = 0.f, O = 0.f;
+      const bool empty = !(mt > kNegInf);
+      if (!empty) {
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) {
+          const float f = __builtin_amdgcn_exp2f(sm.m[ww][h] - mt);
+          L += sm.l[ww][h] * f;
+          O += sm.acc[ww][h][d] * f;
+        }
+      }
+      if (direct) {
+        T::store(out + (int64_t)h * o_h + 2 * d, L > 0.f ? O / L : 0.f);
+      } else {
+        const int64_t row = prow0 + h * phstride;
+        a.part_o[row * D + d] = empty ? 0.f : O;
+        if (d == 0) {
+          a.part_m[row] = empty ? kEmptyM : mt * kLn2;
+          a.part_l[row] = L;
+        }
+      }
+    }
+    __syncthreads();   // the LDS is reused by the next segment
+  }
+}
+
+// Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages.
+template <int D, class WV, class PageFn, class ValidFn>
+__device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n, PageFn page,
+                                                   ValidFn valid) {
+  const int nk = n > w ? (n - w + NW - 1) / NW : 0;
+  if (nk > 0) {
+    auto pk = [&](int k) { return page(w + NW * k); };
+    auto vk = [&](int k) { return valid(w + NW * k); };
+    u32 ka[WV::KW], va[WV::VW];
+    wv.load_page(ka, va, pk(0));
+    stream_pages<prefetch_depth<D>()>(wv, ka, va, nk, pk, vk);
+  }
+}
+
 // ---------------------------------------------------------------- pass 1, explicit split
 template <class T, int D, int G, int NW, bool MFMA>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_split(Pass1Args a) {
   using WV = Wave<T, D, G, MFMA>;
-  constexpr int DPL = WV::DPL;
-  constexpr int NS = WV::NS, GQ = WV::GQ;
-  __shared__ float sm_acc[NW > 1 ? NW : 1][G][D];
-  __shared__ float sm_m[NW > 1 ? NW : 1][G], sm_mt[NW > 1 ? NW : 1][G], sm_l[NW > 1 ? NW : 1][G];
-
+  __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
   WV wv;
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
@@ -648,8 +727,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
   const int b = t / a.split;
 
   const int seq0 = seq_begin(a, b);
-  const int seq1 = max(seq_begin(a, b + 1), seq0);
-  const int npages = seq1 - seq0;
+  const int npages = max(seq_begin(a, b + 1), seq0) - seq0;
   const int pps = (npages + a.split - 1) / a.split;          // attention_ext.cu:249-252
   const int p0 = min(s * pps, npages);
   const int n = max(min(p0 + pps, npages) - p0, 0);
@@ -658,191 +736,97 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
 
   wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
   wv.reset();
-
-  // pages of this wavefront: p0 + w + NW*k, k < nk
-  const int nk = n > w ? (n - w + NW - 1) / NW : 0;
-  const int32_t* ids = a.indices + seq0 + p0 + w;
-  const int last_k = (npages - 1 - p0 - w) % NW == 0 ? (npages - 1 - p0 - w) / NW : -1;
   const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
-  auto page = [&](int k) -> const uint8_t* {
-    u32 pid = (u32)uniform(ld_const(ids, NW * k));
+  auto page = [&](int i) -> const uint8_t* {
+    u32 pid = (u32)uniform(ld_const(a.indices, seq0 + p0 + i));
     pid = pid < a.num_pages ? pid : 0u;
     return kvh_base + (int64_t)pid * a.kv_p;
   };
-  auto valid = [&](int k) -> int { return k == last_k ? valid_last : kPage; };
-
-  u32 ka[WV::KW], va[WV::VW];
-  if (nk > 0) {
-    wv.load_page(ka, va, page(0));
-    stream_pages<prefetch_depth<D>()>(wv, ka, va, nk, page, valid);
-  }
+  auto valid = [&](int i) -> int { return p0 + i == npages - 1 ? valid_last : kPage; };
+  stream_interleaved<D>(wv, NW, w, n, page, valid);
   wv.reduce_rows();
-
-  if constexpr (NW == 1) {
-    if (a.direct) {
-      wv.store_output(a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h);
-    } else {
-      // partial rows of consecutive heads are split rows apart
-      const int64_t row = ((int64_t)b * a.hq + qh0) * a.split + s;
-      float f[NS];
-#pragma unroll
-      for (int ss = 0; ss < NS; ++ss)
-        f[ss] = wv.mtrue[ss] > kNegInf ? __builtin_amdgcn_exp2f(wv.mref[ss] - wv.mtrue[ss]) : 0.f;
-#pragma unroll
-      for (int ss = 0; ss < NS; ++ss)
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-          const int h = ss * GQ + g;
-          const float fh = GQ > 1 ? quad_bcast_i(f[ss], g) : f[ss];
-          if (h % 4 == wv.r16) {
-            float v[DPL];
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) v[j] = wv.acc[h][j] * fh;
-            st_floats<DPL>(a.part_o + (row + (int64_t)h * a.split) * D + wv.c * DPL, v);
-          }
-        }
-      if (wv.r16 == 0 && wv.c < GQ) {
-#pragma unroll
-        for (int ss = 0; ss < NS; ++ss) {
-          const int64_t rr = row + (int64_t)(ss * GQ + wv.c) * a.split;
-          const bool seen = wv.mtrue[ss] > kNegInf;
-          a.part_m[rr] = seen ? wv.mtrue[ss] * kLn2 : kEmptyM;
-          a.part_l[rr] = wv.lsum[ss] * f[ss];
-        }
-      }
-    }
-  } else {
-    // merge the NW wavefronts through LDS
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      if (h % 4 == wv.r16) {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) sm_acc[w][h][wv.c * DPL + j] = wv.acc[h][j];
-      }
-    }
-    if (wv.r16 == 0 && wv.c < GQ) {
-#pragma unroll
-      for (int ss = 0; ss < NS; ++ss) {
-        sm_m[w][ss * GQ + wv.c] = wv.mref[ss];
-        sm_mt[w][ss * GQ + wv.c] = wv.mtrue[ss];
-        sm_l[w][ss * GQ + wv.c] = wv.lsum[ss];
-      }
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
-      const int h = idx / D, d = idx % D;
-      float mt = kNegInf;
-#pragma unroll
-      for (int ww = 0; ww < NW; ++ww) mt = fmaxf(mt, sm_mt[ww][h]);
-      float L = 0.f, O = 0.f;
-      const bool empty = !(mt > kNegInf);
-      if (!empty) {
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-          const float f = __builtin_amdgcn_exp2f(sm_m[ww][h] - mt);
-          L += sm_l[ww][h] * f;
-          O += sm_acc[ww][h][d] * f;
-        }
-      }
-      const int qh = qh0 + h;
-      if (a.direct) {
-        T::store(a.out + (int64_t)b * a.o_b + (int64_t)qh * a.o_h + 2 * d, L > 0.f ? O / L : 0.f);
-      } else {
-        const int64_t row = ((int64_t)b * a.hq + qh) * a.split + s;
-        a.part_o[row * D + d] = empty ? 0.f : O;
-        if (d == 0) {
-          a.part_m[row] = empty ? kEmptyM : mt * kLn2;
-          a.part_l[row] = L;
-        }
-      }
-    }
-  }
+  combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
+                             a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
+                             ((int64_t)b * a.hq + qh0) * a.split + s, a.split);
 }
 
 // ---------------------------------------------------------------- pass 1, balanced
-// Linear unit u of pair p = b * HC + hc (HC = hkv * chunks) and page i of sequence b is
-// (seq_begin(b) - seq_begin(0)) * HC + hc * npages(b) + i. Wavefront w covers
-// [w * L, (w + 1) * L) with L = ceil(U / W); each maximal run of its range inside one pair
-// is a segment, stored at partial slot w + p.
+// Head-major persistent schedule over workgroups. Workgroup g serves head chunk
+// hc = g % HC (HC = hkv * chunks pairs per sequence), so consecutive workgroups -- and the
+// XCDs they are dispatched to round-robin -- cover all kv heads of the same pages at the
+// same time. The Wg = gridDim / HC workgroups of a head chunk split its pages in sequence
+// order ((b, page) is linear unit seq_begin(b) - seq_begin(0) + page) into Wg ranges of
+// L = ceil(P / Wg) pages; workgroup j takes range j and its NW wavefronts interleave the
+// pages of each segment (maximal run of the range inside one sequence). A sequence covered
+// by a single segment is written out directly (when a.direct); otherwise the segment is
+// stored as a partial at slot (j + b) * HC + hc (unique, < Wg * HC + batch * HC) for the
+// merge kernel.
 template <class T, int D, int G, int NW, bool MFMA>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_balanced(Pass1Args a) {
   using WV = Wave<T, D, G, MFMA>;
+  __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
   WV wv;
   wv.init(a);
+  const int w = uniform(threadIdx.x >> 6);
   const int HC = a.hkv * a.chunks;
-  const int W = gridDim.x * NW;
-  const int wid = uniform(blockIdx.x * NW + (threadIdx.x >> 6));
+  const int g = blockIdx.x;
+  const int hc = g % HC;
+  const int Wg = (int)(gridDim.x / HC);
+  const int j = g / HC;
   const int base = seq_begin(a, 0);
-  const int64_t U = (int64_t)max(seq_begin(a, a.batch) - base, 0) * HC;
-  const int64_t L = (U + W - 1) / W;
-  int64_t u = (int64_t)wid * L;
-  const int64_t u_end = min(u + L, U);
+  const int P = max(seq_begin(a, a.batch) - base, 0);        // pages per head chunk
+  const int L = (P + Wg - 1) / Wg;
+  if (L <= 0) return;                                        // whole workgroup
+  int u = (int)min((int64_t)j * L, (int64_t)P);
+  const int u_end = min(u + L, P);
   if (u >= u_end) return;
 
-  // sequence containing u: the largest b with start(b) <= u (binary search)
+  // sequence containing unit u: the largest b with start(b) <= u (binary search)
   int lo = 0, hi = a.batch - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if ((int64_t)(seq_begin(a, mid) - base) * HC <= u) lo = mid; else hi = mid - 1;
+    if (seq_begin(a, mid) - base <= u) lo = mid; else hi = mid - 1;
   }
   int b = lo;
   int seq0 = seq_begin(a, b);
   int np = max(seq_begin(a, b + 1), seq0) - seq0;
-  if (np <= 0) return;   // only for a decreasing kv_indptr (invalid input): stay in bounds
-  const int64_t rel = u - (int64_t)(seq0 - base) * HC;
-  if (rel < 0 || rel >= (int64_t)np * HC) return;
-  int hc = (int)(rel / np);
-  int pg = (int)(rel % np);
+  int pg = u - (seq0 - base);
+  if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
-  auto page_ptr = [&](int bb, int hcc, int i) -> const uint8_t* {
-      u32 pid = (u32)uniform(ld_const(a.indices, seq_begin(a, bb) + i));
-    pid = pid < a.num_pages ? pid : 0u;
-    return a.kv + (int64_t)(hcc / a.chunks) * a.kv_h + (int64_t)pid * a.kv_p;
-  };
+  const int kvh = hc / a.chunks;
+  const int qh0 = kvh * a.group + (hc % a.chunks) * G;
+  const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
 
-  u32 ka[WV::KW], va[WV::VW];
-  wv.load_page(ka, va, page_ptr(b, hc, pg));
   while (true) {
-    const int n = (int)min((int64_t)(np - pg), u_end - u);   // pages in this segment (>= 1)
-    // the pair after this segment (if the range continues)
-    int nb = b, nhc = hc, nseq0 = seq0, nnp = np;
-    bool more = u + n < u_end;
-    if (more && pg + n == np) {
-      if (++nhc == HC) {
-        nhc = 0;
-        do {
-          ++nb;
-          nseq0 = seq_begin(a, nb);
-          nnp = max(seq_begin(a, nb + 1), nseq0) - nseq0;
-        } while (nnp == 0 && nb < a.batch - 1);
-        more = nnp > 0;   // false only for an invalid kv_indptr
-      }
-    }
-    const int kvh = hc / a.chunks;
-    const int qh0 = kvh * a.group + (hc % a.chunks) * G;
+    const int n = min(np - pg, u_end - u);   // pages of this segment (>= 1)
     wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
     wv.reset();
     const int valid_last = min(max(ld_const(a.last_len, b), 0), kPage);
-    const int first = pg;
-    const int cur_b = b, cur_hc = hc;
-    auto page = [&](int k) -> const uint8_t* { return page_ptr(cur_b, cur_hc, first + k); };
-    auto valid = [&](int k) -> int { return first + k == np - 1 ? valid_last : kPage; };
-    stream_pages<prefetch_depth<D>()>(wv, ka, va, n, page, valid);
+    const int first = pg, cur_seq0 = seq0, cur_np = np;
+    auto page = [&](int i) -> const uint8_t* {
+      u32 pid = (u32)uniform(ld_const(a.indices, cur_seq0 + first + i));
+      pid = pid < a.num_pages ? pid : 0u;
+      return kvh_base + (int64_t)pid * a.kv_p;
+    };
+    auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
+    stream_interleaved<D>(wv, NW, w, n, page, valid);
     wv.reduce_rows();
-    const int64_t slot = (int64_t)wid + (int64_t)b * HC + hc;
-    wv.store_partial(a.part_o + slot * G * D, a.part_m + slot * G, a.part_l + slot * G);
-    if (!more) break;
+
+    const int start = seq0 - base;
+    const int nslots = (start + np - 1) / L - start / L + 1;
+    combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
+                               a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
+                               ((int64_t)(j + b) * HC + hc) * G, 1);
+    if (u + n >= u_end) break;
+    // next non-empty sequence
     u += n;
-    if (pg + n == np) {
-      b = nb;
-      hc = nhc;
-      seq0 = nseq0;
-      np = nnp;
-      pg = 0;
-    } else {
-      pg += n;
-    }
-    wv.load_page(ka, va, page_ptr(b, hc, pg));
+    do {
+      ++b;
+      seq0 = seq_begin(a, b);
+      np = max(seq_begin(a, b + 1), seq0) - seq0;
+    } while (np == 0 && b < a.batch - 1);
+    if (np == 0) break;   // only for an invalid kv_indptr
+    pg = 0;
   }
 }
 
@@ -905,26 +889,25 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= m.batch * m.hq) return;
   const int b = row / m.hq, qh = row % m.hq;
-  const int HC = m.pairs_per_seq, G = m.heads;
+  const int HC = m.pairs_per_seq, G = m.heads, Wg = m.waves_per_pair;
   auto sb = [&](int bb) { return min(max(ld_const(m.indptr, bb), 0), m.num_indices); };
   const int base = sb(0);
-  const int64_t U = (int64_t)max(sb(m.batch) - base, 0) * HC;
-  const int W = m.total_waves;
-  const int64_t L = (U + W - 1) / W;
+  const int P = max(sb(m.batch) - base, 0);
+  const int L = (P + Wg - 1) / Wg;
   const int seq0 = sb(b);
   const int np = max(sb(b + 1), seq0) - seq0;
   const int hc = qh / G, g = qh % G;
   int nslots = 0;
-  int64_t first_slot = 0;
+  int64_t r0 = 0;
   if (np > 0 && L > 0) {
-    const int64_t start = (int64_t)(seq0 - base) * HC + (int64_t)hc * np;
-    const int64_t w0 = start / L, w1 = (start + np - 1) / L;
-    nslots = (int)(w1 - w0 + 1);
-    first_slot = w0 + (int64_t)b * HC + hc;
+    const int start = seq0 - base;
+    const int j0 = start / L;
+    nslots = (start + np - 1) / L - j0 + 1;
+    r0 = ((int64_t)(j0 + b) * HC + hc) * G + g;
   }
-  // slot k of this pair is first_slot + k; head g of slot s is row s * G + g
-  const int64_t r0 = first_slot * G + g;
-  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, G);
+  if (nslots == 1) return;   // pass 1 wrote this head's output
+  // slot k of this pair is r0 + k * HC * G (rows of G heads per slot); none -> zeros
+  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, (int64_t)HC * G);
 }
 
 }  // namespace dk

@@ -65,10 +65,12 @@ typedef struct {
  * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
 typedef struct {
   int32_t qk_path;         /* 0 = default (VALU dot2), 1 = MFMA q.k, 2 = VALU q.k          */
-  int32_t waves_per_group; /* 0 = default (4); 1, 2 or 4 wavefronts per workgroup          */
-  int32_t waves_per_cu;    /* split_kv == 0 only: persistent wavefronts per compute unit
-                              (0 = default); the grid is min(2048, CUs * waves_per_cu)     */
-  int32_t reserved[5];     /* must be 0                                                     */
+  int32_t waves_per_group; /* 0 = default (1); 1, 2 or 4 wavefronts per workgroup          */
+  int32_t waves_per_cu;    /* balanced schedule: wavefronts per compute unit of the
+                              persistent grid (0 = default, 2)                              */
+  int32_t schedule;        /* split_kv == 0: 0 = automatic, 1 = balanced, 2 = one workgroup
+                              per (sequence, kv head) (split_kv == 1)                       */
+  int32_t reserved[4];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */
@@ -82,7 +84,8 @@ const char* dk_last_error(void);
  *   split_kv  > 1: partial_O (batch, Hq, split, D) + partial_m and partial_l
  *                  (batch, Hq, split), the scratch of src/cuda_/attention_ext.cu:563-568 /
  *                  src/layout.md:142-152;
- *   split_kv == 0: the partials of the balanced mode (one per wavefront segment).
+ *   split_kv == 0: the partials of the balanced schedule (one per workgroup segment).
+ * The workspace needs no initialisation; calls that share one must not overlap in time.
  * 0 for an invalid shape. */
 size_t dk_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                           int32_t head_dim, int32_t split_kv);
@@ -104,14 +107,25 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t dtype, int64_t avg_pages_per_seq,
                     int32_t device);
 
+/* The schedule that dk_decode_attention_ex runs for these arguments on `device` (-1 =
+ * current): 1 = one pass (one workgroup per (sequence, kv head), no merge), 0 = balanced
+ * schedule + merge, > 1 = that explicit split + merge. No counterpart in the reference;
+ * for callers that size launches or profile the kernels. Returns < 0 on a bad argument. */
+int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t split_kv, const dk_options* opts,
+                     int32_t device);
+
 /* decode_attention: pass 1 (split-KV partials) then pass 2 (log-sum-exp merge).
  *   split_kv == 1: one pass, one workgroup per (sequence, kv head) writing `out` directly
  *                  (no workspace needed);
  *   split_kv  > 1: the reference's partition: one workgroup per (sequence, kv head,
  *                  split) over ceil(pages/split)-page ranges, then the merge;
- *   split_kv == 0: balanced mode: a persistent grid whose wavefronts each stream an equal
- *                  share of all (sequence, kv head, page) units, whatever the lengths,
- *                  then the merge.
+ *   split_kv == 0: automatic: the split_kv == 1 pass when the (sequence, kv head) pairs
+ *                  give every compute unit options.waves_per_cu (default 2) wavefronts,
+ *                  else the balanced schedule
+ *                  (a persistent grid whose workgroups each stream an equal share of all
+ *                  (sequence, kv head, page) units whatever the lengths; sequences that
+ *                  one workgroup covers are written directly, the rest merged).
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
  * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
  * functions behind src/attention.py:50-58. Differences: the caller allocates `out`

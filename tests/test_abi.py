@@ -44,7 +44,7 @@ def test_workspace_and_partials_layout():
     rows = 32 * 32 * 4
     assert o == 0 and m == rows * 128 * 4 and l == m + rows * 4 and total == l + rows * 4
     assert dk_lib.workspace_bytes(32, 32, 8, 128, 4) == total
-    # balanced mode: (2048 wavefront slots + batch * kv_heads pairs) * 4 heads rows
+    # balanced schedule: (2048 workgroup slots + batch * kv_heads pairs) * 4 heads rows
     rows_b = (2048 + 32 * 8) * 4
     assert dk_lib.workspace_bytes(32, 32, 8, 128, 0) == \
         ((rows_b * 128 * 4 + 255) // 256 * 256) + ((rows_b * 4 + 255) // 256 * 256) + rows_b * 4

@@ -349,9 +349,9 @@ def test_balanced_ragged_with_empty_sequences(waves_per_cu, dtype):
         for wpg in (1, 4):
             _announce(f"balanced wpc={waves_per_cu} {dtype} path={path} wpg={wpg}")
             out = decode_attention(q, kv, indptr, ids, last, split_kv=0, qk_path=path,
-                                   waves_per_group=wpg, waves_per_cu=waves_per_cu)
+                                   waves_per_group=wpg, waves_per_cu=waves_per_cu, schedule=1)
             out2 = decode_attention(q, kv, indptr, ids, last, split_kv=0, qk_path=path,
-                                    waves_per_group=wpg, waves_per_cu=waves_per_cu)
+                                    waves_per_group=wpg, waves_per_cu=waves_per_cu, schedule=1)
             torch.cuda.synchronize()
             assert torch.equal(out, out2)
             _check(out, want, label=f"wpc={waves_per_cu} path={path} wpg={wpg}")
@@ -368,7 +368,8 @@ def test_balanced_head_layouts(d, hq, hkv):
     want = _oracle(q, kv, indptr, ids, last)
     for wpc in (1, 8):
         _announce(f"balanced heads d={d} {hq}/{hkv} wpc={wpc}")
-        out = decode_attention(q, kv, indptr, ids, last, split_kv=0, waves_per_cu=wpc)
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=0, waves_per_cu=wpc,
+                               schedule=1)
         torch.cuda.synchronize()
         _check(out, want, label=f"d={d} {hq}/{hkv} wpc={wpc}")
 
@@ -387,3 +388,31 @@ def test_balanced_pass1_alone_runs():
                                 torch.cuda.current_stream().cuda_stream)
     dk_lib.check(rc, "partials")
     torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- schedules
+
+@pytest.mark.parametrize("batch", [5, 40])
+def test_schedules_agree_and_reuse_a_dirty_workspace(batch):
+    # split_kv=0: the automatic choice, the balanced schedule (at two grid sizes, so the
+    # same sequence is covered by one workgroup in one call and several in another) and
+    # the one-pass kernel all match the oracle; the workspace is reused across calls and
+    # first filled with junk, which no schedule may read
+    import dk_lib
+    base = [3000, 17, 0, 800, 1]
+    lens = (base * (batch // len(base) + 1))[:batch]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, lens, 32, 8, 128, device=DEV, page_table="permuted", seed=batch + 11)
+    want = _oracle(q, kv, indptr, ids, last)
+    ws = torch.randint(0, 256, (dk_lib.workspace_bytes(batch, 32, 8, 128, 0),),
+                       dtype=torch.uint8, device=DEV)
+    outs = []
+    for sched, wpc in ((0, 0), (1, 1), (1, 8), (2, 0), (0, 0)):
+        _announce(f"schedule={sched} wpc={wpc} batch={batch}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=0, workspace=ws,
+                               schedule=sched, waves_per_cu=wpc)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"schedule={sched} wpc={wpc}")
+        outs.append(out.clone())
+    for o in outs[1:]:
+        assert torch.allclose(o.float(), outs[0].float(), atol=2e-3)
