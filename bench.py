@@ -4,7 +4,9 @@ Workload (BASELINE.json metric config): batch 32, context 8192 per sequence, 32 
 8 kv heads, head_dim 128, fp16, page_size 16, page table a seeded random permutation of
 the 16384-page pool; synthetic N(0,1) data already resident in HBM.
 
-A step is one decode_attention call (pass 1 + pass 2) through the C ABI. Before every
+A step is one decode_attention call (pass 1 + pass 2) through the C ABI, with split_kv 0
+(automatic schedule) and the plan hint max_pages_per_seq taken once from the host copy of
+kv_indptr before the timed region (as a serving framework plans a batch). Before every
 step a 1 GiB device fill evicts the 4 MB L2s and the 256 MB Infinity Cache, as the
 reference flushes L2 before each timed call (bench/microbench_cuda.py:75-90,140-157);
 HIP events on the launch stream bracket the call itself. The flush is enqueued without a
@@ -52,7 +54,12 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
+    ap.add_argument("--no-plan-hint", action="store_true",
+                    help="do not pass the host-side max_pages_per_seq plan hint")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
+                    help="after the run, copy a MIB-MiB device buffer twice (a kernel of "
+                         "known traffic that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-sample", type=int, default=16,
                     help="sequences of the workload the CPU baseline computes")
     return ap.parse_args()
@@ -125,11 +132,14 @@ def main():
     ws = torch.empty(max(ws_bytes, p_total), dtype=torch.uint8, device=dev)
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
     strides = attention._strides(q, kv, out)
-    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule)
-    # the schedule the full call runs (split_kv 0 resolves on the device's CU count)
-    eff = dk_lib.plan_schedule(B, hq, hkv, d, split, opts)
-    stream = torch.cuda.current_stream(dev)
+    # plan step, outside the timed region: the longest sequence's page count from the host
+    # side of the page table (what a serving framework keeps on the host)
+    hint = 0 if args.no_plan_hint else attention.plan_hint(indptr.cpu())
+    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule, hint)
     code = attention._DTYPE_CODE[dtype]
+    # the schedule the full call runs (split_kv 0 resolves on the device's CU count)
+    eff = dk_lib.plan_schedule(B, hq, hkv, d, ids.shape[0], code, split, opts)
+    stream = torch.cuda.current_stream(dev)
     common = (q.data_ptr(), kv.data_ptr(), indptr.data_ptr(), ids.data_ptr(), last.data_ptr())
     shape = (B, hq, hkv, d, 16, kv.shape[0], ids.shape[0], code, ctypes.byref(strides))
 
@@ -188,7 +198,9 @@ def main():
                    "split_kv": split,
                    "schedule": {1: "one pass"}.get(eff, "balanced + merge" if eff == 0
                                                    else f"split {eff} + merge"),
-                   "qk_path": "mfma" if args.qk_path == 1 else "valu"},
+                   "plan_hint_max_pages": hint,
+                   "qk_path": "mfma" if args.qk_path == 1 or (args.qk_path == 0 and
+                                                               args.dtype == "bf16") else "valu"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
         "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
         "bytes_per_call": nbytes, "wall_s_timed_loop": round(wall, 3),
@@ -208,6 +220,12 @@ def main():
                       f"sequences (full ctx), median of 3, scaled to the whole batch"}
         rec["max_abs_err_vs_fp32"] = err
     print(json.dumps(rec), flush=True)
+    if args.calibration_copy > 0:
+        src = torch.ones(args.calibration_copy << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     return 0
 
 

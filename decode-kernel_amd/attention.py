@@ -109,6 +109,18 @@ def resolve_split(split_kv: Optional[int]) -> int:
     return split_kv
 
 
+def plan_hint(kv_indptr_host) -> int:
+    """max_pages_per_seq for decode_attention from a HOST copy of kv_indptr (a list, numpy
+    array or CPU tensor), computed once per batch outside the decode call, as serving
+    frameworks keep sequence lengths on the host. Never reads device memory."""
+    if isinstance(kv_indptr_host, torch.Tensor):
+        if kv_indptr_host.device.type != "cpu":
+            raise ValueError("plan_hint takes a host copy of kv_indptr")
+        kv_indptr_host = kv_indptr_host.tolist()
+    ip = [int(x) for x in kv_indptr_host]
+    return max((b - a for a, b in zip(ip[:-1], ip[1:])), default=0)
+
+
 def choose_split(q: torch.Tensor, kv_data: torch.Tensor, kv_indices: torch.Tensor) -> int:
     """An explicit split count chosen from occupancy (for callers that want one)."""
     batch = q.shape[0]
@@ -131,6 +143,7 @@ def decode_attention(
     waves_per_group: int = 0,
     waves_per_cu: int = 0,
     schedule: int = 0,
+    max_pages_per_seq: int = 0,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
@@ -150,6 +163,8 @@ def decode_attention(
         qk_path, waves_per_group, waves_per_cu, schedule : tuning knobs (0 =
                            defaults; qk_path 1 = MFMA q.k, 2 = VALU q.k; schedule (for
                            split_kv 0) 1 = always balanced, 2 = always one pass)
+        max_pages_per_seq: plan hint for split_kv 0 (see plan_hint): the longest
+                           sequence's page count, 0 = unknown. Affects speed only.
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
@@ -178,7 +193,7 @@ def decode_attention(
     ws_ptr = workspace.data_ptr() if ws_need else None
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
-    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule)
+    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.dk_decode_attention_ex(

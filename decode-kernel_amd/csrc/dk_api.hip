@@ -68,13 +68,30 @@ int waves_per_cu(const Problem& p) {
   return p.opt.waves_per_cu ? p.opt.waves_per_cu : kDefaultWavesPerCU;
 }
 
-// Whether split_kv == 0 runs the one-pass kernel: forced by options.schedule, else when
-// the (sequence, head chunk) pairs alone give every compute unit its wavefronts.
-// Pass-1-only calls always take the balanced schedule (they return partials).
+// Workgroups of the balanced grid: about waves_per_cu wavefronts per compute unit, a
+// whole number of workgroups per head chunk, at most kMaxWaves wavefronts.
+int64_t balanced_groups(const Problem& p, const Plan& pl, int cus) {
+  const int64_t hc = pl.pairs_per_seq;
+  const int64_t max_groups = std::max<int64_t>(hc, kMaxWaves / pl.waves / hc * hc);
+  const int64_t groups = std::max<int64_t>(1, (int64_t)cus * waves_per_cu(p) / pl.waves);
+  return std::min(max_groups, std::max(hc, (groups + hc / 2) / hc * hc));
+}
+
+// Whether split_kv == 0 runs the one-pass kernel: forced by options.schedule; else only
+// with the max_pages_per_seq hint, when one workgroup per (sequence, head chunk) fits in
+// the balanced grid and no sequence is longer than a balanced workgroup's share of
+// pages (then one pass finishes no later and needs no merge). Pass-1-only calls always
+// take the balanced schedule (they return partials).
 bool auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return false;
-  return p.opt.schedule == 2 ||
-         (int64_t)p.batch * pl.pairs_per_seq * pl.waves >= (int64_t)cus * waves_per_cu(p);
+  if (p.opt.schedule == 2) return true;
+  const int64_t hint = p.opt.max_pages_per_seq;
+  if (hint <= 0) return false;
+  const int64_t groups = balanced_groups(p, pl, cus);
+  const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
+  const int64_t per_group = groups / pl.pairs_per_seq;   // workgroups per head chunk
+  const int64_t share = (p.num_indices + per_group - 1) / per_group;
+  return pairs <= groups && hint <= share;
 }
 
 }  // namespace
@@ -95,14 +112,8 @@ int run(Problem p, bool do_merge, void* stream) {
       pl.balanced = false;
       pl.grid = (int64_t)p.batch * pl.pairs_per_seq;
     } else {
-      // a whole number of workgroups per head chunk
-      const int per_cu = waves_per_cu(p);
-      const int64_t hc = pl.pairs_per_seq;
-      const int64_t max_groups = std::max<int64_t>(hc, kMaxWaves / pl.waves / hc * hc);
-      int64_t groups = std::max<int64_t>(1, (int64_t)cus * per_cu / pl.waves);
-      groups = std::min(max_groups, std::max(hc, (groups + hc / 2) / hc * hc));
-      pl.grid = groups;
-      waves_per_pair = (int)(groups / hc);
+      pl.grid = balanced_groups(p, pl, cus);
+      waves_per_pair = (int)(pl.grid / pl.pairs_per_seq);
     }
   }
   const bool direct = p.need_out && (p.split == 1 || pl.balanced);
@@ -265,10 +276,12 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, in
 }
 
 int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                     int32_t split_kv, const dk_options* opts, int32_t device) {
+                     int64_t num_indices, int32_t dtype, int32_t split_kv,
+                     const dk_options* opts, int32_t device) {
   dk::clear_error();
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
-      (head_dim != 64 && head_dim != 128 && head_dim != 256) || split_kv < 0 || split_kv > 4096)
+      (head_dim != 64 && head_dim != 128 && head_dim != 256) || split_kv < 0 ||
+      split_kv > 4096 || num_indices < 0 || (dtype != DK_F16 && dtype != DK_BF16))
     return dk::set_error(DK_EINVAL, "dk_plan_schedule: bad argument");
   if (split_kv != 0) return split_kv;
   Problem p;
@@ -276,6 +289,8 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, i
   p.hq = num_q_heads;
   p.hkv = num_kv_heads;
   p.head_dim = head_dim;
+  p.num_indices = num_indices;
+  p.dtype = dtype;
   if (opts) p.opt = *opts;
   if (p.opt.schedule < 0 || p.opt.schedule > 2)
     return dk::set_error(DK_EINVAL, "options.schedule must be 0, 1 or 2; got %d", p.opt.schedule);

@@ -91,7 +91,9 @@ Plan make_plan(const Problem& p) {
   pl.chunks = pl.group / pl.heads;
   pl.pairs_per_seq = p.hkv * pl.chunks;
   pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : kDefaultWavesPerGroup;
-  pl.mfma = p.opt.qk_path == 1;
+  // q.k on MFMA for bf16 by default: its VALU path converts every K element to fp32,
+  // while fp16 has packed dot products (measured: bf16 MFMA faster, fp16 VALU faster)
+  pl.mfma = p.opt.qk_path == 1 || (p.opt.qk_path == 0 && p.dtype == DK_BF16);
   pl.balanced = p.split == 0;
   pl.grid = pl.balanced ? 0 : (int64_t)p.batch * pl.pairs_per_seq * std::max(p.split, 1);
   return pl;
@@ -131,6 +133,9 @@ int validate(const Problem& p) {
     return set_error(DK_EINVAL, "options.waves_per_cu must be in [0, 32]; got %d", o.waves_per_cu);
   if (o.schedule < 0 || o.schedule > 2)
     return set_error(DK_EINVAL, "options.schedule must be 0, 1 or 2; got %d", o.schedule);
+  if (o.max_pages_per_seq < 0)
+    return set_error(DK_EINVAL, "options.max_pages_per_seq must be >= 0; got %d",
+                     o.max_pages_per_seq);
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything

@@ -13,7 +13,7 @@ namespace dk {
 constexpr int kPageSize = 16;        // tokens per page (reference: PAGE_SIZE=16, attention_ext.cu:509)
 constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid (wavefronts)
 constexpr int kDefaultWavesPerCU = 2;
-constexpr int kDefaultWavesPerGroup = 1;
+constexpr int kDefaultWavesPerGroup = 2;
 
 // Everything a launch needs that is known on the host.
 struct Problem {

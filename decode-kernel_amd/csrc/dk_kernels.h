@@ -517,28 +517,60 @@ struct Wave {
       for (int j = 0; j < DPL; ++j) acc[h][j] = sum_xor32(sum_xor16(acc[h][j]));
   }
 
+  // After reduce_rows every lane holds every head's sums. Lane row r16 stores heads
+  // 4k + r16 (k < ceil(G/4)); the value of that head is picked with selects on r16, never
+  // by indexing acc with a lane-dependent value (which would move acc to scratch memory).
+  static constexpr int KR = (G + 3) / 4;   // heads stored per lane row
+
+  // acc[4k + r16][j]. Each candidate passes through an empty asm so that the compiler
+  // cannot fold the selects into one load from a lane-dependent address of acc.
+  __device__ __forceinline__ float row_head(int k, int j) const {
+    float v = acc[4 * k][j];
+    __asm__("" : "+v"(v));
+#pragma unroll
+    for (int t = 1; t < 4; ++t)
+      if (4 * k + t < G) {
+        float o = acc[4 * k + t][j];
+        __asm__("" : "+v"(o));
+        v = r16 == t ? o : v;
+      }
+    return v;
+  }
+
+  // per-head-set value x[ss] of head 4k + r16 (head h sits in set h / GQ at quad lane h % GQ)
+  __device__ __forceinline__ float row_head_scalar(const float (&x)[NS], int k) const {
+    float v = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int h = 4 * k + t;
+      if (h < G) {
+        const float xt = GQ > 1 ? quad_bcast_i(x[h / GQ], h % GQ) : x[h / GQ];
+        v = r16 == t ? xt : v;
+      }
+    }
+    return v;
+  }
+
   // After reduce_rows: rescale to the exact maximum and store the partial of the G
   // heads, head h at row row0 + h * hstride of part_o (D floats) / part_m / part_l
   // (reference semantics: m = max score in natural units or -1e9 if nothing was seen,
-  // l = sum exp(s - m), O = sum exp(s - m) V). Rows of lanes split the heads between them.
+  // l = sum exp(s - m), O = sum exp(s - m) V).
   __device__ __forceinline__ void store_partial(const Pass1Args& a, int64_t row0, int64_t hstride) {
     float f[NS];
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss)
       f[ss] = mtrue[ss] > kNegInf ? __builtin_amdgcn_exp2f(mref[ss] - mtrue[ss]) : 0.f;
 #pragma unroll
-    for (int ss = 0; ss < NS; ++ss)
+    for (int k = 0; k < KR; ++k) {
+      const int h = 4 * k + r16;
+      const float fh = row_head_scalar(f, k);
+      if (h < G) {
+        float v[DPL];
 #pragma unroll
-      for (int g = 0; g < GQ; ++g) {
-        const int h = ss * GQ + g;
-        const float fh = GQ > 1 ? quad_bcast_i(f[ss], g) : f[ss];
-        if (h % 4 == r16) {
-          float v[DPL];
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) v[j] = acc[h][j] * fh;
-          st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
-        }
+        for (int j = 0; j < DPL; ++j) v[j] = row_head(k, j) * fh;
+        st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
       }
+    }
     if (r16 == 0 && c < GQ) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
@@ -553,18 +585,16 @@ struct Wave {
   // After reduce_rows: normalised output of the G heads (q head h at out + h * o_h).
   __device__ __forceinline__ void store_output(uint8_t* out, int64_t o_h) {
 #pragma unroll
-    for (int ss = 0; ss < NS; ++ss)
+    for (int k = 0; k < KR; ++k) {
+      const int h = 4 * k + r16;
+      const float L = row_head_scalar(lsum, k);
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      if (h < G) {
 #pragma unroll
-      for (int g = 0; g < GQ; ++g) {
-        const int h = ss * GQ + g;
-        const float L = GQ > 1 ? quad_bcast_i(lsum[ss], g) : lsum[ss];
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        if (h % 4 == r16) {
-#pragma unroll
-          for (int j = 0; j < DPL; ++j)
-            T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), acc[h][j] * inv);
-        }
+        for (int j = 0; j < DPL; ++j)
+          T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), row_head(k, j) * inv);
       }
+    }
   }
 };
 
@@ -650,10 +680,11 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
   } else {
     const int w = uniform(threadIdx.x >> 6);
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      if (h % 4 == wv.r16) {
+    for (int k = 0; k < WV::KR; ++k) {
+      const int h = 4 * k + wv.r16;
+      if (h < G) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) sm.acc[w][h][wv.c * DPL + j] = wv.acc[h][j];
+        for (int j = 0; j < DPL; ++j) sm.acc[w][h][wv.c * DPL + j] = wv.row_head(k, j);
       }
     }
     if (wv.r16 == 0 && wv.c < GQ) {

@@ -7,6 +7,7 @@ argument checker (csrc/dk_args.cpp) is compiled with g++ and linked in.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -38,24 +39,51 @@ def _hipcc() -> str:
 HIP_SOURCES = ("dk_api.hip", "dk_f16.hip", "dk_bf16.hip")
 
 
+# Per-kernel resource report of the device compiler (VGPRs, scratch, occupancy).
+RESOURCE_FLAG = "-Rpass-analysis=kernel-resource-usage"
+
+
 def _filter(out: str) -> str:
-    # hipcc's host pass reports the device-only feature flag as unknown; drop that noise.
-    return "\n".join(l for l in out.splitlines() if "packed-fp32-ops" not in l)
+    # hipcc's host pass reports the device-only feature flag as unknown; the resource
+    # remarks are parsed separately. Drop both from what is echoed.
+    return "\n".join(l for l in out.splitlines()
+                     if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l
+                     and not l.startswith(("  ", "In file included from")))
 
 
-def _run_all(cmds: list[list[str]]) -> None:
-    """Run compile commands in parallel; raise with the output of the first failure."""
+def kernel_resources(out: str) -> dict:
+    """{kernel: {"VGPRs": n, "ScratchSize": bytes per lane, "Occupancy": waves/SIMD}}."""
+    res, cur = {}, None
+    for line in out.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            cur = res.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"(VGPRs|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]): (\d+)",
+                      line)
+        if m and cur is not None:
+            cur[m.group(1).split()[0]] = int(m.group(2))
+    return res
+
+
+def _run_all(cmds: list[list[str]]) -> str:
+    """Run compile commands in parallel; raise with the output of the first failure.
+    Returns the concatenated raw output (for the resource remarks)."""
     procs = [(c, subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True))
              for c in cmds]
     failed = None
+    raw = []
     for cmd, proc in procs:
-        out = _filter(proc.communicate()[0])
+        text = proc.communicate()[0]
+        raw.append(text)
+        out = _filter(text)
         if proc.returncode != 0 and failed is None:
             failed = f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}"
         elif out.strip():
             print(out, file=sys.stderr)
     if failed:
         raise RuntimeError(failed)
+    return "\n".join(raw)
 
 
 def build(verbose: bool = False) -> Path:
@@ -68,8 +96,17 @@ def build(verbose: bool = False) -> Path:
     for src in HIP_SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)])
-    _run_all(cmds)
+        cmds.append([hipcc, *HIP_FLAGS, RESOURCE_FLAG, f"-I{INCLUDE}", "-c", str(CSRC / src),
+                     "-o", str(obj)])
+    res = kernel_resources(_run_all(cmds))
+    (BUILD_DIR / "kernel_resources.txt").write_text("".join(
+        f"{k} VGPRs={v.get('VGPRs')} scratch={v.get('ScratchSize')} "
+        f"occupancy={v.get('Occupancy')}\n" for k, v in sorted(res.items())))
+    # Every kernel keeps its state in registers and LDS: scratch memory here would mean an
+    # array indexed by a lane-dependent value or a spill, both a large slowdown.
+    scratch = sorted(k for k, v in res.items() if v.get("ScratchSize", 0) > 0)
+    if scratch:
+        raise RuntimeError(f"{len(scratch)} kernels use scratch memory: {scratch[:4]}")
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run_all([[hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs),
                "-o", str(tmp)]])

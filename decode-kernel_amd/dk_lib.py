@@ -47,7 +47,7 @@ class DkStrides(ctypes.Structure):
 class DkOptions(ctypes.Structure):
     _fields_ = [("qk_path", ctypes.c_int32), ("waves_per_group", ctypes.c_int32),
                 ("waves_per_cu", ctypes.c_int32), ("schedule", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 4)]
+                ("max_pages_per_seq", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
 
 
 _P = ctypes.c_void_p
@@ -64,7 +64,7 @@ SIGNATURES = {
                                           ctypes.POINTER(_SZ), ctypes.POINTER(_SZ),
                                           ctypes.POINTER(_SZ)]),
     "dk_choose_split": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _I64, _I32]),
-    "dk_plan_schedule": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32,
+    "dk_plan_schedule": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I64, _I32, _I32,
                                         ctypes.POINTER(DkOptions), _I32]),
     "dk_decode_attention": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I32, _I32, _I32,
                                            _I32, _I32, _I64, _I64, _I32,
@@ -139,9 +139,11 @@ def choose_split(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
 
 
 def plan_schedule(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
-                  split_kv: int, opts: "DkOptions | None" = None, device: int = -1) -> int:
+                  num_indices: int, dtype_code: int, split_kv: int,
+                  opts: "DkOptions | None" = None, device: int = -1) -> int:
     """Schedule a full call runs: 1 one pass, 0 balanced + merge, > 1 explicit split."""
-    rc = load().dk_plan_schedule(batch, num_q_heads, num_kv_heads, head_dim, split_kv,
+    rc = load().dk_plan_schedule(batch, num_q_heads, num_kv_heads, head_dim, num_indices,
+                                 dtype_code, split_kv,
                                  ctypes.byref(opts) if opts is not None else None, device)
     if rc < 0:
         check(rc, "dk_plan_schedule")
@@ -154,10 +156,11 @@ SCHEDULE_ONE_PASS = 2
 
 
 def options(qk_path: int = 0, waves_per_group: int = 0, waves_per_cu: int = 0,
-            schedule: int = SCHEDULE_AUTO) -> DkOptions:
+            schedule: int = SCHEDULE_AUTO, max_pages_per_seq: int = 0) -> DkOptions:
     o = DkOptions()
     o.qk_path = qk_path
     o.waves_per_group = waves_per_group
     o.waves_per_cu = waves_per_cu
     o.schedule = schedule
+    o.max_pages_per_seq = max_pages_per_seq
     return o

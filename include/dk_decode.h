@@ -64,13 +64,19 @@ typedef struct {
 /* Optional tuning knobs (NULL = defaults). No counterpart in the reference, which
  * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
 typedef struct {
-  int32_t qk_path;         /* 0 = default (VALU dot2), 1 = MFMA q.k, 2 = VALU q.k          */
-  int32_t waves_per_group; /* 0 = default (1); 1, 2 or 4 wavefronts per workgroup          */
-  int32_t waves_per_cu;    /* balanced schedule: wavefronts per compute unit of the
-                              persistent grid (0 = default, 2)                              */
+  int32_t qk_path;         /* 0 = default (fp16: VALU dot2, bf16: MFMA), 1 = MFMA q.k,
+                              2 = VALU q.k                                                  */
+  int32_t waves_per_group; /* 0 = default (2); 1, 2 or 4 wavefronts per workgroup          */
+  int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
+                              schedules aim for (0 = default, 2)                            */
   int32_t schedule;        /* split_kv == 0: 0 = automatic, 1 = balanced, 2 = one workgroup
                               per (sequence, kv head) (split_kv == 1)                       */
-  int32_t reserved[4];     /* must be 0                                                     */
+  int32_t max_pages_per_seq; /* plan hint for split_kv == 0: the most pages any sequence
+                              has (from the host copy of kv_indptr), 0 = unknown. With it
+                              the automatic schedule runs one pass when that is as short
+                              as the balanced one; without it, it always balances.
+                              Too small a value affects speed only, never results.       */
+  int32_t reserved[3];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */
@@ -112,20 +118,20 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  * schedule + merge, > 1 = that explicit split + merge. No counterpart in the reference;
  * for callers that size launches or profile the kernels. Returns < 0 on a bad argument. */
 int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                     int32_t head_dim, int32_t split_kv, const dk_options* opts,
-                     int32_t device);
+                     int32_t head_dim, int64_t num_indices, int32_t dtype, int32_t split_kv,
+                     const dk_options* opts, int32_t device);
 
 /* decode_attention: pass 1 (split-KV partials) then pass 2 (log-sum-exp merge).
  *   split_kv == 1: one pass, one workgroup per (sequence, kv head) writing `out` directly
  *                  (no workspace needed);
  *   split_kv  > 1: the reference's partition: one workgroup per (sequence, kv head,
  *                  split) over ceil(pages/split)-page ranges, then the merge;
- *   split_kv == 0: automatic: the split_kv == 1 pass when the (sequence, kv head) pairs
- *                  give every compute unit options.waves_per_cu (default 2) wavefronts,
- *                  else the balanced schedule
- *                  (a persistent grid whose workgroups each stream an equal share of all
- *                  (sequence, kv head, page) units whatever the lengths; sequences that
- *                  one workgroup covers are written directly, the rest merged).
+ *   split_kv == 0: automatic: the balanced schedule (a persistent grid of about
+ *                  options.waves_per_cu wavefronts per compute unit whose workgroups each
+ *                  stream an equal share of all (sequence, kv head, page) units whatever
+ *                  the lengths; sequences one workgroup covers are written directly, the
+ *                  rest merged), or the split_kv == 1 pass when options.max_pages_per_seq
+ *                  shows that one workgroup per pair fits that grid and is no longer.
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
  * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
  * functions behind src/attention.py:50-58. Differences: the caller allocates `out`

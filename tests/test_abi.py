@@ -97,6 +97,8 @@ def _call(lib, **kw):
     (dict(opts=dk_lib.options(qk_path=3)), dk_lib.DK_EINVAL, "qk_path"),
     (dict(opts=dk_lib.options(waves_per_group=3)), dk_lib.DK_EINVAL, "waves_per_group"),
     (dict(opts=dk_lib.options(waves_per_cu=40)), dk_lib.DK_EINVAL, "waves_per_cu"),
+    (dict(opts=dk_lib.options(max_pages_per_seq=-1)), dk_lib.DK_EINVAL, "max_pages_per_seq"),
+    (dict(opts=dk_lib.options(schedule=3)), dk_lib.DK_EINVAL, "schedule"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(kw, code, needle):
     lib = dk_lib.load()
@@ -199,3 +201,21 @@ def test_attention_bytes_matches_reference_model():
     # bench/microbench_cuda.py:114-121 (Q + KV + O) plus the int32 tables
     b = layout.attention_bytes(32, 8192, 32, 8, 128)
     assert b == 1_074_266_112 + 4 * 33 + 4 * 32 * 512 + 4 * 32
+
+
+def test_plan_hint_reads_host_indptr_only():
+    import attention
+    assert attention.plan_hint([0, 3, 3, 10, 11]) == 7
+    assert attention.plan_hint(torch.tensor([0, 512, 1024], dtype=torch.int32)) == 512
+    assert attention.plan_hint([0]) == 0
+
+
+def test_options_struct_matches_header():
+    # dk_options is 8 int32 fields: qk_path, waves_per_group, waves_per_cu, schedule,
+    # max_pages_per_seq, reserved[3]
+    assert ctypes.sizeof(dk_lib.DkOptions) == 32
+    names = [f[0] for f in dk_lib.DkOptions._fields_]
+    hdr = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = hdr[hdr.index("int32_t qk_path"):hdr.index("} dk_options;")]
+    declared = re.findall(r"int32_t (\w+)", body)
+    assert declared == names

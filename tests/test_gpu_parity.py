@@ -406,13 +406,36 @@ def test_schedules_agree_and_reuse_a_dirty_workspace(batch):
     want = _oracle(q, kv, indptr, ids, last)
     ws = torch.randint(0, 256, (dk_lib.workspace_bytes(batch, 32, 8, 128, 0),),
                        dtype=torch.uint8, device=DEV)
+    # plan hints: none, the true longest sequence, and one far too small (speed only)
+    hint = attention.plan_hint(indptr.cpu())
     outs = []
-    for sched, wpc in ((0, 0), (1, 1), (1, 8), (2, 0), (0, 0)):
-        _announce(f"schedule={sched} wpc={wpc} batch={batch}")
+    for sched, wpc, h in ((0, 0, 0), (1, 1, 0), (1, 8, 0), (2, 0, 0), (0, 0, hint), (0, 0, 1),
+                          (0, 16, hint), (0, 0, 0)):
+        _announce(f"schedule={sched} wpc={wpc} hint={h} batch={batch}")
         out = decode_attention(q, kv, indptr, ids, last, split_kv=0, workspace=ws,
-                               schedule=sched, waves_per_cu=wpc)
+                               schedule=sched, waves_per_cu=wpc, max_pages_per_seq=h)
         torch.cuda.synchronize()
-        _check(out, want, label=f"schedule={sched} wpc={wpc}")
+        _check(out, want, label=f"schedule={sched} wpc={wpc} hint={h}")
         outs.append(out.clone())
     for o in outs[1:]:
         assert torch.allclose(o.float(), outs[0].float(), atol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_plan_hint_one_pass_on_uniform_batch(dtype):
+    # uniform batch that fills the balanced grid: with the hint the automatic schedule is
+    # the one pass (no merge); results agree with the balanced schedule and the oracle
+    import dk_lib
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        32, 1000, 32, 8, 128, dtype=dtype, device=DEV, page_table="permuted", seed=21)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[dtype]
+    assert dk_lib.plan_schedule(32, 32, 8, 128, ids.shape[0], code, 0,
+                                dk_lib.options(max_pages_per_seq=hint)) == 1
+    assert dk_lib.plan_schedule(32, 32, 8, 128, ids.shape[0], code, 0) == 0
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=range(0, 32, 5))
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0)
+    torch.cuda.synchronize()
+    _check(a, want, rows=list(range(0, 32, 5)), label="hinted")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
