@@ -20,6 +20,7 @@ work whatever the sequence lengths; work runs on torch's current stream of q's d
 from __future__ import annotations
 
 import ctypes
+import math
 from types import SimpleNamespace
 from typing import Optional
 
@@ -37,34 +38,63 @@ def _fail(msg: str) -> None:
     raise DecodeArgumentError(msg)
 
 
-def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) -> None:
+def _kv_layout(kv_data):
+    """The paged cache in either FlashInfer NHD form: one tensor
+    (num_pages, 2, page_size, num_kv_heads, head_dim) with K at [:, 0] and V at [:, 1]
+    (src/layout.md:41-69), or a (k_cache, v_cache) pair of (num_pages, page_size,
+    num_kv_heads, head_dim) tensors with equal strides (SGLang's token pools)."""
+    if isinstance(kv_data, (tuple, list)):
+        if len(kv_data) != 2 or not all(isinstance(t, torch.Tensor) for t in kv_data):
+            raise TypeError("kv_data must be a tensor or a (k_cache, v_cache) pair of tensors")
+        k, v = kv_data
+        if k.dim() != 4 or v.shape != k.shape:
+            _fail("k_cache and v_cache must both be (num_pages, page_size, num_kv_heads, "
+                  f"head_dim); got {tuple(k.shape)} and {tuple(v.shape)}")
+        if v.stride() != k.stride() or v.dtype != k.dtype or v.device != k.device:
+            _fail("k_cache and v_cache must have the same strides, dtype and device")
+        return SimpleNamespace(k=k, v=v, num_pages=k.shape[0], page_size=k.shape[1],
+                               hkv=k.shape[2], d=k.shape[3], dtype=k.dtype, device=k.device,
+                               strides=(k.stride(0), 0, k.stride(1), k.stride(2)),
+                               d_stride=k.stride(3))
+    if not isinstance(kv_data, torch.Tensor):
+        raise TypeError(f"kv_data must be a torch.Tensor, got {type(kv_data).__name__}")
+    if kv_data.dim() != 5:
+        _fail("kv_data must be 5-D")
+    if kv_data.shape[1] != 2:
+        _fail("kv_data dim-1 must be 2 (K/V)")
+    return SimpleNamespace(k=kv_data, v=None, num_pages=kv_data.shape[0],
+                           page_size=kv_data.shape[2], hkv=kv_data.shape[3],
+                           d=kv_data.shape[4], dtype=kv_data.dtype, device=kv_data.device,
+                           strides=(kv_data.stride(0), kv_data.stride(1), kv_data.stride(2),
+                                    kv_data.stride(3)),
+                           d_stride=kv_data.stride(4))
+
+
+def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
     """Host-side checks: the reference's TORCH_CHECKs (attention_ext.cu:506-509,549-552)
-    plus the layout invariants that need no device read (src/layout.md:171-178)."""
-    for name, t in (("q", q), ("kv_data", kv_data), ("kv_indptr", kv_indptr),
+    plus the layout invariants that need no device read (src/layout.md:171-178).
+    Returns the cache layout."""
+    for name, t in (("q", q), ("kv_indptr", kv_indptr),
                     ("kv_indices", kv_indices), ("kv_last_page_len", kv_last_page_len)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    kv = _kv_layout(kv_data)
     if not q.is_cuda:
         _fail("q must be on CUDA")
     if q.dtype not in _DTYPE_CODE:
         _fail(f"q must be fp16 or bf16, got {q.dtype}")
     if q.dim() != 3:
         _fail(f"q must be 3-D (batch, num_q_heads, head_dim), got shape {tuple(q.shape)}")
-    if kv_data.dim() != 5:
-        _fail("kv_data must be 5-D")
-    if kv_data.shape[1] != 2:
-        _fail("kv_data dim-1 must be 2 (K/V)")
-    if kv_data.dtype != q.dtype:
-        _fail(f"kv_data dtype {kv_data.dtype} must match q dtype {q.dtype}")
-    if kv_data.shape[2] != PAGE_SIZE:
-        _fail(f"page_size must be 16 for the HIP kernel, got {kv_data.shape[2]}")
-    if q.shape[2] != kv_data.shape[4]:
-        _fail(f"head_dim mismatch: q has {q.shape[2]}, kv_data has {kv_data.shape[4]}")
+    if kv.dtype != q.dtype:
+        _fail(f"kv_data dtype {kv.dtype} must match q dtype {q.dtype}")
+    if kv.page_size != PAGE_SIZE:
+        _fail(f"page_size must be 16 for the HIP kernel, got {kv.page_size}")
+    if q.shape[2] != kv.d:
+        _fail(f"head_dim mismatch: q has {q.shape[2]}, kv_data has {kv.d}")
     if q.shape[2] not in SUPPORTED_HEAD_DIMS:
         _fail(f"head_dim must be 64, 128, or 256; got {q.shape[2]}")
-    if q.shape[1] % kv_data.shape[3] != 0:
-        _fail(f"num_q_heads ({q.shape[1]}) must be divisible by num_kv_heads "
-              f"({kv_data.shape[3]})")
+    if q.shape[1] % kv.hkv != 0:
+        _fail(f"num_q_heads ({q.shape[1]}) must be divisible by num_kv_heads ({kv.hkv})")
     for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
                     ("kv_last_page_len", kv_last_page_len)):
         if t.dtype != torch.int32:
@@ -73,15 +103,16 @@ def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) -> None:
             _fail(f"{name} must be 1-D")
         if t.device != q.device:
             _fail(f"{name} must be on {q.device}, got {t.device}")
-    if kv_data.device != q.device:
-        _fail(f"kv_data must be on {q.device}, got {kv_data.device}")
+    if kv.device != q.device:
+        _fail(f"kv_data must be on {q.device}, got {kv.device}")
     if q.shape[0] != kv_indptr.shape[0] - 1:
         _fail(f"q.shape[0] ({q.shape[0]}) must equal kv_indptr.shape[0] - 1 "
               f"({kv_indptr.shape[0] - 1})")
     if kv_last_page_len.shape[0] != q.shape[0]:
         _fail("kv_last_page_len must have one entry per sequence")
-    if q.stride(2) != 1 or kv_data.stride(4) != 1:
+    if q.stride(2) != 1 or kv.d_stride != 1:
         _fail("the head_dim stride of q and kv_data must be 1")
+    return kv
 
 
 def _contig1d(t: torch.Tensor) -> torch.Tensor:
@@ -91,8 +122,7 @@ def _contig1d(t: torch.Tensor) -> torch.Tensor:
 def _strides(q, kv_data, out) -> dk_lib.DkStrides:
     s = dk_lib.DkStrides()
     s.q_b, s.q_h = q.stride(0), q.stride(1)
-    s.kv_p, s.kv_r, s.kv_s, s.kv_h = (kv_data.stride(0), kv_data.stride(1), kv_data.stride(2),
-                                      kv_data.stride(3))
+    s.kv_p, s.kv_r, s.kv_s, s.kv_h = _kv_layout(kv_data).strides
     if out is not None:
         s.o_b, s.o_h = out.stride(0), out.stride(1)
     return s
@@ -125,7 +155,7 @@ def choose_split(q: torch.Tensor, kv_data: torch.Tensor, kv_indices: torch.Tenso
     """An explicit split count chosen from occupancy (for callers that want one)."""
     batch = q.shape[0]
     avg = kv_indices.shape[0] // batch if batch else 0
-    return dk_lib.choose_split(batch, q.shape[1], kv_data.shape[3], q.shape[2],
+    return dk_lib.choose_split(batch, q.shape[1], _kv_layout(kv_data).hkv, q.shape[2],
                                _DTYPE_CODE[q.dtype], avg, q.device.index or 0)
 
 
@@ -144,12 +174,15 @@ def decode_attention(
     waves_per_cu: int = 0,
     schedule: int = 0,
     max_pages_per_seq: int = 0,
+    sm_scale: Optional[float] = None,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
     Args:
         q                : (batch, num_q_heads, head_dim), fp16 or bf16, on a GPU
-        kv_data          : (num_pages, 2, 16, num_kv_heads, head_dim), q's dtype (NHD)
+        kv_data          : (num_pages, 2, 16, num_kv_heads, head_dim), q's dtype (NHD), or
+                           a (k_cache, v_cache) pair of (num_pages, 16, num_kv_heads,
+                           head_dim) tensors with equal strides
         kv_indptr        : (batch + 1,) int32 CSR row pointer into kv_indices
         kv_indices       : (kv_indptr[-1],) int32 physical page ids
         kv_last_page_len : (batch,) int32 valid tokens in each sequence's last page
@@ -165,11 +198,14 @@ def decode_attention(
                            split_kv 0) 1 = always balanced, 2 = always one pass)
         max_pages_per_seq: plan hint for split_kv 0 (see plan_hint): the longest
                            sequence's page count, 0 = unknown. Affects speed only.
+        sm_scale         : softmax scale; None = 1/sqrt(head_dim) as in the reference
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
     """
-    _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale == 0.0):
+        _fail(f"sm_scale must be finite and non-zero, got {sm_scale}")
     lib = dk_lib.load()
     split = resolve_split(split_kv)
     batch, hq, d = q.shape
@@ -183,7 +219,7 @@ def decode_attention(
     kv_indptr = _contig1d(kv_indptr)
     kv_indices = _contig1d(kv_indices)
     kv_last_page_len = _contig1d(kv_last_page_len)
-    ws_need = dk_lib.workspace_bytes(batch, hq, kv_data.shape[3], d, split)
+    ws_need = dk_lib.workspace_bytes(batch, hq, kv.hkv, d, split)
     if ws_need:
         if workspace is None:
             workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
@@ -193,14 +229,20 @@ def decode_attention(
     ws_ptr = workspace.data_ptr() if ws_need else None
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
-    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq)
+    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
+                          sm_scale or 0.0)
+    shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
+             _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts))
+    tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+              out.data_ptr(), ws_ptr, ws_bytes)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = lib.dk_decode_attention_ex(
-            q.data_ptr(), kv_data.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
-            kv_last_page_len.data_ptr(), out.data_ptr(), ws_ptr, ws_bytes, batch, hq,
-            kv_data.shape[3], d, kv_data.shape[2], kv_data.shape[0], kv_indices.shape[0],
-            _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts), stream)
+        if kv.v is None:
+            rc = lib.dk_decode_attention_ex(q.data_ptr(), kv.k.data_ptr(), *tables, *shape,
+                                            stream)
+        else:
+            rc = lib.dk_decode_attention_kv(q.data_ptr(), kv.k.data_ptr(), kv.v.data_ptr(),
+                                            *tables, *shape, stream)
     dk_lib.check(rc, "decode_attention")
     return out
 
@@ -211,7 +253,8 @@ def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_k
     fp32, with the semantics of the reference partition kernel
     (src/cuda_/attention_ext.cu:207-349): m is the split's max of q.k*scale (-1e9 when the
     split is empty), l = sum exp(score - m), O = sum exp(score - m) * V (unnormalised)."""
-    _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    if _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len).v is not None:
+        _fail("decode_partials takes the combined (num_pages, 2, 16, Hkv, D) cache")
     lib = dk_lib.load()
     split = choose_split(q, kv_data, kv_indices) if split_kv in (None, 0) else \
         resolve_split(split_kv)

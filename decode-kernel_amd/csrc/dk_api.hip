@@ -145,7 +145,9 @@ int run(Problem p, bool do_merge, void* stream) {
   a.kv_p = p.st.kv_p * esize;
   a.o_b = p.st.o_b * esize;
   a.o_h = p.st.o_h * esize;
-  a.kv_r = (int32_t)(p.st.kv_r * esize);
+  // V slice of a page: kv_r further in the combined cache, or the same offset in the
+  // separate V cache
+  a.kv_v = p.v ? (int64_t)((const uint8_t*)p.v - (const uint8_t*)p.kv) : p.st.kv_r * esize;
   a.kv_s = (int32_t)(p.st.kv_s * esize);
   a.kv_h = (int32_t)(p.st.kv_h * esize);
   a.batch = p.batch;
@@ -156,10 +158,10 @@ int run(Problem p, bool do_merge, void* stream) {
   a.split = std::max(p.split, 1);
   a.num_indices = (int32_t)p.num_indices;
   a.num_pages = (uint32_t)std::min<int64_t>(p.num_pages, (int64_t)1 << 31);
-  // bytes from a kv head's slice base that its K and V rows reach (validated < 2^31)
-  a.page_extent = (uint32_t)((p.st.kv_r + (int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * esize);
+  // bytes from a kv head's K (or V) slice base that its rows reach (validated < 2^31)
+  a.page_extent = (uint32_t)(((int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * esize);
   a.direct = direct ? 1 : 0;
-  a.kscale = kLog2e / sqrtf((float)p.head_dim);
+  a.kscale = kLog2e * (p.opt.sm_scale != 0.f ? p.opt.sm_scale : 1.f / sqrtf((float)p.head_dim));
   // every launch that can store partials has them (or the library is inconsistent)
   if ((pl.balanced || !direct) && (!a.part_o || !a.part_m || !a.part_l))
     return set_error(DK_EWORKSPACE, "internal: partials not assigned for this schedule");
@@ -203,7 +205,7 @@ int run(Problem p, bool do_merge, void* stream) {
 // ---------------------------------------------------------------- C ABI
 using dk::Problem;
 
-static Problem make_problem(const void* q, const void* kv, const int32_t* indptr,
+static Problem make_problem(const void* q, const void* kv, const void* v, const int32_t* indptr,
                             const int32_t* indices, const int32_t* last_len, void* out,
                             void* ws, size_t ws_bytes, int32_t batch, int32_t hq, int32_t hkv,
                             int32_t d, int32_t page, int64_t num_pages, int64_t num_indices,
@@ -212,6 +214,7 @@ static Problem make_problem(const void* q, const void* kv, const int32_t* indptr
   Problem p;
   p.q = q;
   p.kv = kv;
+  p.v = v;
   p.indptr = indptr;
   p.indices = indices;
   p.last_len = last_len;
@@ -309,10 +312,30 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
                            const dk_options* opts, void* hip_stream) {
   dk::clear_error();
   if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
-  Problem p = make_problem(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out, workspace,
+  Problem p = make_problem(q, kv_data, nullptr, kv_indptr, kv_indices, kv_last_page_len, out,
+                           workspace,
                            workspace_bytes, batch, num_q_heads, num_kv_heads, head_dim,
                            page_size, num_pages, num_indices, dtype, strides, split_kv, opts,
                            true);
+  return dk::run(p, true, hip_stream);
+}
+
+int dk_decode_attention_kv(const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* kv_indptr, const int32_t* kv_indices,
+                           const int32_t* kv_last_page_len, void* out, void* workspace,
+                           size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                           int64_t num_pages, int64_t num_indices, int32_t dtype,
+                           const dk_strides* strides, int32_t split_kv, const dk_options* opts,
+                           void* hip_stream) {
+  dk::clear_error();
+  if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
+  if (batch > 0 && (!k_cache || !v_cache))
+    return dk::set_error(DK_ENULL, "k_cache and v_cache must be non-NULL");
+  Problem p = make_problem(q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, out,
+                           workspace, workspace_bytes, batch, num_q_heads, num_kv_heads,
+                           head_dim, page_size, num_pages, num_indices, dtype, strides, split_kv,
+                           opts, true);
   return dk::run(p, true, hip_stream);
 }
 
@@ -338,7 +361,7 @@ int dk_decode_partials(const void* q, const void* kv_data, const int32_t* kv_ind
                        void* hip_stream) {
   dk::clear_error();
   if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
-  Problem p = make_problem(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, nullptr,
+  Problem p = make_problem(q, kv_data, nullptr, kv_indptr, kv_indices, kv_last_page_len, nullptr,
                            workspace, workspace_bytes, batch, num_q_heads, num_kv_heads,
                            head_dim, page_size, num_pages, num_indices, dtype, strides,
                            split_kv, opts, false);

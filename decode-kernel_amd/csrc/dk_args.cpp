@@ -11,6 +11,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <cmath>
+
 #include <algorithm>
 #include <string>
 
@@ -136,6 +138,8 @@ int validate(const Problem& p) {
   if (o.max_pages_per_seq < 0)
     return set_error(DK_EINVAL, "options.max_pages_per_seq must be >= 0; got %d",
                      o.max_pages_per_seq);
+  if (!std::isfinite(o.sm_scale))
+    return set_error(DK_EINVAL, "options.sm_scale must be finite (0 = 1/sqrt(head_dim))");
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything
@@ -149,22 +153,25 @@ int validate(const Problem& p) {
   // Strides: non-negative, and every 16-byte vector access aligned. Row loads of K/V are
   // up to 16 bytes wide (8 elements), so page/row/head strides and the base must be
   // multiples of 8 elements; q rows are loaded the same way.
+  // With a separate V cache the K->V stride kv_r is unused.
   const dk_strides& s = p.st;
-  const int64_t all[] = {s.q_b, s.q_h, s.kv_p, s.kv_r, s.kv_s, s.kv_h, s.o_b, s.o_h};
+  const int64_t kv_r = p.v ? 0 : s.kv_r;
+  const int64_t all[] = {s.q_b, s.q_h, s.kv_p, kv_r, s.kv_s, s.kv_h, s.o_b, s.o_h};
   for (int64_t v : all)
     if (v < 0) return set_error(DK_EINVAL, "strides must be non-negative");
   const int64_t esize = 2;
   auto aligned16 = [](int64_t elems) { return (elems * 2) % 16 == 0; };
-  if (!aligned16(s.q_b) || !aligned16(s.q_h) || !aligned16(s.kv_p) || !aligned16(s.kv_r) ||
+  if (!aligned16(s.q_b) || !aligned16(s.q_h) || !aligned16(s.kv_p) || !aligned16(kv_r) ||
       !aligned16(s.kv_s) || !aligned16(s.kv_h))
     return set_error(DK_EUNSUPPORTED,
                      "q and kv_data strides must be multiples of 8 elements (16-byte rows); "
                      "pass contiguous tensors");
-  if (((uintptr_t)p.q % 16) != 0 || ((uintptr_t)p.kv % 16) != 0)
-    return set_error(DK_EUNSUPPORTED, "q and kv_data must be 16-byte aligned");
-  // Offsets inside one page are carried in 32 bits.
-  const int64_t in_page = (s.kv_r + (int64_t)(kPageSize - 1) * s.kv_s +
-                           (int64_t)(p.hkv - 1) * s.kv_h + p.head_dim) * esize;
+  if (((uintptr_t)p.q % 16) != 0 || ((uintptr_t)p.kv % 16) != 0 ||
+      ((uintptr_t)p.v % 16) != 0)
+    return set_error(DK_EUNSUPPORTED, "q and the K/V caches must be 16-byte aligned");
+  // Offsets inside one page slice (all kv heads' rows of K, or of V) are 32-bit.
+  const int64_t in_page = ((int64_t)(kPageSize - 1) * s.kv_s + (int64_t)(p.hkv - 1) * s.kv_h +
+                           p.head_dim) * esize;
   if (in_page >= ((int64_t)1 << 31))
     return set_error(DK_EUNSUPPORTED, "kv_data page extent exceeds 2 GiB");
 

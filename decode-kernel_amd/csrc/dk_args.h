@@ -18,7 +18,8 @@ constexpr int kDefaultWavesPerGroup = 2;
 // Everything a launch needs that is known on the host.
 struct Problem {
   const void* q = nullptr;
-  const void* kv = nullptr;
+  const void* kv = nullptr;      // K cache (or the combined NHD cache)
+  const void* v = nullptr;       // separate V cache (same strides as K), or null
   const int32_t* indptr = nullptr;
   const int32_t* indices = nullptr;
   const int32_t* last_len = nullptr;

@@ -70,11 +70,13 @@ struct Pass1Args {
   float* part_l;
   uint8_t* out;
   int64_t q_b, q_h, kv_p, o_b, o_h;   // bytes
-  int32_t kv_r, kv_s, kv_h;           // bytes
+  int64_t kv_v;                       // bytes from a K page slice to the V slice of the
+                                      // same page (in-page offset, or V cache - K cache)
+  int32_t kv_s, kv_h;                 // bytes
   int32_t batch, hq, hkv, group, chunks, split;
   int32_t num_indices;
   uint32_t num_pages;                 // clamp bound for page ids (min(num_pages, 2^31))
-  uint32_t page_extent;               // bytes of a page a kv head's loads may touch (< 2^31)
+  uint32_t page_extent;               // bytes one kv head's K (or V) rows of a page span (< 2^31)
   int32_t direct;                     // explicit split 1 / balanced: may write the
                                       // normalised output (0: partials only)
   float kscale;                       // log2(e) / sqrt(head_dim)
@@ -283,6 +285,7 @@ struct Wave {
 
   int r16, c;
   u32 koff, voff, tok_s, extent;
+  int64_t kv_v;
   float kscale;
   u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, dims 32i+8r16..
   u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
@@ -295,8 +298,9 @@ struct Wave {
     c = lane & 15;
     tok_s = (u32)a.kv_s;
     koff = MFMA ? (u32)(c * a.kv_s + 16 * r16) : (u32)(4 * r16 * a.kv_s + 2 * DPL * c);
-    voff = (u32)(a.kv_r + 4 * r16 * a.kv_s + 2 * DPL * c);
+    voff = (u32)(4 * r16 * a.kv_s + 2 * DPL * c);
     extent = a.page_extent;
+    kv_v = a.kv_v;
     kscale = a.kscale;
   }
 
@@ -331,16 +335,17 @@ struct Wave {
   // pg: base of this kv head's slice of a page (page base + kvh * kv_h). Buffer loads:
   // the address is the page base (scalar) + a per-lane offset + a per-row scalar offset.
   __device__ __forceinline__ void load_page(u32 (&kb)[KW], u32 (&vb)[VW], const uint8_t* pg) const {
-    const __amdgpu_buffer_rsrc_t rs = page_rsrc(pg, extent);
+    const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, extent);
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(pg + kv_v, extent);
     if constexpr (MFMA) {
 #pragma unroll
-      for (int i = 0; i < NMF; ++i) ld_buf<4>(&kb[4 * i], rs, koff, 64 * i);
+      for (int i = 0; i < NMF; ++i) ld_buf<4>(&kb[4 * i], rk, koff, 64 * i);
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ld_buf<VWT>(&kb[r * VWT], rs, koff, r * tok_s);
+      for (int r = 0; r < 4; ++r) ld_buf<VWT>(&kb[r * VWT], rk, koff, r * tok_s);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ld_buf<VWT>(&vb[r * VWT], rs, voff, r * tok_s);
+    for (int r = 0; r < 4; ++r) ld_buf<VWT>(&vb[r * VWT], rv, voff, r * tok_s);
   }
 
   // Scores of tokens 4*r16 + r for head ss*GQ + c%GQ from per-lane partials of the G

@@ -47,7 +47,8 @@ class DkStrides(ctypes.Structure):
 class DkOptions(ctypes.Structure):
     _fields_ = [("qk_path", ctypes.c_int32), ("waves_per_group", ctypes.c_int32),
                 ("waves_per_cu", ctypes.c_int32), ("schedule", ctypes.c_int32),
-                ("max_pages_per_seq", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3)]
+                ("max_pages_per_seq", ctypes.c_int32), ("sm_scale", ctypes.c_float),
+                ("reserved", ctypes.c_int32 * 2)]
 
 
 _P = ctypes.c_void_p
@@ -73,6 +74,11 @@ SIGNATURES = {
                                               _I32, _I32, _I32, _I64, _I64, _I32,
                                               ctypes.POINTER(DkStrides), _I32,
                                               ctypes.POINTER(DkOptions), _P]),
+    "dk_decode_attention_kv": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I32, _I32,
+                                              _I32, _I32, _I32, _I64, _I64, _I32,
+                                              ctypes.POINTER(DkStrides), _I32,
+                                              ctypes.POINTER(DkOptions), _P]),
+    "dk_build_page_table": (ctypes.c_int, [_P, _I64, _P, _P, _I32, _I32, _P, _P, _I64, _P, _P]),
     "dk_decode_partials": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _I32, _I32, _I32, _I32,
                                           _I32, _I64, _I64, _I32, ctypes.POINTER(DkStrides),
                                           _I32, ctypes.POINTER(DkOptions), _P]),
@@ -156,8 +162,10 @@ SCHEDULE_ONE_PASS = 2
 
 
 def options(qk_path: int = 0, waves_per_group: int = 0, waves_per_cu: int = 0,
-            schedule: int = SCHEDULE_AUTO, max_pages_per_seq: int = 0) -> DkOptions:
+            schedule: int = SCHEDULE_AUTO, max_pages_per_seq: int = 0,
+            sm_scale: float = 0.0) -> DkOptions:
     o = DkOptions()
+    o.sm_scale = sm_scale
     o.qk_path = qk_path
     o.waves_per_group = waves_per_group
     o.waves_per_cu = waves_per_cu

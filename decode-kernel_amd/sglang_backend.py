@@ -1,0 +1,226 @@
+"""SGLang attention backend on the MI355X split-KV decode kernel.
+
+Counterpart of the reference adapter (integration/sglang_backend.py:50-137): decode steps
+go to the HIP kernel through `decode_attention`; prefill (extend) stays outside this path.
+Two entry styles are provided:
+
+* SGLang's backend API — `init_forward_metadata(forward_batch)` once per batch, then
+  `forward_decode(q, k, v, layer, forward_batch, save_kv_cache=True)` per layer — reading
+  the token pool SGLang owns: per-layer K and V buffers of shape (slots, kv_heads,
+  head_dim) with 16-token pages (server `page_size=16`), the request-to-token map and the
+  batch's sequence lengths. The page table is built on the device once per batch
+  (paging.build_page_table) and shared by every layer; the pool is read in place as a
+  (k_cache, v_cache) pair of (pages, 16, kv_heads, head_dim) views.
+* The reference shim's `forward(q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+  is_prefill=False)` (integration/sglang_backend.py:85-101), for callers that already
+  hold FlashInfer page tables.
+
+Registration mirrors the reference (:112-137): `register_backend()` or the environment
+variable SGLANG_ATTENTION_BACKEND=split_kv_hip. SGLang is imported lazily; without it the
+class derives from a stub so that the module imports (and is tested) anywhere.
+"""
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+import attention
+import paging
+from attention import decode_attention
+
+BACKEND_NAME = "split_kv_hip"
+PAGE_SIZE = 16
+# split_kv for decode: 0 = automatic (balanced / one pass, chosen per batch); the
+# reference's SPLIT_KV variable (integration/sglang_backend.py:32) is honoured.
+DEFAULT_SPLIT_KV = int(os.environ.get("SPLIT_KV", "0"))
+
+
+def _import_sglang_base():
+    try:
+        from sglang.srt.layers.attention.base_attn_backend import AttentionBackend
+        return AttentionBackend
+    except ImportError:
+        pass
+    try:
+        from sglang.srt.layers.attention import AttentionBackend
+        return AttentionBackend
+    except ImportError:
+        class AttentionBackend:  # stand-in when SGLang is not installed
+            def forward(self, *a, **kw):
+                raise NotImplementedError
+        return AttentionBackend
+
+
+@dataclass
+class DecodeMetadata:
+    """Per-batch state shared by every layer's decode call."""
+    kv_indptr: torch.Tensor
+    kv_indices: torch.Tensor
+    kv_last_page_len: torch.Tensor
+    max_pages_per_seq: int          # plan hint (0 = unknown)
+
+
+class SplitKVHipBackend(_import_sglang_base()):
+    """Decode attention on the HIP split-KV kernel; prefill on PyTorch SDPA."""
+
+    def __init__(self, model_runner=None, split_kv: Optional[int] = None):
+        self.model_runner = model_runner
+        self.split_kv = DEFAULT_SPLIT_KV if split_kv is None else split_kv
+        self.forward_metadata: Optional[DecodeMetadata] = None
+        self._workspace: Optional[torch.Tensor] = None
+
+    @classmethod
+    def name(cls) -> str:
+        return BACKEND_NAME
+
+    # ---------------------------------------------------------------- SGLang API
+    def init_forward_metadata(self, forward_batch) -> None:
+        """Build the batch's page table on the device (no host sync)."""
+        req_to_token = forward_batch.req_to_token_pool.req_to_token
+        seq_lens = forward_batch.seq_lens
+        batch = int(seq_lens.shape[0])
+        seq_lens_sum = getattr(forward_batch, "seq_lens_sum", None)
+        lens_cpu = getattr(forward_batch, "seq_lens_cpu", None)
+        if seq_lens_sum is None:
+            # last resort: one device read (SGLang always provides seq_lens_sum)
+            seq_lens_sum = int(seq_lens.sum().item())
+        indptr, indices, last = paging.build_page_table(
+            req_to_token, forward_batch.req_pool_indices, seq_lens,
+            capacity=paging.page_capacity(seq_lens_sum, batch))
+        hint = 0
+        if lens_cpu is not None and batch:
+            hint = (int(torch.as_tensor(lens_cpu).max()) + PAGE_SIZE - 1) // PAGE_SIZE
+        self.forward_metadata = DecodeMetadata(indptr, indices, last, hint)
+
+    def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
+        """One layer's decode attention; returns (batch, q_heads * head_dim)."""
+        if getattr(layer, "logit_cap", 0) not in (0, 0.0, None):
+            raise NotImplementedError("logit soft-capping is not supported by this kernel")
+        pool = forward_batch.token_to_kv_pool
+        if k is not None and save_kv_cache:
+            pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
+        md = self.forward_metadata
+        if md is None:
+            raise RuntimeError("init_forward_metadata must run before forward_decode")
+        hq, d = layer.tp_q_head_num, layer.head_dim
+        kc, vc = self._paged_views(pool, layer.layer_id)
+        qv = q.reshape(-1, hq, d)
+        out = decode_attention(
+            qv, (kc, vc), md.kv_indptr, md.kv_indices, md.kv_last_page_len,
+            split_kv=self.split_kv, workspace=self._workspace_for(qv, kc.shape[2]),
+            max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d))
+        return out.view(-1, hq * d)
+
+    def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
+        """Prefill / extend: causal attention of the new tokens over each request's cached
+        prefix and themselves, with PyTorch SDPA per request (outside the decode path)."""
+        pool = forward_batch.token_to_kv_pool
+        if k is not None and save_kv_cache:
+            pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
+        hq, hkv, d = layer.tp_q_head_num, layer.tp_k_head_num, layer.head_dim
+        kb, vb = pool.get_key_buffer(layer.layer_id), pool.get_value_buffer(layer.layer_id)
+        req_to_token = forward_batch.req_to_token_pool.req_to_token
+        qv = q.reshape(-1, hq, d)
+        out = torch.empty_like(qv)
+        ext = forward_batch.extend_seq_lens_cpu
+        lens = forward_batch.seq_lens_cpu
+        rows = forward_batch.req_pool_indices.tolist()
+        start = 0
+        for row, n_new, n_all in zip(rows, list(ext), list(lens)):
+            n_new, n_all = int(n_new), int(n_all)
+            slots = req_to_token[row, :n_all].long()
+            kk = kb[slots].float().transpose(0, 1)           # (hkv, n_all, d)
+            vv = vb[slots].float().transpose(0, 1)
+            qq = qv[start:start + n_new].float().transpose(0, 1)   # (hq, n_new, d)
+            g = hq // hkv
+            kk = kk.repeat_interleave(g, dim=0)
+            vv = vv.repeat_interleave(g, dim=0)
+            # new token i sits at position n_all - n_new + i and sees positions <= it
+            pos_q = torch.arange(n_all - n_new, n_all, device=q.device)[:, None]
+            mask = torch.arange(n_all, device=q.device)[None, :] <= pos_q
+            o = torch.nn.functional.scaled_dot_product_attention(
+                qq, kk, vv, attn_mask=mask, scale=_scale(layer, d) or 1.0 / math.sqrt(d))
+            out[start:start + n_new] = o.transpose(0, 1).to(out.dtype)
+            start += n_new
+        return out.view(-1, hq * d)
+
+    def forward_sglang(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
+        """SGLang's dispatch by forward mode."""
+        if forward_batch.forward_mode.is_decode():
+            return self.forward_decode(q, k, v, layer, forward_batch, save_kv_cache)
+        return self.forward_extend(q, k, v, layer, forward_batch, save_kv_cache)
+
+    # ---------------------------------------------------------------- reference shim API
+    def forward(self, q, kv_data=None, kv_indptr=None, kv_indices=None, kv_last_page_len=None,
+                is_prefill: bool = False, **kwargs):
+        """The reference adapter's entry (integration/sglang_backend.py:85-101): page
+        tables given by the caller; decode runs the HIP kernel. Called with SGLang's
+        (q, k, v, layer, forward_batch) it dispatches like SGLang's own backends."""
+        fb = kwargs.pop("forward_batch", None)
+        if fb is None and hasattr(kv_last_page_len, "forward_mode"):
+            fb = kv_last_page_len
+        if fb is not None:
+            # SGLang's signature: forward(q, k, v, layer, forward_batch, save_kv_cache=True)
+            layer = kwargs.pop("layer", kv_indices)
+            k = kwargs.pop("k", kv_data)
+            v = kwargs.pop("v", kv_indptr)
+            return self.forward_sglang(q, k, v, layer, fb, kwargs.pop("save_kv_cache", True))
+        if is_prefill:
+            raise NotImplementedError(
+                "prefill is not on the decode path; use forward_extend with SGLang's batch")
+        return decode_attention(q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
+                                split_kv=self.split_kv)
+
+    # ---------------------------------------------------------------- helpers
+    @staticmethod
+    def _paged_views(pool, layer_id):
+        kb, vb = pool.get_key_buffer(layer_id), pool.get_value_buffer(layer_id)
+        pages = kb.shape[0] // PAGE_SIZE
+        shape = (pages, PAGE_SIZE) + tuple(kb.shape[1:])
+        return kb[:pages * PAGE_SIZE].view(shape), vb[:pages * PAGE_SIZE].view(shape)
+
+    def _workspace_for(self, q, hkv):
+        need = attention.dk_lib.workspace_bytes(q.shape[0], q.shape[1], hkv, q.shape[2],
+                                                attention.resolve_split(self.split_kv))
+        if need == 0:
+            return None
+        ws = self._workspace
+        if ws is None or ws.numel() < need or ws.device != q.device:
+            ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        return ws
+
+
+def _scale(layer, d) -> Optional[float]:
+    s = getattr(layer, "scaling", None)
+    if s is None or abs(s * math.sqrt(d) - 1.0) < 1e-7:
+        return None
+    return float(s)
+
+
+def register_backend() -> bool:
+    """Register with SGLang's backend registry (reference :112-137). Returns success."""
+    try:
+        from sglang.srt.layers.attention import register_attention_backend
+        register_attention_backend(BACKEND_NAME, SplitKVHipBackend)
+        print(f"[{BACKEND_NAME}] Backend registered with SGLang.")
+        return True
+    except ImportError:
+        print(f"[{BACKEND_NAME}] WARNING: sglang not installed; backend registration skipped.")
+        return False
+    except AttributeError:
+        try:
+            import sglang.srt.layers.attention as attn_mod
+            attn_mod._BACKEND_REGISTRY[BACKEND_NAME] = SplitKVHipBackend
+            print(f"[{BACKEND_NAME}] Backend injected into registry (legacy path).")
+            return True
+        except Exception as e:  # noqa: BLE001 - report and carry on, as the reference does
+            print(f"[{BACKEND_NAME}] Registration failed: {e}")
+            return False
+
+
+if os.environ.get("SGLANG_ATTENTION_BACKEND") == BACKEND_NAME:
+    register_backend()

@@ -76,7 +76,9 @@ typedef struct {
                               the automatic schedule runs one pass when that is as short
                               as the balanced one; without it, it always balances.
                               Too small a value affects speed only, never results.       */
-  int32_t reserved[3];     /* must be 0                                                     */
+  float sm_scale;          /* softmax scale applied to q.k; 0 = 1/sqrt(head_dim), the
+                              reference's fixed scale (attention_ext.cu:79-80)             */
+  int32_t reserved[2];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */
@@ -153,6 +155,36 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
                            int32_t head_dim, int32_t page_size, int64_t num_pages,
                            int64_t num_indices, int32_t dtype, const dk_strides* strides,
                            int32_t split_kv, const dk_options* opts, void* hip_stream);
+
+/* dk_decode_attention_ex over separate K and V caches, each
+ * (num_pages, page_size, num_kv_heads, head_dim) with the same strides (kv_p, kv_s, kv_h;
+ * kv_r is ignored): the `(k_cache, v_cache)` form of FlashInfer's paged KV cache that
+ * SGLang's token pools hand to attention backends (the pool the reference adapter
+ * integration/sglang_backend.py:85-101 forwards). Both caches hold num_pages pages. */
+int dk_decode_attention_kv(const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* kv_indptr, const int32_t* kv_indices,
+                           const int32_t* kv_last_page_len, void* out, void* workspace,
+                           size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                           int64_t num_pages, int64_t num_indices, int32_t dtype,
+                           const dk_strides* strides, int32_t split_kv, const dk_options* opts,
+                           void* hip_stream);
+
+/* CSR page table (kv_indptr, kv_indices, kv_last_page_len as in src/layout.md:27-138) of
+ * `batch` requests from a token-slot map: request b is row req_pool_indices[b] of
+ * req_to_token (rows req_stride int32 apart), holding seq_lens[b] tokens whose cache slot
+ * is 16 * page + position % 16, so page p of the request is req_to_token[row][16 p] / 16.
+ * This is the map SGLang's ReqToTokenPool keeps and its attention backends turn into
+ * FlashInfer page tables; the reference adapter (integration/sglang_backend.py:85-101)
+ * expects the caller to have built them. Writes batch + 1 indptr entries, batch last-page
+ * lengths (0 for an empty request) and min(total pages, capacity) indices; size
+ * kv_indices for sum(ceil(seq_lens / 16)) (at most (sum(seq_lens) + 15 * batch) / 16).
+ * Device pointers; enqueued on hip_stream. No counterpart in the reference. */
+int dk_build_page_table(const int32_t* req_to_token, int64_t req_stride,
+                        const int32_t* req_pool_indices, const int32_t* seq_lens,
+                        int32_t batch, int32_t page_size, int32_t* kv_indptr,
+                        int32_t* kv_indices, int64_t capacity, int32_t* kv_last_page_len,
+                        void* hip_stream);
 
 /* Pass 1 only: writes partial_O / partial_m / partial_l for split_kv >= 1 splits into
  * the workspace (layout from dk_partials_layout; partial_m is the split's max of

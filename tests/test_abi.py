@@ -211,11 +211,15 @@ def test_plan_hint_reads_host_indptr_only():
 
 
 def test_options_struct_matches_header():
-    # dk_options is 8 int32 fields: qk_path, waves_per_group, waves_per_cu, schedule,
-    # max_pages_per_seq, reserved[3]
+    # dk_options: qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq
+    # (int32), sm_scale (float), reserved[2] (int32): 32 bytes
     assert ctypes.sizeof(dk_lib.DkOptions) == 32
-    names = [f[0] for f in dk_lib.DkOptions._fields_]
+    fields = [(f[0], f[1]) for f in dk_lib.DkOptions._fields_]
     hdr = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     body = hdr[hdr.index("int32_t qk_path"):hdr.index("} dk_options;")]
-    declared = re.findall(r"int32_t (\w+)", body)
-    assert declared == names
+    declared = re.findall(r"(int32_t|float) (\w+)", body)
+    ctype = {"int32_t": ctypes.c_int32, "float": ctypes.c_float}
+    assert [n for _, n in declared] == [n for n, _ in fields]
+    for (ty, n), (_, cty) in zip(declared, fields):
+        base = cty._type_ if issubclass(cty, ctypes.Array) else cty
+        assert base is ctype[ty], n

@@ -249,3 +249,64 @@ def test_planted_last_page_mistake_is_caught_by_golden():
     bad = ref.reference_attention_paged(z["q_f32"], z["kv_f32"], z["kv_indptr"],
                                         z["kv_indices"], full)
     assert np.abs(bad - z["out"]).max() > 1e-2
+
+
+# ---------------------------------------------------------------- page table from a slot map
+
+from oracle import page_table as ptab  # noqa: E402
+
+
+def _slot_map(lens, rows, seed, pool_pages=None):
+    """req_to_token filled by a 16-token-page allocator over a shuffled free list."""
+    rng = np.random.default_rng(seed)
+    need = sum(-(-n // 16) for n in lens)
+    perm = list(rng.permutation(pool_pages or need + 5))
+    r2t = np.full((max(rows) + 1, max(lens + [1]) + 16), -1, np.int64)
+    for r, n in zip(rows, lens):
+        for p in range(-(-n // 16)):
+            page = int(perm.pop())
+            for t in range(p * 16, min(n, p * 16 + 16)):
+                r2t[r, t] = page * 16 + t % 16
+    return r2t
+
+
+def test_page_table_known_answer():
+    # hand-built: request in row 1 has 20 tokens on pages 7 then 3; row 0 has 16 tokens on
+    # page 5; row 2 is empty
+    r2t = np.zeros((3, 40), np.int64)
+    r2t[1, :16] = 7 * 16 + np.arange(16)
+    r2t[1, 16:20] = 3 * 16 + np.arange(4)
+    r2t[0, :16] = 5 * 16 + np.arange(16)
+    indptr, indices, last = ptab.build_page_table(r2t, [1, 0, 2], [20, 16, 0])
+    assert indptr.tolist() == [0, 2, 3, 3]
+    assert indices.tolist() == [7, 3, 5]
+    assert last.tolist() == [4, 16, 0]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_page_table_round_trip_reproduces_token_slots(seed):
+    # the page table must describe exactly the slots the map holds, token by token, and
+    # satisfy the layout invariants (src/layout.md:171-178)
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.integers(0, 80, size=9)]
+    rows = [int(x) for x in rng.permutation(12)[:9]]
+    r2t = _slot_map(lens, rows, seed)
+    indptr, indices, last = ptab.build_page_table(r2t, rows, lens)
+    assert indptr[0] == 0 and indptr[-1] == len(indices)
+    for b, (r, n) in enumerate(zip(rows, lens)):
+        np.testing.assert_array_equal(ptab.token_slots(indptr, indices, last, b), r2t[r, :n])
+        assert (last[b] == 0) == (n == 0) and 0 <= last[b] <= 16
+
+
+def test_planted_page_table_mistake_is_caught_by_round_trip():
+    # a last-page length off by one (n % 16 instead of the 1..16 range) breaks the round
+    # trip for lengths that are multiples of 16
+    lens, rows = [32, 5], [0, 1]
+    r2t = _slot_map(lens, rows, 3)
+    indptr, indices, last = ptab.build_page_table(r2t, rows, lens)
+    bad_last = np.array([n % 16 for n in lens], np.int32)
+    ok = all(np.array_equal(ptab.token_slots(indptr, indices, last, b), r2t[r, :n])
+             for b, (r, n) in enumerate(zip(rows, lens)))
+    bad = all(np.array_equal(ptab.token_slots(indptr, indices, bad_last, b), r2t[r, :n])
+              for b, (r, n) in enumerate(zip(rows, lens)))
+    assert ok and not bad

@@ -1,0 +1,180 @@
+"""The SGLang backend adapter, the device page-table builder and the (k_cache, v_cache)
+and sm_scale paths it uses.
+
+CPU tests: the adapter imports and registers without SGLang (as the reference's does,
+integration/sglang_backend.py:37-47,112-137). GPU tests: a decode step through the
+adapter on an SGLang-shaped token pool against the oracle, the page table against
+oracle/page_table.py (bit-exact), split caches and custom scales against the oracle.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import attention
+import layout
+import paging
+import sglang_backend
+from helpers import err_stats, to_np
+from oracle import page_table as ptab
+from oracle import reference as ref
+from sglang_fakes import make_batch
+
+DEV = "cuda"
+
+
+# ---------------------------------------------------------------- CPU
+
+def test_backend_imports_and_names_without_sglang():
+    b = sglang_backend.SplitKVHipBackend(split_kv=4)
+    assert b.name() == "split_kv_hip" and b.split_kv == 4
+    assert sglang_backend.SplitKVHipBackend().split_kv == sglang_backend.DEFAULT_SPLIT_KV
+
+
+def test_register_backend_reports_missing_sglang(capsys):
+    assert sglang_backend.register_backend() is False
+    assert "sglang not installed" in capsys.readouterr().out
+
+
+def test_page_capacity_bounds_the_page_count():
+    rng = np.random.default_rng(0)
+    for _ in range(100):
+        lens = rng.integers(0, 300, size=rng.integers(1, 20))
+        pages = sum(-(-int(n) // 16) for n in lens)
+        assert pages <= paging.page_capacity(int(lens.sum()), len(lens))
+
+
+def test_decode_without_metadata_is_an_error():
+    fb = type("FB", (), {"token_to_kv_pool": None, "out_cache_loc": None})()
+    layer = type("L", (), {"logit_cap": 0.0})()
+    with pytest.raises(RuntimeError, match="init_forward_metadata"):
+        sglang_backend.SplitKVHipBackend().forward_decode(None, None, None, layer, fb)
+
+
+# ---------------------------------------------------------------- GPU
+
+def _pool_as_combined(pool, layer_id):
+    """(pages, 2, 16, Hkv, D) numpy copy of one layer's pool, the reference layout."""
+    kb, vb = pool.get_key_buffer(layer_id), pool.get_value_buffer(layer_id)
+    pages = kb.shape[0] // 16
+    k = to_np(kb[:pages * 16].reshape(pages, 16, *kb.shape[1:]))
+    v = to_np(vb[:pages * 16].reshape(pages, 16, *vb.shape[1:]))
+    return np.stack([k, v], axis=1)
+
+
+def _want(q, pool, layer_id, r2t, rows, lens, scale_mult=1.0):
+    indptr, indices, last = ptab.build_page_table(r2t, rows, lens)
+    qn = to_np(q) * np.float32(scale_mult)
+    return ref.reference_attention_paged(qn, _pool_as_combined(pool, layer_id), indptr,
+                                         indices, last)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens", [[1, 17, 300, 16, 1000, 33], [2048] * 12, [5]])
+def test_device_page_table_matches_oracle(lens):
+    fb, _, _, r2t = make_batch(lens, layers=1, seed=len(lens))
+    rows = fb.req_pool_indices.tolist()
+    print(f"[case] page table lens={lens[:4]}...", flush=True)
+    indptr, indices, last = paging.build_page_table(
+        fb.req_to_token_pool.req_to_token, fb.req_pool_indices, fb.seq_lens,
+        seq_lens_sum=fb.seq_lens_sum)
+    torch.cuda.synchronize()
+    wi, wx, wl = ptab.build_page_table(r2t.numpy(), rows, lens)
+    assert indptr.cpu().tolist() == wi.tolist()
+    assert last.cpu().tolist() == wl.tolist()
+    assert indices[:int(wi[-1])].cpu().tolist() == wx.tolist()
+
+
+@pytest.mark.gpu
+def test_device_page_table_empty_requests_and_capacity_clamp():
+    fb, _, _, r2t = make_batch([0, 40, 0, 16], layers=1, seed=9)
+    rows = fb.req_pool_indices.tolist()
+    indptr, indices, last = paging.build_page_table(
+        fb.req_to_token_pool.req_to_token, fb.req_pool_indices, fb.seq_lens, capacity=2)
+    torch.cuda.synchronize()
+    wi, wx, wl = ptab.build_page_table(r2t.numpy(), rows, [0, 40, 0, 16])
+    assert indptr.cpu().tolist() == wi.tolist() and last.cpu().tolist() == wl.tolist()
+    assert indices.cpu().tolist() == wx[:2].tolist()     # writes past capacity are dropped
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("split_kv", [0, 1, 4])
+def test_decode_step_through_the_adapter(dtype, split_kv):
+    lens = [1, 17, 300, 16, 1000, 33, 129]
+    fb, layers, pool, r2t = make_batch(lens, dtype=dtype, seed=3)
+    rows = fb.req_pool_indices.tolist()
+    backend = sglang_backend.SplitKVHipBackend(split_kv=split_kv)
+    backend.init_forward_metadata(fb)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    for layer in layers:
+        print(f"[case] adapter {dtype} split={split_kv} layer={layer.layer_id}", flush=True)
+        q = torch.randn(len(lens), 32 * 128, generator=g, device=DEV).to(dtype)
+        k = torch.randn(len(lens), 8 * 128, generator=g, device=DEV).to(dtype)
+        v = torch.randn(len(lens), 8 * 128, generator=g, device=DEV).to(dtype)
+        out = backend.forward(q, k, v, layer, fb)          # SGLang's positional call
+        torch.cuda.synchronize()
+        assert out.shape == (len(lens), 32 * 128)
+        # the new token's K/V landed in the pool at out_cache_loc
+        kb = pool.get_key_buffer(layer.layer_id)
+        assert torch.equal(kb[fb.out_cache_loc.long()].reshape(len(lens), -1), k)
+        want = _want(q.view(-1, 32, 128), pool, layer.layer_id, r2t.numpy(), rows, lens)
+        mx, mean = err_stats(out.view(-1, 32, 128), want)
+        assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+
+
+@pytest.mark.gpu
+def test_adapter_custom_scaling_and_reference_shim():
+    lens = [64, 500, 3]
+    fb, layers, pool, r2t = make_batch(lens, layers=1, seed=4)
+    rows = fb.req_pool_indices.tolist()
+    layer = layers[0]
+    layer.scaling = 0.05                           # not 1/sqrt(128)
+    backend = sglang_backend.SplitKVHipBackend()
+    backend.init_forward_metadata(fb)
+    q = torch.randn(3, 32 * 128, device=DEV).half()
+    out = backend.forward_decode(q, None, None, layer, fb)
+    torch.cuda.synchronize()
+    # softmax(0.05 q.k) = softmax((0.05 sqrt(128) q).k / sqrt(128))
+    want = _want(q.view(-1, 32, 128), pool, 0, r2t.numpy(), rows, lens,
+                 scale_mult=0.05 * math.sqrt(128))
+    mx, mean = err_stats(out.view(-1, 32, 128), want)
+    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+    # the reference shim's forward(q, kv_data, indptr, indices, last) on the same pool
+    kv = torch.from_numpy(_pool_as_combined(pool, 0)).to(DEV).half()
+    md = backend.forward_metadata
+    o2 = backend.forward(q.view(-1, 32, 128), kv, md.kv_indptr, md.kv_indices,
+                         md.kv_last_page_len)
+    torch.cuda.synchronize()
+    mx2, _ = err_stats(o2, _want(q.view(-1, 32, 128), pool, 0, r2t.numpy(), rows, lens))
+    assert mx2 <= 1e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("split_kv", [1, 3, 0])
+def test_split_caches_equal_combined_cache(split_kv):
+    # the (k_cache, v_cache) form (separate buffers; V allocated first, so its offset from
+    # K may be negative) gives the same result as the combined cache holding the same data
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        5, [100, 1, 4000, 0, 333], 32, 8, 128, device=DEV, page_table="permuted", seed=8)
+    v_cache = kv[:, 1].clone()
+    k_cache = kv[:, 0].clone()
+    a = attention.decode_attention(q, kv, indptr, ids, last, split_kv=split_kv)
+    b = attention.decode_attention(q, (k_cache, v_cache), indptr, ids, last, split_kv=split_kv)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("scale", [0.02, 0.3])
+def test_sm_scale_matches_prescaled_q(scale):
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        4, [700, 20, 1, 64], 32, 8, 64, device=DEV, page_table="permuted", seed=12)
+    out = attention.decode_attention(q, kv, indptr, ids, last, split_kv=0, sm_scale=scale)
+    torch.cuda.synchronize()
+    want = ref.reference_attention_paged(to_np(q) * np.float32(scale * 8.0), to_np(kv),
+                                         to_np(indptr), to_np(ids), to_np(last))
+    mx, mean = err_stats(out, want)
+    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
