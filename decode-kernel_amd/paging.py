@@ -1,4 +1,4 @@
-"""Page tables for the decode path built on the device from a token-slot map.
+"""Page tables and cache writes around the decode path, on the device.
 
 `build_page_table` turns a serving framework's per-request token-slot map (SGLang's
 ReqToTokenPool.req_to_token) into the CSR page table of src/layout.md:27-138 with one
@@ -8,6 +8,7 @@ trip. Tokens are assumed to sit in 16-token pages: token t of a request at slot
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -63,3 +64,59 @@ def build_page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
             kv_last.data_ptr(), stream)
     dk_lib.check(rc, "build_page_table")
     return kv_indptr, kv_indices[:int(capacity)], kv_last
+
+
+def rope_inv_freq(head_dim: int, theta: float = 10000.0, device="cuda") -> torch.Tensor:
+    """Plain rotary frequencies theta^(-2i/head_dim), i < head_dim/2, fp32. Frequency
+    scalings (Llama 3's, YaRN, ...) produce their own inv_freq and pass it instead."""
+    i = torch.arange(0, head_dim, 2, dtype=torch.float64)
+    return (1.0 / (theta ** (i / head_dim))).to(device=device, dtype=torch.float32)
+
+
+def append_kv(q: Optional[torch.Tensor], k_new: torch.Tensor, v_new: torch.Tensor, kv_data,
+              kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
+              inv_freq: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
+              rope_style: int = 0) -> None:
+    """Write each sequence's new token into the paged cache (dk_append_kv), in place.
+
+    The token's slot is the last one the page table describes (grow the table first).
+    q (batch, num_q_heads, head_dim) or None is rotated in place; k_new / v_new
+    (batch, num_kv_heads, head_dim) are the token's K (rotated on the way in) and V rows;
+    kv_data is the combined cache or a (k_cache, v_cache) pair as for decode_attention.
+    inv_freq (head_dim/2,) fp32 on the device, or None for no rotation; positions (batch,)
+    int32, or None for each token's index in its sequence; rope_style 0 = rotate-half
+    pairs (i, i + D/2) (Llama), 1 = interleaved pairs (2i, 2i + 1).
+    """
+    import attention                     # local: attention imports nothing from here
+    kv = attention._kv_layout(kv_data)
+    batch, hkv, d = k_new.shape
+    if v_new.shape != k_new.shape or k_new.dtype != kv.dtype or v_new.dtype != kv.dtype:
+        raise DecodeArgumentError("k_new and v_new must be (batch, num_kv_heads, head_dim) in "
+                                  "the cache's dtype")
+    if v_new.stride() != k_new.stride() or k_new.stride(2) != 1:
+        raise DecodeArgumentError("k_new and v_new need equal strides and a unit head_dim stride")
+    if hkv != kv.hkv or d != kv.d or kv.page_size != PAGE_SIZE or kv.d_stride != 1:
+        raise DecodeArgumentError("k_new does not match the cache's heads / head_dim")
+    if q is not None and (q.dim() != 3 or q.shape[0] != batch or q.shape[2] != d or
+                          q.dtype != kv.dtype or q.stride(2) != 1):
+        raise DecodeArgumentError("q must be (batch, num_q_heads, head_dim) in the cache dtype")
+    if inv_freq is not None and (inv_freq.dtype != torch.float32 or inv_freq.numel() != d // 2
+                                 or not inv_freq.is_contiguous()):
+        raise DecodeArgumentError("inv_freq must be a contiguous fp32 tensor of head_dim/2")
+    if positions is not None:
+        positions = positions.to(dtype=torch.int32).contiguous()
+    s = dk_lib.DkStrides()
+    if q is not None:
+        s.q_b, s.q_h = q.stride(0), q.stride(1)
+    s.kv_p, s.kv_r, s.kv_s, s.kv_h = kv.strides
+    code = dk_lib.DK_F16 if kv.dtype == torch.float16 else dk_lib.DK_BF16
+    ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
+    with torch.cuda.device(k_new.device):
+        stream = torch.cuda.current_stream(k_new.device).cuda_stream
+        rc = dk_lib.load().dk_append_kv(
+            ptr(q), k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+            kv.k.data_ptr(), ptr(kv.v), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+            kv_last_page_len.data_ptr(), ptr(positions), ptr(inv_freq), rope_style, batch,
+            q.shape[1] if q is not None else 1, hkv, d, PAGE_SIZE, kv.num_pages,
+            kv_indices.shape[0], code, ctypes.byref(s), stream)
+    dk_lib.check(rc, "append_kv")

@@ -186,6 +186,27 @@ int dk_build_page_table(const int32_t* req_to_token, int64_t req_stride,
                         int32_t* kv_indices, int64_t capacity, int32_t* kv_last_page_len,
                         void* hip_stream);
 
+/* Cache write before a decode step: for every sequence b, the new token is the last one
+ * the page table describes (page kv_indices[kv_indptr[b+1] - 1], slot
+ * kv_last_page_len[b] - 1; grow the table first). Writes its K row rotated by rotary
+ * position embedding and its V row there for all kv heads, and rotates q (optional, NULL
+ * to skip) in place. k_new / v_new are (batch, num_kv_heads, head_dim) with element
+ * strides new_b, new_h (unit head_dim stride); q and the caches use `strides` (q_b, q_h;
+ * kv_p, kv_s, kv_h, and kv_r for the combined cache when v_cache is NULL). Rotation:
+ * position = positions[b] (or, when positions is NULL, the token's index in its sequence),
+ * angle_i = position * inv_freq[i] for i < head_dim / 2, pairs (i, i + head_dim/2) when
+ * rope_style == 0 (Llama / GPT-NeoX) or (2i, 2i + 1) when 1 (GPT-J); fp32 arithmetic,
+ * one rounding. inv_freq NULL: rows copied unrotated. A sequence without pages is skipped.
+ * No counterpart in the reference, which has no cache write (src/layout.md:41-69 fixes
+ * the format written). */
+int dk_append_kv(void* q, const void* k_new, const void* v_new, int64_t new_b, int64_t new_h,
+                 void* k_cache, void* v_cache, const int32_t* kv_indptr,
+                 const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                 const int32_t* positions, const float* inv_freq, int32_t rope_style,
+                 int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                 int32_t page_size, int64_t num_pages, int64_t num_indices, int32_t dtype,
+                 const dk_strides* strides, void* hip_stream);
+
 /* Pass 1 only: writes partial_O / partial_m / partial_l for split_kv >= 1 splits into
  * the workspace (layout from dk_partials_layout; partial_m is the split's max of
  * q.k*scale, -1e9 for an empty split, partial_l = sum exp(score - partial_m),

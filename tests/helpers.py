@@ -13,8 +13,7 @@ def to_np(t: torch.Tensor) -> np.ndarray:
     """CPU numpy copy; bfloat16 becomes its exact float32 value, fp16 stays fp16."""
     t = t.detach().cpu()
     if t.dtype == torch.bfloat16:
-        bits = t.contiguous().view(torch.int16).numpy().astype(np.uint16)
-        return (bits.astype(np.uint32) << 16).view(np.float32)
+        return t.float().numpy()          # every bf16 value is exactly representable
     return t.numpy()
 
 

@@ -310,3 +310,76 @@ def test_planted_page_table_mistake_is_caught_by_round_trip():
     bad = all(np.array_equal(ptab.token_slots(indptr, indices, bad_last, b), r2t[r, :n])
               for b, (r, n) in enumerate(zip(rows, lens)))
     assert ok and not bad
+
+
+# ---------------------------------------------------------------- RoPE + cache write
+
+from oracle import append as oapp  # noqa: E402
+
+
+def _hf_rope(x, pos, inv_freq):
+    """transformers' Llama rotation (apply_rotary_pos_emb, rotate_half) in float64 with the
+    same fp32 angles: an independent implementation of the rotate-half convention."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    ang = torch.from_numpy((np.float32(pos) * np.asarray(inv_freq, np.float32)).astype(np.float64))
+    emb = torch.cat([ang, ang])
+    cos, sin = emb.cos()[None, None], emb.sin()[None, None]
+    t = torch.from_numpy(np.asarray(x, np.float64))[None, :, None, :]   # (1, H, 1, D)
+    q_rot, _ = apply_rotary_pos_emb(t, t, cos, sin, unsqueeze_dim=1)
+    return q_rot[0, :, 0].numpy()
+
+
+@pytest.mark.parametrize("pos", [0, 1, 17, 2047, 70000])
+def test_rope_matches_transformers_llama(pos):
+    rng = np.random.default_rng(pos)
+    x = rng.standard_normal((4, 64))
+    inv = 1.0 / (500000.0 ** (np.arange(0, 64, 2) / 64))
+    np.testing.assert_allclose(oapp.rope(x, pos, inv), _hf_rope(x, pos, inv), rtol=0, atol=1e-12)
+
+
+def test_rope_identities():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 16))
+    inv = 2.0 ** -np.arange(8)                      # exact angles for small integer positions
+    np.testing.assert_array_equal(oapp.rope(x, 0, inv), x)
+    for style in (0, 1):
+        y = oapp.rope(x, 5, inv, style)
+        # each rotated pair keeps its length
+        if style == 0:
+            n0, n1 = x[:, :8] ** 2 + x[:, 8:] ** 2, y[:, :8] ** 2 + y[:, 8:] ** 2
+        else:
+            n0, n1 = x[:, 0::2] ** 2 + x[:, 1::2] ** 2, y[:, 0::2] ** 2 + y[:, 1::2] ** 2
+        np.testing.assert_allclose(n1, n0, rtol=1e-12)
+        # rotations compose: R(3) R(5) = R(8)
+        np.testing.assert_allclose(oapp.rope(oapp.rope(x, 3, inv, style), 5, inv, style),
+                                   oapp.rope(x, 8, inv, style), atol=1e-12)
+
+
+def test_rope_interleaved_known_answer():
+    # D = 4, GPT-J pairs (0,1), (2,3); inv_freq (pi/2, 0) at position 1: the first pair
+    # turns by 90 degrees, the second not at all
+    y = oapp.rope([1.0, 2.0, 3.0, 4.0], 1, [np.pi / 2, 0.0], style=1)
+    np.testing.assert_allclose(y, [-2.0, 1.0, 3.0, 4.0], atol=1e-6)
+
+
+def test_append_writes_the_last_slot_of_each_sequence():
+    kv = np.zeros((4, 2, 16, 1, 2))
+    indptr, indices, last = [0, 2, 2, 3], [3, 1, 0], [5, 1, 16]
+    k_new = np.array([[[1.0, 2.0]], [[3.0, 4.0]], [[5.0, 6.0]]])
+    v_new = k_new + 10
+    out, _ = oapp.append_kv(kv, None, k_new, v_new, indptr, indices, last)
+    assert out[1, 0, 4, 0].tolist() == [1.0, 2.0] and out[1, 1, 4, 0].tolist() == [11.0, 12.0]
+    assert out[0, 0, 15, 0].tolist() == [5.0, 6.0]
+    assert np.count_nonzero(out) == 8                # sequence 1 has no pages: skipped
+
+
+def test_planted_rope_sign_mistake_is_caught_by_transformers():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((2, 8))
+    inv = 1.0 / (10000.0 ** (np.arange(0, 8, 2) / 8))
+    ang = np.float32(9) * inv.astype(np.float32)
+    bad = x.copy()
+    bad[:, :4] = x[:, :4] * np.cos(ang) + x[:, 4:] * np.sin(ang)     # sign of sin flipped
+    bad[:, 4:] = x[:, 4:] * np.cos(ang) - x[:, :4] * np.sin(ang)
+    assert np.abs(bad - _hf_rope(x, 9, inv)).max() > 1e-2
+    np.testing.assert_allclose(oapp.rope(x, 9, inv), _hf_rope(x, 9, inv), atol=1e-12)
