@@ -11,6 +11,8 @@ step a 1 GiB device fill evicts the 4 MB L2s and the 256 MB Infinity Cache, as t
 reference flushes L2 before each timed call (bench/microbench_cuda.py:75-90,140-157);
 HIP events on the launch stream bracket the call itself. The flush is enqueued without a
 host sync, so host launch overhead is hidden behind it and the events measure GPU time.
+The W warm-up steps are such flush + call steps too, after an untimed settling phase of
+the same steps (0.3 s) that lets the GPU clocks reach their steady state.
 
 Prints one JSON line. `value` is achieved algorithmic HBM bandwidth in TB/s
 (bytes of the reference's model, bench/microbench_cuda.py:114-121, plus page tables,
@@ -36,6 +38,7 @@ for _p in (ROOT / "decode-kernel_amd", ROOT):
 METRIC = ("µs/call + achieved HBM TB/s (% peak), decode B=32 ctx=8k Hq32/Hkv8 d128")
 PEAK_GBPS = 8000.0          # MI355X HBM3E
 FLUSH_BYTES = 1 << 30
+SETTLE_S = 0.3              # untimed flush + call steps before the warm-up
 TRAFFIC_FILE = ROOT / "profiles" / "pass1_metric_hbm_traffic.md"
 
 
@@ -54,6 +57,10 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
+    ap.add_argument("--flush", default="write", choices=["write", "read"],
+                    help="cache flush before each step: fill (write) or sum (read) 1 GiB")
+    ap.add_argument("--page-table", default="permuted", choices=["permuted", "contiguous"],
+                    help="page-table shape of the synthetic pool (the metric uses permuted)")
     ap.add_argument("--no-plan-hint", action="store_true",
                     help="do not pass the host-side max_pages_per_seq plan hint")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -123,14 +130,21 @@ def main():
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     B, ctx, hq, hkv, d = args.batch, args.ctx, 32, 8, 128
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-        B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table="permuted", seed=1)
+        B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table=args.page_table, seed=1)
     split = attention.resolve_split(args.split)
     nbytes = layout.attention_bytes(B, ctx, hq, hkv, d)
     out = torch.empty_like(q)
     ws_bytes = dk_lib.workspace_bytes(B, hq, hkv, d, split)
     p_total = dk_lib.partials_layout(B, hq, d, split)[3] if split else ws_bytes
     ws = torch.empty(max(ws_bytes, p_total), dtype=torch.uint8, device=dev)
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+
+    def flush():
+        # evict the caches: write (fill) or read (sum) a 1 GiB buffer
+        if args.flush == "write":
+            flush_buf.zero_()
+        else:
+            flush_buf.sum()
     strides = attention._strides(q, kv, out)
     # plan step, outside the timed region: the longest sequence's page count from the host
     # side of the page table (what a serving framework keeps on the host)
@@ -156,21 +170,25 @@ def main():
 
     dk_lib.check(full_call(), "decode_attention")
     dk_lib.check(pass1_call(), "decode_partials")
-    for _ in range(args.warmup):
-        full_call()
-    torch.cuda.synchronize()
 
     def timed(fn, steps):
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(steps)]
         for e0, e1 in evs:
-            flush.zero_()
+            flush()
             e0.record(stream)
             fn()
             e1.record(stream)
         torch.cuda.synchronize()
         return [e0.elapsed_time(e1) * 1e3 for e0, e1 in evs]     # microseconds
 
+    # Warm-up: W steps exactly like the timed ones (flush + call), after an untimed
+    # settling phase of the same steps (at least SETTLE_S seconds) that brings the GPU's
+    # clocks to their steady state; without it the first timed steps run slow.
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        timed(full_call, 20)
+    timed(full_call, args.warmup)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     call_us = timed(full_call, args.steps)
@@ -192,7 +210,7 @@ def main():
         "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
         "config": {"workload": f"paged decode attention B={B} ctx={ctx} Hq={hq} Hkv={hkv} "
-                               f"D={d} {args.dtype} page_size=16 permuted pages",
+                               f"D={d} {args.dtype} page_size=16 {args.page_table} pages",
                    "batch": B, "context_length": ctx, "num_q_heads": hq, "num_kv_heads": hkv,
                    "head_dim": d, "page_size": 16,
                    "split_kv": split,

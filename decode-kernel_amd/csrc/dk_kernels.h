@@ -334,9 +334,12 @@ struct Wave {
 
   // pg: base of this kv head's slice of a page (page base + kvh * kv_h). Buffer loads:
   // the address is the page base (scalar) + a per-lane offset + a per-row scalar offset.
-  __device__ __forceinline__ void load_page(u32 (&kb)[KW], u32 (&vb)[VW], const uint8_t* pg) const {
-    const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, extent);
-    const __amdgpu_buffer_rsrc_t rv = page_rsrc(pg + kv_v, extent);
+  // live == false: a zero-extent descriptor, the loads return zeros without touching memory
+  __device__ __forceinline__ void load_page(u32 (&kb)[KW], u32 (&vb)[VW], const uint8_t* pg,
+                                            bool live = true) const {
+    const u32 ext = live ? extent : 0u;
+    const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, ext);
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(pg + kv_v, ext);
     if constexpr (MFMA) {
 #pragma unroll
       for (int i = 0; i < NMF; ++i) ld_buf<4>(&kb[4 * i], rk, koff, 64 * i);
@@ -603,11 +606,19 @@ struct Wave {
   }
 };
 
+// Pages kept in flight ahead of the one being computed: two for head_dim <= 128, one for
+// 256 (whose page buffers are twice as large); a build may set another depth.
+#ifndef DK_PREFETCH_DEPTH
+#define DK_PREFETCH_DEPTH 0
+#endif
+template <int D>
+constexpr int prefetch_depth() { return DK_PREFETCH_DEPTH ? DK_PREFETCH_DEPTH : (D <= 128 ? 2 : 1); }
+
 // Resident wavefronts per SIMD the register allocator is held to: the page buffers
 // (D/4 words each), G*D/16 accumulators and the q operand must fit without spilling.
 template <int D, int G>
 constexpr int min_waves_per_simd() {
-  return D >= 256 ? 1 : (D * G >= 1024 ? 1 : 2);
+  return (D >= 256 || prefetch_depth<D>() > 2) ? 1 : (D * G >= 1024 ? 1 : 2);
 }
 
 // Pages [first, first + n) of one (sequence, kv head), streamed through register buffers:
@@ -658,10 +669,25 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KW], u32 (&va)[
   }
 }
 
-// Pages kept in flight ahead of the one being computed: two for head_dim <= 128, one for
-// 256 (whose page buffers are twice as large).
-template <int D>
-constexpr int prefetch_depth() { return D <= 128 ? 2 : 1; }
+// Ring of DEPTH + 1 page buffers for any DEPTH: buffer j % (DEPTH + 1) holds page j. Every
+// step issues one page's loads and computes another, so the wait counters see the same
+// pending loads on every path; steps past the last page load with a zero-extent
+// descriptor (no memory access) and skip the compute.
+template <int DEPTH, class W, class PageFn, class ValidFn>
+__device__ __forceinline__ void stream_ring(W& wv, int n, PageFn page, ValidFn valid) {
+  constexpr int NB = DEPTH + 1;
+  u32 kb[NB][W::KW], vb[NB][W::VW];
+#pragma unroll
+  for (int j = 0; j < DEPTH; ++j) wv.load_page(kb[j], vb[j], page(min(j, n - 1)), j < n);
+  for (int k = 0; k < n; k += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int ld = k + j + DEPTH;
+      wv.load_page(kb[(j + DEPTH) % NB], vb[(j + DEPTH) % NB], page(min(ld, n - 1)), ld < n);
+      if (k + j < n) wv.compute_page(kb[j], vb[j], valid(k + j));
+    }
+  }
+}
 
 // ---------------------------------------------------------------- workgroup combine
 // LDS scratch for merging the NW wavefronts of a workgroup.
@@ -739,9 +765,13 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
-    u32 ka[WV::KW], va[WV::VW];
-    wv.load_page(ka, va, pk(0));
-    stream_pages<prefetch_depth<D>()>(wv, ka, va, nk, pk, vk);
+    if constexpr (prefetch_depth<D>() <= 2) {
+      u32 ka[WV::KW], va[WV::VW];
+      wv.load_page(ka, va, pk(0));
+      stream_pages<prefetch_depth<D>()>(wv, ka, va, nk, pk, vk);
+    } else {
+      stream_ring<prefetch_depth<D>()>(wv, nk, pk, vk);
+    }
   }
 }
 

@@ -86,20 +86,26 @@ def _run_all(cmds: list[list[str]]) -> str:
     return "\n".join(raw)
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile csrc/ into libdk_decode.so (always rebuilds). Returns the library path."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, defines: tuple = (), out: Path = LIB_PATH,
+          build_dir: Path = BUILD_DIR) -> Path:
+    """Compile csrc/ into libdk_decode.so (always rebuilds). Returns the library path.
+    `defines` (e.g. ("DK_PREFETCH_DEPTH=4",)) and another `out` / `build_dir` make a side
+    build for comparisons, loadable through the DK_DECODE_LIB environment variable."""
+    build_dir = Path(build_dir)
+    out = Path(out)
+    build_dir.mkdir(parents=True, exist_ok=True)
     hipcc = _hipcc()
-    objs = [BUILD_DIR / "dk_args.o"]
+    dflags = [f"-D{d}" for d in defines]
+    objs = [build_dir / "dk_args.o"]
     cmds = [["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}",
              "-c", str(CSRC / "dk_args.cpp"), "-o", str(objs[0])]]
     for src in HIP_SOURCES:
-        obj = BUILD_DIR / (Path(src).stem + ".o")
+        obj = build_dir / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *HIP_FLAGS, RESOURCE_FLAG, f"-I{INCLUDE}", "-c", str(CSRC / src),
-                     "-o", str(obj)])
+        cmds.append([hipcc, *HIP_FLAGS, *dflags, RESOURCE_FLAG, f"-I{INCLUDE}", "-c",
+                     str(CSRC / src), "-o", str(obj)])
     res = kernel_resources(_run_all(cmds))
-    (BUILD_DIR / "kernel_resources.txt").write_text("".join(
+    (build_dir / "kernel_resources.txt").write_text("".join(
         f"{k} VGPRs={v.get('VGPRs')} scratch={v.get('ScratchSize')} "
         f"occupancy={v.get('Occupancy')}\n" for k, v in sorted(res.items())))
     # Every kernel keeps its state in registers and LDS: scratch memory here would mean an
@@ -107,13 +113,13 @@ def build(verbose: bool = False) -> Path:
     scratch = sorted(k for k, v in res.items() if v.get("ScratchSize", 0) > 0)
     if scratch:
         raise RuntimeError(f"{len(scratch)} kernels use scratch memory: {scratch[:4]}")
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     _run_all([[hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs),
                "-o", str(tmp)]])
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":
