@@ -217,8 +217,7 @@ def main():
                    "schedule": {1: "one pass"}.get(eff, "balanced + merge" if eff == 0
                                                    else f"split {eff} + merge"),
                    "plan_hint_max_pages": hint,
-                   "qk_path": "mfma" if args.qk_path == 1 or (args.qk_path == 0 and
-                                                               args.dtype == "bf16") else "valu"},
+                   "qk_path": "mfma" if args.qk_path == 1 else "valu", "pv_path": "mfma"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
         "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
         "bytes_per_call": nbytes, "wall_s_timed_loop": round(wall, 3),

@@ -93,9 +93,9 @@ Plan make_plan(const Problem& p) {
   pl.chunks = pl.group / pl.heads;
   pl.pairs_per_seq = p.hkv * pl.chunks;
   pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : kDefaultWavesPerGroup;
-  // q.k on MFMA for bf16 by default: its VALU path converts every K element to fp32,
-  // while fp16 has packed dot products (measured: bf16 MFMA faster, fp16 VALU faster)
-  pl.mfma = p.opt.qk_path == 1 || (p.opt.qk_path == 0 && p.dtype == DK_BF16);
+  // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
+  // 64-byte row segments on the NHD layout (measured for both fp16 and bf16)
+  pl.mfma = p.opt.qk_path == 1;
   pl.balanced = p.split == 0;
   pl.grid = pl.balanced ? 0 : (int64_t)p.batch * pl.pairs_per_seq * std::max(p.split, 1);
   return pl;

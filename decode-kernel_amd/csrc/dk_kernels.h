@@ -15,11 +15,10 @@
 //   Every K/V element is read once and serves all G heads of its kv head.
 //   Online softmax is fp32 in the log2 domain (v_exp_f32); the reference max only moves
 //   when a score exceeds it by more than 2^8, so accumulators are rescaled a handful of
-//   times per split instead of every page. P.V: fp16 pairs tokens with v_dot2_f32_f16
-//   (p rounded to nearest fp16, and l summed from the same rounded p, so the output is an
-//   exact weighted mean under weights perturbed by <= 2^-11); bf16 uses fp32 fma. The p
-//   of the other heads of a quad come through DPP quad_perm. The next page's loads are
-//   in flight while the current page is computed.
+//   times per split instead of every page. P.V runs on v_mfma_f32_16x16x16_{f16,bf16}
+//   with p split into hi + lo parts of the element type (weights exact to 2^-22 / 2^-16)
+//   and B taken from the V registers as loaded. The next pages' loads are in flight while
+//   the current page is computed.
 //
 // Pass 1, explicit split (dk_pass1_split): one workgroup per (sequence, kv head, split)
 //   over ceil(N/S)-page ranges as in the reference partition kernel
@@ -37,7 +36,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace dk {
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, each i a compile-time constant
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 using u32 = uint32_t;
 typedef u32 u32x4 __attribute__((ext_vector_type(4)));
@@ -47,7 +58,9 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPage = 16;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -56,7 +69,6 @@ constexpr float kEmptyM = -1e9f;        // partial_m of an empty split (attentio
 constexpr float kMinit = -1e30f;        // running reference before the first score
 constexpr float kSlack = 8.0f;          // log2 headroom before the reference max moves
 constexpr float kNegInf = -__builtin_inff();
-constexpr u32 kOnesF16x2 = 0x3C003C00u; // (1.0h, 1.0h)
 
 // ---------------------------------------------------------------- launch arguments
 struct Pass1Args {
@@ -95,9 +107,6 @@ struct MergeArgs {
 
 // ---------------------------------------------------------------- element types
 struct F16 {
-  static constexpr bool kDotPV = true;
-  static __device__ __forceinline__ float lo(u32 w) { return (float)__builtin_bit_cast(f16x2, w)[0]; }
-  static __device__ __forceinline__ float hi(u32 w) { return (float)__builtin_bit_cast(f16x2, w)[1]; }
   static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -109,14 +118,19 @@ struct F16 {
   static __device__ __forceinline__ void store(uint8_t* p, float x) {
     *reinterpret_cast<_Float16*>(p) = (_Float16)x;
   }
+  static __device__ __forceinline__ f32x4 mfma_pv(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ u32 pack2(float x0, float x1, float* r0, float* r1) {
+    const f16x2 h = __builtin_convertvector(f32x2{x0, x1}, f16x2);
+    *r0 = (float)h[0];
+    *r1 = (float)h[1];
+    return __builtin_bit_cast(u32, h);
+  }
 };
 
 struct BF16 {
-  static constexpr bool kDotPV = false;
-  static __device__ __forceinline__ float lo(u32 w) { return __builtin_bit_cast(float, w << 16); }
-  static __device__ __forceinline__ float hi(u32 w) {
-    return __builtin_bit_cast(float, w & 0xffff0000u);
-  }
   static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -124,6 +138,19 @@ struct BF16 {
   static __device__ __forceinline__ float dot2(u32 a, u32 b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
                                            __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  // C += A.B with A 16x16 (rows: lane%16, k: 4 per lane), B 16x16 (k: 4 per lane, cols:
+  // lane%16), 4 bf16 per lane in two words each
+  static __device__ __forceinline__ f32x4 mfma_pv(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a),
+                                                     __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
+  }
+  // (bf16(x0), bf16(x1)) rounded to nearest, and the fp32 values they stand for
+  static __device__ __forceinline__ u32 pack2(float x0, float x1, float* r0, float* r1) {
+    const bf16x2 h = __builtin_convertvector(f32x2{x0, x1}, bf16x2);
+    *r0 = (float)h[0];
+    *r1 = (float)h[1];
+    return __builtin_bit_cast(u32, h);
   }
   static __device__ __forceinline__ void store(uint8_t* p, float x) {
     *reinterpret_cast<__bf16*>(p) = (__bf16)x;
@@ -150,10 +177,6 @@ __device__ __forceinline__ u32 quad_bcast_u(u32 x) { return dpp_u<Q * 0x55>(x); 
 __device__ __forceinline__ float quad_bcast_i(float x, int q) {
   return q == 0 ? quad_bcast<0>(x) : q == 1 ? quad_bcast<1>(x) : q == 2 ? quad_bcast<2>(x)
                                                                         : quad_bcast<3>(x);
-}
-__device__ __forceinline__ u32 quad_bcast_iu(u32 x, int q) {
-  return q == 0 ? quad_bcast_u<0>(x) : q == 1 ? quad_bcast_u<1>(x)
-                                              : q == 2 ? quad_bcast_u<2>(x) : quad_bcast_u<3>(x);
 }
 template <int N>
 __device__ __forceinline__ float row_ror(float x) { return dpp<0x120 + N>(x); }
@@ -289,7 +312,9 @@ struct Wave {
   float kscale;
   u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, dims 32i+8r16..
   u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
-  float acc[G][DPL];
+  float acc[G][DPL];      // after reduce_rows: head h, dim c*DPL + j (every lane row)
+  f32x4 cv[NS][DPL];      // while pages stream: the P.V accumulators as MFMA C vectors,
+                          // element g = head ss*GQ + g of dim c*DPL + j
   float mref[NS], mtrue[NS], lsum[NS];
 
   __device__ __forceinline__ void init(const Pass1Args& a) {
@@ -321,9 +346,9 @@ struct Wave {
 
   __device__ __forceinline__ void reset() {
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int ss = 0; ss < NS; ++ss)
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[h][j] = 0.f;
+      for (int j = 0; j < DPL; ++j) cv[ss][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss) {
       mref[ss] = kMinit;
@@ -440,12 +465,11 @@ struct Wave {
         const float mn = allmax_head<GQ>(fmaxf(mref[ss], mx[ss]));
         const float al = __builtin_amdgcn_exp2f(mref[ss] - mn);
         lsum[ss] *= al;
+        f32x4 ab4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-          const float ab = GQ > 1 ? quad_bcast_i(al, g) : al;
+        for (int g = 0; g < GQ; ++g) ab4[g] = GQ > 1 ? quad_bcast_i(al, g) : al;
 #pragma unroll
-          for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] *= ab;
-        }
+        for (int j = 0; j < DPL; ++j) cv[ss][j] *= ab4;
         mref[ss] = mn;
       }
     }
@@ -455,74 +479,61 @@ struct Wave {
 #pragma unroll
       for (int r = 0; r < 4; ++r) p[ss][r] = __builtin_amdgcn_exp2f(x[ss][r] - mref[ss]);
 
-    if constexpr (T::kDotPV) {
-      // fp16: p rounded to fp16 pairs (tokens 0,1 and 2,3); l from the same rounded p
-      u32 pk[NS][2], pb[NS][GQ][2];
+    {
+      // P.V on MFMA (v_mfma_f32_16x16x16_{f16,bf16}): C[head][dim] += P[head][token]
+      // V[token][dim] over the page's 16 tokens. The lane holding the scores of tokens
+      // 4r..4r+3 for head c mod GQ is exactly A's row c, k = 4r..4r+3; B (V) is the
+      // lane's own 4 tokens of one dim, paired by v_perm. p enters as hi + lo (p - hi) in
+      // the element type, so the weights keep 22 (fp16) / 16 (bf16) significant bits;
+      // l sums the fp32 p. C row i of every lane row is head i: no reduction across
+      // lane rows is needed afterwards.
+      u32x2 ah[NS], al[NS];
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
-        // round to nearest even (v_cvt_pk_f16_f32)
-        pk[ss][0] = __builtin_bit_cast(u32, __builtin_convertvector(f32x2{p[ss][0], p[ss][1]}, f16x2));
-        pk[ss][1] = __builtin_bit_cast(u32, __builtin_convertvector(f32x2{p[ss][2], p[ss][3]}, f16x2));
-        lsum[ss] = T::dot2(pk[ss][0], kOnesF16x2, T::dot2(pk[ss][1], kOnesF16x2, lsum[ss]));
-#pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-          pb[ss][g][0] = GQ > 1 ? quad_bcast_iu(pk[ss][0], g) : pk[ss][0];
-          pb[ss][g][1] = GQ > 1 ? quad_bcast_iu(pk[ss][1], g) : pk[ss][1];
-        }
+        lsum[ss] += (p[ss][0] + p[ss][1]) + (p[ss][2] + p[ss][3]);
+        float h0, h1, h2, h3, e;
+        const u32 w01 = T::pack2(p[ss][0], p[ss][1], &h0, &h1);
+        const u32 w23 = T::pack2(p[ss][2], p[ss][3], &h2, &h3);
+        ah[ss] = u32x2{w01, w23};
+        al[ss] = u32x2{T::pack2(p[ss][0] - h0, p[ss][1] - h1, &e, &e),
+                       T::pack2(p[ss][2] - h2, p[ss][3] - h3, &e, &e)};
       }
 #pragma unroll
       for (int q = 0; q < VWT; ++q) {
         const u32 v0 = vb[q], v1 = vb[VWT + q], v2 = vb[2 * VWT + q], v3 = vb[3 * VWT + q];
-        const u32 lo01 = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
-        const u32 hi01 = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
-        const u32 lo23 = __builtin_amdgcn_perm(v3, v2, 0x05040100u);
-        const u32 hi23 = __builtin_amdgcn_perm(v3, v2, 0x07060302u);
+        const u32x2 blo = {__builtin_amdgcn_perm(v1, v0, 0x05040100u),
+                           __builtin_amdgcn_perm(v3, v2, 0x05040100u)};
+        const u32x2 bhi = {__builtin_amdgcn_perm(v1, v0, 0x07060302u),
+                           __builtin_amdgcn_perm(v3, v2, 0x07060302u)};
 #pragma unroll
-        for (int ss = 0; ss < NS; ++ss)
+        for (int half = 0; half < 2; ++half) {
+          const int j = 2 * q + half;
+          const u32x2 b = half ? bhi : blo;
 #pragma unroll
-          for (int g = 0; g < GQ; ++g) {
-            float& a0 = acc[ss * GQ + g][2 * q];
-            float& a1 = acc[ss * GQ + g][2 * q + 1];
-            a0 = T::dot2(lo01, pb[ss][g][0], T::dot2(lo23, pb[ss][g][1], a0));
-            a1 = T::dot2(hi01, pb[ss][g][0], T::dot2(hi23, pb[ss][g][1], a1));
+          for (int ss = 0; ss < NS; ++ss) {
+            cv[ss][j] = T::mfma_pv(ah[ss], b, cv[ss][j]);
+            cv[ss][j] = T::mfma_pv(al[ss], b, cv[ss][j]);
           }
-      }
-    } else {
-#pragma unroll
-      for (int ss = 0; ss < NS; ++ss)
-        lsum[ss] += (p[ss][0] + p[ss][1]) + (p[ss][2] + p[ss][3]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float vf[DPL];
-#pragma unroll
-        for (int q = 0; q < VWT; ++q) {
-          vf[2 * q] = T::lo(vb[r * VWT + q]);
-          vf[2 * q + 1] = T::hi(vb[r * VWT + q]);
         }
-#pragma unroll
-        for (int ss = 0; ss < NS; ++ss)
-#pragma unroll
-          for (int g = 0; g < GQ; ++g) {
-            const float pbv = GQ > 1 ? quad_bcast_i(p[ss][r], g) : p[ss][r];
-#pragma unroll
-            for (int j = 0; j < DPL; ++j)
-              acc[ss * GQ + g][j] = fmaf(pbv, vf[j], acc[ss * GQ + g][j]);
-          }
       }
     }
   }
 
-  // Sum acc and lsum over the four lane rows; exact max over the lanes of each head.
+  // Sum lsum over the four lane rows, exact max over the lanes of each head, and unpack
+  // the P.V accumulators into acc.
   __device__ __forceinline__ void reduce_rows() {
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss) {
       lsum[ss] = sum_xor32(sum_xor16(lsum[ss]));
       mtrue[ss] = allmax_head<GQ>(mtrue[ss]);
     }
+    // the MFMA P.V already summed over all tokens of every lane row
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int ss = 0; ss < NS; ++ss)
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[h][j] = sum_xor32(sum_xor16(acc[h][j]));
+      for (int g = 0; g < GQ; ++g)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] = cv[ss][j][g];
   }
 
   // After reduce_rows every lane holds every head's sums. Lane row r16 stores heads
@@ -530,29 +541,34 @@ struct Wave {
   // by indexing acc with a lane-dependent value (which would move acc to scratch memory).
   static constexpr int KR = (G + 3) / 4;   // heads stored per lane row
 
-  // acc[4k + r16][j]. Each candidate passes through an empty asm so that the compiler
-  // cannot fold the selects into one load from a lane-dependent address of acc.
-  __device__ __forceinline__ float row_head(int k, int j) const {
-    float v = acc[4 * k][j];
+  // acc[4K + r16][j]. K is a template argument and each candidate passes through an
+  // empty asm, so that the compiler cannot fold the selects into one load from a
+  // lane-dependent (or loop-dependent) address of acc.
+  template <int K>
+  __device__ __forceinline__ float row_head(int j) const {
+    float v = acc[4 * K][j];
     __asm__("" : "+v"(v));
 #pragma unroll
     for (int t = 1; t < 4; ++t)
-      if (4 * k + t < G) {
-        float o = acc[4 * k + t][j];
+      if (4 * K + t < G) {
+        float o = acc[4 * K + t][j];
         __asm__("" : "+v"(o));
         v = r16 == t ? o : v;
       }
     return v;
   }
 
-  // per-head-set value x[ss] of head 4k + r16 (head h sits in set h / GQ at quad lane h % GQ)
-  __device__ __forceinline__ float row_head_scalar(const float (&x)[NS], int k) const {
+  // per-head-set value x[ss] of head 4K + r16 (head h sits in set h / GQ at quad lane
+  // h % GQ), selected the same way
+  template <int K>
+  __device__ __forceinline__ float row_head_scalar(const float (&x)[NS]) const {
     float v = 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int h = 4 * k + t;
+      const int h = 4 * K + t;
       if (h < G) {
-        const float xt = GQ > 1 ? quad_bcast_i(x[h / GQ], h % GQ) : x[h / GQ];
+        float xt = GQ > 1 ? quad_bcast_i(x[h / GQ], h % GQ) : x[h / GQ];
+        __asm__("" : "+v"(xt));
         v = r16 == t ? xt : v;
       }
     }
@@ -568,17 +584,17 @@ struct Wave {
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss)
       f[ss] = mtrue[ss] > kNegInf ? __builtin_amdgcn_exp2f(mref[ss] - mtrue[ss]) : 0.f;
-#pragma unroll
-    for (int k = 0; k < KR; ++k) {
+    static_for<KR>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
       const int h = 4 * k + r16;
-      const float fh = row_head_scalar(f, k);
+      const float fh = row_head_scalar<k>(f);
       if (h < G) {
         float v[DPL];
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) v[j] = row_head(k, j) * fh;
+        for (int j = 0; j < DPL; ++j) v[j] = row_head<k>(j) * fh;
         st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
       }
-    }
+    });
     if (r16 == 0 && c < GQ) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
@@ -592,17 +608,17 @@ struct Wave {
 
   // After reduce_rows: normalised output of the G heads (q head h at out + h * o_h).
   __device__ __forceinline__ void store_output(uint8_t* out, int64_t o_h) {
-#pragma unroll
-    for (int k = 0; k < KR; ++k) {
+    static_for<KR>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
       const int h = 4 * k + r16;
-      const float L = row_head_scalar(lsum, k);
+      const float L = row_head_scalar<k>(lsum);
       const float inv = L > 0.f ? 1.f / L : 0.f;
       if (h < G) {
 #pragma unroll
         for (int j = 0; j < DPL; ++j)
-          T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), row_head(k, j) * inv);
+          T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), row_head<k>(j) * inv);
       }
-    }
+    });
   }
 };
 
@@ -710,14 +726,15 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
     else wv.store_partial(a, prow0, phstride);
   } else {
     const int w = uniform(threadIdx.x >> 6);
-#pragma unroll
-    for (int k = 0; k < WV::KR; ++k) {
+    static_for<WV::KR>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
       const int h = 4 * k + wv.r16;
       if (h < G) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) sm.acc[w][h][wv.c * DPL + j] = wv.row_head(k, j);
+        for (int j = 0; j < DPL; ++j)
+          sm.acc[w][h][wv.c * DPL + j] = wv.template row_head<k>(j);
       }
-    }
+    });
     if (wv.r16 == 0 && wv.c < GQ) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {

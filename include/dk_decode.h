@@ -64,8 +64,8 @@ typedef struct {
 /* Optional tuning knobs (NULL = defaults). No counterpart in the reference, which
  * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
 typedef struct {
-  int32_t qk_path;         /* 0 = default (fp16: VALU dot2, bf16: MFMA), 1 = MFMA q.k,
-                              2 = VALU q.k                                                  */
+  int32_t qk_path;         /* 0 = default (VALU dot2), 1 = MFMA q.k, 2 = VALU q.k;
+                              P.V always runs on MFMA                                      */
   int32_t waves_per_group; /* 0 = default (2); 1, 2 or 4 wavefronts per workgroup          */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
                               schedules aim for (0 = default, 2)                            */
