@@ -842,7 +842,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
 // L = ceil(P / Wg) pages; workgroup j takes range j and its NW wavefronts interleave the
 // pages of each segment (maximal run of the range inside one sequence). A sequence covered
 // by a single segment is written out directly (when a.direct); otherwise the segment is
-// stored as a partial at slot (j + b) * HC + hc (unique, < Wg * HC + batch * HC) for the
+// stored as a partial at slot hc * (Wg + batch) + j + b (unique, < HC * (Wg + batch)) for the
 // merge kernel.
 template <class T, int D, int G, int NW, bool MFMA>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_balanced(Pass1Args a) {
@@ -899,7 +899,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
     const int nslots = (start + np - 1) / L - start / L + 1;
     combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
                                a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
-                               ((int64_t)(j + b) * HC + hc) * G, 1);
+                               ((int64_t)hc * (Wg + a.batch) + j + b) * G, 1);
     if (u + n >= u_end) break;
     // next non-empty sequence
     u += n;
@@ -914,49 +914,57 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
 }
 
 // ---------------------------------------------------------------- pass 2
+// Partial k of a row: O at po + k * stride_rows * D, m and l at pm / pl + k * stride_rows.
+// One wavefront per row, lanes over the D dims (E = D/64 each). The slots' loads are
+// issued kU at a time before any is consumed, so a row with many slots costs a few
+// memory round trips rather than one per slot.
 template <class T, int D>
 __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const float* po,
                                           const float* pm, const float* pl, int nslots,
                                           int64_t stride_rows) {
-  // row's partial k sits at po + k * stride_rows * D, pm/pl + k * stride_rows
   constexpr int E = D / 64;
+  constexpr int kU = E <= 2 ? 16 : 8;
+  typedef float vecE __attribute__((ext_vector_type(E)));
   const int lane = threadIdx.x & 63;
-  float M = kNegInf;
-  for (int k = lane; k < nslots; k += 64) M = fmaxf(M, pm[(int64_t)k * stride_rows]);
+  // the first 64 slots' m and l stay in registers (one slot per lane)
+  float pm0 = kNegInf, pl0 = 0.f;
+  if (lane < nslots) {
+    pm0 = pm[(int64_t)lane * stride_rows];
+    pl0 = pl[(int64_t)lane * stride_rows];
+  }
+  float M = pm0;
+  for (int k = lane + 64; k < nslots; k += 64) M = fmaxf(M, pm[(int64_t)k * stride_rows]);
   M = wave_max(M);
-  float accv[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) accv[e] = 0.f;
+  vecE acc = {};
   float L = 0.f;
   for (int k0 = 0; k0 < nslots; k0 += 64) {
     const int k = k0 + lane;
     float wgt = 0.f;
     if (k < nslots) {
-      wgt = __builtin_amdgcn_exp2f((pm[(int64_t)k * stride_rows] - M) * kLog2e);
-      L += wgt * pl[(int64_t)k * stride_rows];
+      const float mk = k0 == 0 ? pm0 : pm[(int64_t)k * stride_rows];
+      const float lk = k0 == 0 ? pl0 : pl[(int64_t)k * stride_rows];
+      wgt = __builtin_amdgcn_exp2f((mk - M) * kLog2e);
+      L += wgt * lk;
     }
     const int cnt = min(64, nslots - k0);
-    for (int j = 0; j < cnt; ++j) {
-      const float wk = readlane_f(wgt, j);
-      const float* o = po + ((int64_t)(k0 + j) * stride_rows) * D + lane * E;
-      if constexpr (E == 1) {
-        accv[0] = fmaf(wk, o[0], accv[0]);
-      } else if constexpr (E == 2) {
-        const f32x2 v = *reinterpret_cast<const f32x2*>(o);
-        accv[0] = fmaf(wk, v[0], accv[0]);
-        accv[1] = fmaf(wk, v[1], accv[1]);
-      } else {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(o);
+    const float* o = po + (int64_t)k0 * stride_rows * D + lane * E;
+    int j = 0;
+    for (; j + kU <= cnt; j += kU) {
+      vecE v[kU];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) accv[e] = fmaf(wk, v[e], accv[e]);
-      }
+      for (int u = 0; u < kU; ++u)
+        v[u] = *reinterpret_cast<const vecE*>(o + (int64_t)(j + u) * stride_rows * D);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, j + u) * v[u];
     }
+    for (; j < cnt; ++j)
+      acc += readlane_f(wgt, j) * *reinterpret_cast<const vecE*>(o + (int64_t)j * stride_rows * D);
   }
   L = wave_sum(L);
   const int b = row / m.hq, qh = row % m.hq;
   uint8_t* op = m.out + (int64_t)b * m.o_b + (int64_t)qh * m.o_h + 2 * lane * E;
 #pragma unroll
-  for (int e = 0; e < E; ++e) T::store(op + 2 * e, L > 0.f ? accv[e] / L : 0.f);
+  for (int e = 0; e < E; ++e) T::store(op + 2 * e, L > 0.f ? acc[e] / L : 0.f);
 }
 
 template <class T, int D>
@@ -972,7 +980,7 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= m.batch * m.hq) return;
   const int b = row / m.hq, qh = row % m.hq;
-  const int HC = m.pairs_per_seq, G = m.heads, Wg = m.waves_per_pair;
+  const int G = m.heads, Wg = m.waves_per_pair;
   auto sb = [&](int bb) { return min(max(ld_const(m.indptr, bb), 0), m.num_indices); };
   const int base = sb(0);
   const int P = max(sb(m.batch) - base, 0);
@@ -986,11 +994,11 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
     const int start = seq0 - base;
     const int j0 = start / L;
     nslots = (start + np - 1) / L - j0 + 1;
-    r0 = ((int64_t)(j0 + b) * HC + hc) * G + g;
+    r0 = ((int64_t)hc * (Wg + m.batch) + j0 + b) * G + g;
   }
   if (nslots == 1) return;   // pass 1 wrote this head's output
-  // slot k of this pair is r0 + k * HC * G (rows of G heads per slot); none -> zeros
-  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, (int64_t)HC * G);
+  // slot k of this pair is r0 + k * G (rows of G heads per slot); none -> zeros
+  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, (int64_t)G);
 }
 
 }  // namespace dk
