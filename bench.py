@@ -39,7 +39,8 @@ METRIC = ("µs/call + achieved HBM TB/s (% peak), decode B=32 ctx=8k Hq32/Hkv8 d
 PEAK_GBPS = 8000.0          # MI355X HBM3E
 FLUSH_BYTES = 1 << 30
 SETTLE_S = 0.3              # untimed flush + call steps before the warm-up
-TRAFFIC_FILE = ROOT / "profiles" / "pass1_metric_hbm_traffic.md"
+TRAFFIC_FILES = {"same": ROOT / "profiles" / "pass1_metric_hbm_traffic.md",
+                 "fp8": ROOT / "profiles" / "pass1_metric_fp8_hbm_traffic.md"}
 
 
 def parse_args():
@@ -57,6 +58,9 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
+    ap.add_argument("--kv-dtype", default="same", choices=["same", "fp8"],
+                    help="cache element type: q's (the metric's fp16) or fp8 E4M3 (an "
+                         "extension; random finite codes, unit scales)")
     ap.add_argument("--flush", default="write", choices=["write", "read"],
                     help="cache flush before each step: fill (write) or sum (read) 1 GiB")
     ap.add_argument("--page-table", default="permuted", choices=["permuted", "contiguous"],
@@ -72,11 +76,12 @@ def parse_args():
     return ap.parse_args()
 
 
-def read_traffic():
+def read_traffic(kv_dtype="same"):
     """HBM bytes per pass-1 launch recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE."""
-    if not TRAFFIC_FILE.exists():
+    path = TRAFFIC_FILES[kv_dtype]
+    if not path.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             try:
                 return int(line.split(":", 1)[1].strip())
@@ -92,10 +97,13 @@ def cpu_baseline(q, kv, indptr, ids, last, out, sample):
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
 
+    import torch
+
     from oracle.reference import reference_attention_paged
 
     cores = min(os.cpu_count() or 1, 16)
-    qn, kvn = q.cpu().numpy(), kv.cpu().numpy()
+    as_np = lambda t: (t.float() if t.dtype == torch.bfloat16 else t).cpu().numpy()  # noqa: E731
+    qn, kvn = as_np(q), as_np(kv)
     ipn, idn, ln = indptr.cpu().numpy(), ids.cpu().numpy(), last.cpu().numpy()
     subset = list(range(min(sample, q.shape[0])))
     with threadpool_limits(limits=cores):
@@ -131,8 +139,26 @@ def main():
     B, ctx, hq, hkv, d = args.batch, args.ctx, 32, 8, 128
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table=args.page_table, seed=1)
+    kv_ref = kv                        # the cache's values for the CPU baseline
+    kv8 = args.kv_dtype == "fp8"
+    if kv8:
+        # random finite E4M3 codes of moderate magnitude (|value| <= 3.75), unit scales;
+        # the CPU baseline attends over the same values stored as fp16 (exact)
+        import numpy as np
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        codes = torch.randint(0, 0x48, kv.shape, generator=g, device=dev, dtype=torch.int32)
+        codes |= torch.randint(0, 2, kv.shape, generator=g, device=dev,
+                               dtype=torch.int32) * 0x80
+        codes = codes.to(torch.uint8)
+        from oracle import fp8 as fp8_oracle        # the CPU baseline's input only
+        table = torch.from_numpy(fp8_oracle.decode(np.arange(256)).astype(np.float32))
+        table = torch.nan_to_num(table).to(dev).to(dtype)
+        del kv
+        kv_ref = table[codes.long()]
+        kv = codes.view(attention.KV_FP8)
     split = attention.resolve_split(args.split)
-    nbytes = layout.attention_bytes(B, ctx, hq, hkv, d)
+    nbytes = layout.attention_bytes(B, ctx, hq, hkv, d, kv_elem_bytes=1 if kv8 else 0)
     out = torch.empty_like(q)
     ws_bytes = dk_lib.workspace_bytes(B, hq, hkv, d, split)
     p_total = dk_lib.partials_layout(B, hq, d, split)[3] if split else ws_bytes
@@ -149,7 +175,8 @@ def main():
     # plan step, outside the timed region: the longest sequence's page count from the host
     # side of the page table (what a serving framework keeps on the host)
     hint = 0 if args.no_plan_hint else attention.plan_hint(indptr.cpu())
-    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule, hint)
+    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule, hint,
+                          kv_dtype=dk_lib.DK_KV_FP8_E4M3 if kv8 else dk_lib.DK_KV_SAME)
     code = attention._DTYPE_CODE[dtype]
     # the schedule the full call runs (split_kv 0 resolves on the device's CU count)
     eff = dk_lib.plan_schedule(B, hq, hkv, d, ids.shape[0], code, split, opts)
@@ -210,7 +237,9 @@ def main():
         "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
         "config": {"workload": f"paged decode attention B={B} ctx={ctx} Hq={hq} Hkv={hkv} "
-                               f"D={d} {args.dtype} page_size=16 {args.page_table} pages",
+                               f"D={d} {args.dtype}{' (fp8 E4M3 cache)' if kv8 else ''} "
+                               f"page_size=16 {args.page_table} pages",
+                   "kv_dtype": "fp8_e4m3" if kv8 else args.dtype,
                    "batch": B, "context_length": ctx, "num_q_heads": hq, "num_kv_heads": hkv,
                    "head_dim": d, "page_size": 16,
                    "split_kv": split,
@@ -224,12 +253,12 @@ def main():
         "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": read_traffic(),
+                     "traffic": read_traffic(args.kv_dtype),
                      "kernel": "dk_pass1_balanced" if eff == 0 else "dk_pass1_split"},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        us, cores, n, err = cpu_baseline(q, kv, indptr, ids, last, out, args.cpu_sample)
+        us, cores, n, err = cpu_baseline(q, kv_ref, indptr, ids, last, out, args.cpu_sample)
         rec["cpu_baseline"] = {
             "value": round(us, 1), "unit": "us/call", "cores": cores, "kind": "port",
             "tb_s": round(nbytes / (us * 1e-6) / 1e12, 5),

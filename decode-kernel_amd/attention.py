@@ -11,7 +11,8 @@ are provided too, behind `get_hip_ext()` (the counterpart of `get_cuda_ext()`,
 src/cuda_/build.py:256). Every call goes to libdk_decode.so (HIP, gfx950); there is no
 PyTorch or CPU fallback, and a missing library raises ImportError.
 
-Differences from the reference, all extensions: bf16 as well as fp16; any split_kv >= 1
+Differences from the reference, all extensions: bf16 as well as fp16; an fp8 (E4M3) cache
+under fp16/bf16 queries, with per-tensor k_scale / v_scale; any split_kv >= 1
 (the reference allows 1..32), and split_kv=0 or None selects the balanced mode, in which
 a persistent grid gives every wavefront an equal share of all (sequence, kv head, page)
 work whatever the sequence lengths; work runs on torch's current stream of q's device
@@ -32,6 +33,7 @@ from dk_lib import DecodeArgumentError
 PAGE_SIZE = 16
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 _DTYPE_CODE = {torch.float16: dk_lib.DK_F16, torch.bfloat16: dk_lib.DK_BF16}
+KV_FP8 = torch.float8_e4m3fn            # OCP E4M3: the fp8 cache format the kernel reads
 
 
 def _fail(msg: str) -> None:
@@ -85,8 +87,9 @@ def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
         _fail(f"q must be fp16 or bf16, got {q.dtype}")
     if q.dim() != 3:
         _fail(f"q must be 3-D (batch, num_q_heads, head_dim), got shape {tuple(q.shape)}")
-    if kv.dtype != q.dtype:
-        _fail(f"kv_data dtype {kv.dtype} must match q dtype {q.dtype}")
+    if kv.dtype != q.dtype and kv.dtype != KV_FP8:
+        _fail(f"kv_data dtype {kv.dtype} must match q dtype {q.dtype} (or be "
+              f"torch.float8_e4m3fn)")
     if kv.page_size != PAGE_SIZE:
         _fail(f"page_size must be 16 for the HIP kernel, got {kv.page_size}")
     if q.shape[2] != kv.d:
@@ -117,6 +120,22 @@ def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
 
 def _contig1d(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
+
+
+def _kv_options(kv, k_scale, v_scale):
+    """(kv_dtype, k_scale, v_scale) for dk_options: an fp8 cache takes positive finite
+    per-tensor scales (default 1); a cache of q's type takes none."""
+    if kv.dtype != KV_FP8:
+        if k_scale not in (None, 1.0) or v_scale not in (None, 1.0):
+            _fail("k_scale / v_scale apply to a torch.float8_e4m3fn cache only")
+        return dk_lib.DK_KV_SAME, 0.0, 0.0
+    scales = []
+    for name, x in (("k_scale", k_scale), ("v_scale", v_scale)):
+        x = 1.0 if x is None else float(x)
+        if not math.isfinite(x) or x <= 0.0:
+            _fail(f"{name} must be finite and > 0, got {x}")
+        scales.append(x)
+    return dk_lib.DK_KV_FP8_E4M3, scales[0], scales[1]
 
 
 def _strides(q, kv_data, out) -> dk_lib.DkStrides:
@@ -175,14 +194,17 @@ def decode_attention(
     schedule: int = 0,
     max_pages_per_seq: int = 0,
     sm_scale: Optional[float] = None,
+    k_scale: Optional[float] = None,
+    v_scale: Optional[float] = None,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
     Args:
         q                : (batch, num_q_heads, head_dim), fp16 or bf16, on a GPU
-        kv_data          : (num_pages, 2, 16, num_kv_heads, head_dim), q's dtype (NHD), or
-                           a (k_cache, v_cache) pair of (num_pages, 16, num_kv_heads,
-                           head_dim) tensors with equal strides
+        kv_data          : (num_pages, 2, 16, num_kv_heads, head_dim), q's dtype or
+                           torch.float8_e4m3fn (NHD), or a (k_cache, v_cache) pair of
+                           (num_pages, 16, num_kv_heads, head_dim) tensors with equal
+                           strides
         kv_indptr        : (batch + 1,) int32 CSR row pointer into kv_indices
         kv_indices       : (kv_indptr[-1],) int32 physical page ids
         kv_last_page_len : (batch,) int32 valid tokens in each sequence's last page
@@ -199,6 +221,8 @@ def decode_attention(
         max_pages_per_seq: plan hint for split_kv 0 (see plan_hint): the longest
                            sequence's page count, 0 = unknown. Affects speed only.
         sm_scale         : softmax scale; None = 1/sqrt(head_dim) as in the reference
+        k_scale, v_scale : fp8 cache only: K = k_scale * fp8 value, V = v_scale * fp8 value
+                           (per tensor; None = 1)
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
@@ -206,6 +230,7 @@ def decode_attention(
     kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
     if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale == 0.0):
         _fail(f"sm_scale must be finite and non-zero, got {sm_scale}")
+    kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
     lib = dk_lib.load()
     split = resolve_split(split_kv)
     batch, hq, d = q.shape
@@ -230,7 +255,7 @@ def decode_attention(
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
     opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
-                          sm_scale or 0.0)
+                          sm_scale or 0.0, kv_dtype, k_sc, v_sc)
     shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
              _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts))
     tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
@@ -248,13 +273,16 @@ def decode_attention(
 
 
 def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv: int,
-                    *, qk_path: int = 0, waves_per_group: int = 0):
+                    *, qk_path: int = 0, waves_per_group: int = 0,
+                    k_scale: Optional[float] = None, v_scale: Optional[float] = None):
     """Pass 1 only. Returns (partial_O (B,Hq,S,D), partial_m (B,Hq,S), partial_l (B,Hq,S)),
     fp32, with the semantics of the reference partition kernel
     (src/cuda_/attention_ext.cu:207-349): m is the split's max of q.k*scale (-1e9 when the
     split is empty), l = sum exp(score - m), O = sum exp(score - m) * V (unnormalised)."""
-    if _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len).v is not None:
+    kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+    if kv.v is not None:
         _fail("decode_partials takes the combined (num_pages, 2, 16, Hkv, D) cache")
+    kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
     lib = dk_lib.load()
     split = choose_split(q, kv_data, kv_indices) if split_kv in (None, 0) else \
         resolve_split(split_kv)
@@ -262,7 +290,8 @@ def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_k
     off_o, off_m, off_l, total = dk_lib.partials_layout(batch, hq, d, split)
     ws = torch.empty(total, dtype=torch.uint8, device=q.device)
     strides = _strides(q, kv_data, None)
-    opts = dk_lib.options(qk_path, waves_per_group)
+    opts = dk_lib.options(qk_path, waves_per_group, kv_dtype=kv_dtype, k_scale=k_sc,
+                          v_scale=v_sc)
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.dk_decode_partials(

@@ -36,6 +36,9 @@ int cu_count(int device) {
 }
 
 const void* pass1_fn(int dtype, const Plan& pl, int d) {
+  if (pl.kv8)
+    return dtype == DK_F16 ? pass1_symbol_kv8<F16>(d, pl.heads, pl.waves, pl.balanced)
+                           : pass1_symbol_kv8<BF16>(d, pl.heads, pl.waves, pl.balanced);
   return dtype == DK_F16 ? pass1_symbol<F16>(d, pl.heads, pl.waves, pl.mfma, pl.balanced)
                          : pass1_symbol<BF16>(d, pl.heads, pl.waves, pl.mfma, pl.balanced);
 }
@@ -63,9 +66,11 @@ int explicit_split(const Problem& p, int device) {
 }
 
 // Wavefronts per compute unit the balanced schedule keeps resident. Two measured best on
-// MI355X at every decode shape tried (each wavefront keeps two pages of loads in flight).
+// MI355X at every decode shape tried with a 16-bit cache (each wavefront keeps two pages
+// of loads in flight); four with an fp8 cache.
 int waves_per_cu(const Problem& p) {
-  return p.opt.waves_per_cu ? p.opt.waves_per_cu : kDefaultWavesPerCU;
+  if (p.opt.waves_per_cu) return p.opt.waves_per_cu;
+  return p.opt.kv_dtype == DK_KV_FP8_E4M3 ? kDefaultWavesPerCUKv8 : kDefaultWavesPerCU;
 }
 
 // Workgroups of the balanced grid: about waves_per_cu wavefronts per compute unit, a
@@ -117,7 +122,8 @@ int run(Problem p, bool do_merge, void* stream) {
     }
   }
   const bool direct = p.need_out && (p.split == 1 || pl.balanced);
-  const int64_t esize = 2;
+  const int64_t esize = 2;              // q and out
+  const int64_t kes = p.kv_esize();     // the cache
 
   Pass1Args a{};
   a.q = static_cast<const uint8_t*>(p.q);
@@ -142,14 +148,14 @@ int run(Problem p, bool do_merge, void* stream) {
   a.out = static_cast<uint8_t*>(p.out);
   a.q_b = p.st.q_b * esize;
   a.q_h = p.st.q_h * esize;
-  a.kv_p = p.st.kv_p * esize;
+  a.kv_p = p.st.kv_p * kes;
   a.o_b = p.st.o_b * esize;
   a.o_h = p.st.o_h * esize;
   // V slice of a page: kv_r further in the combined cache, or the same offset in the
   // separate V cache
-  a.kv_v = p.v ? (int64_t)((const uint8_t*)p.v - (const uint8_t*)p.kv) : p.st.kv_r * esize;
-  a.kv_s = (int32_t)(p.st.kv_s * esize);
-  a.kv_h = (int32_t)(p.st.kv_h * esize);
+  a.kv_v = p.v ? (int64_t)((const uint8_t*)p.v - (const uint8_t*)p.kv) : p.st.kv_r * kes;
+  a.kv_s = (int32_t)(p.st.kv_s * kes);
+  a.kv_h = (int32_t)(p.st.kv_h * kes);
   a.batch = p.batch;
   a.hq = p.hq;
   a.hkv = p.hkv;
@@ -159,9 +165,13 @@ int run(Problem p, bool do_merge, void* stream) {
   a.num_indices = (int32_t)p.num_indices;
   a.num_pages = (uint32_t)std::min<int64_t>(p.num_pages, (int64_t)1 << 31);
   // bytes from a kv head's K (or V) slice base that its rows reach (validated < 2^31)
-  a.page_extent = (uint32_t)(((int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * esize);
+  a.page_extent = (uint32_t)(((int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * kes);
   a.direct = direct ? 1 : 0;
-  a.kscale = kLog2e * (p.opt.sm_scale != 0.f ? p.opt.sm_scale : 1.f / sqrtf((float)p.head_dim));
+  const bool kv8 = pl.kv8;
+  const float k_scale = kv8 && p.opt.k_scale != 0.f ? p.opt.k_scale : 1.f;
+  a.kscale = kLog2e * k_scale *
+             (p.opt.sm_scale != 0.f ? p.opt.sm_scale : 1.f / sqrtf((float)p.head_dim));
+  a.vscale = kv8 && p.opt.v_scale != 0.f ? p.opt.v_scale : 1.f;
   // every launch that can store partials has them (or the library is inconsistent)
   if ((pl.balanced || !direct) && (!a.part_o || !a.part_m || !a.part_l))
     return set_error(DK_EWORKSPACE, "internal: partials not assigned for this schedule");
@@ -172,6 +182,7 @@ int run(Problem p, bool do_merge, void* stream) {
   L.waves = pl.waves;
   L.mfma = pl.mfma;
   L.balanced = pl.balanced;
+  L.kv8 = pl.kv8;
   L.grid = (int)pl.grid;
   L.stream = static_cast<hipStream_t>(stream);
   hipError_t e = p.dtype == DK_F16 ? launch_pass1<F16>(a, L) : launch_pass1<BF16>(a, L);

@@ -92,10 +92,13 @@ Plan make_plan(const Problem& p) {
   pl.heads = heads_per_group(pl.group, p.head_dim);
   pl.chunks = pl.group / pl.heads;
   pl.pairs_per_seq = p.hkv * pl.chunks;
-  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group : kDefaultWavesPerGroup;
+  const bool kv8 = p.opt.kv_dtype == DK_KV_FP8_E4M3;
+  pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group
+                                   : (kv8 ? kDefaultWavesPerGroupKv8 : kDefaultWavesPerGroup);
   // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
   // 64-byte row segments on the NHD layout (measured for both fp16 and bf16)
   pl.mfma = p.opt.qk_path == 1;
+  pl.kv8 = kv8;
   pl.balanced = p.split == 0;
   pl.grid = pl.balanced ? 0 : (int64_t)p.batch * pl.pairs_per_seq * std::max(p.split, 1);
   return pl;
@@ -140,6 +143,16 @@ int validate(const Problem& p) {
                      o.max_pages_per_seq);
   if (!std::isfinite(o.sm_scale))
     return set_error(DK_EINVAL, "options.sm_scale must be finite (0 = 1/sqrt(head_dim))");
+  if (o.kv_dtype != DK_KV_SAME && o.kv_dtype != DK_KV_FP8_E4M3)
+    return set_error(DK_EINVAL, "options.kv_dtype must be DK_KV_SAME or DK_KV_FP8_E4M3; got %d",
+                     o.kv_dtype);
+  if (!std::isfinite(o.k_scale) || !std::isfinite(o.v_scale) || o.k_scale < 0 ||
+      o.v_scale < 0)
+    return set_error(DK_EINVAL, "options.k_scale and v_scale must be finite and >= 0");
+  if (o.kv_dtype == DK_KV_SAME && (o.k_scale != 0.f || o.v_scale != 0.f))
+    return set_error(DK_EINVAL, "options.k_scale and v_scale apply to an fp8 cache only");
+  if (o.kv_dtype == DK_KV_FP8_E4M3 && o.qk_path == 1)
+    return set_error(DK_EUNSUPPORTED, "an fp8 cache supports the VALU q.k path only");
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything
@@ -159,13 +172,13 @@ int validate(const Problem& p) {
   const int64_t all[] = {s.q_b, s.q_h, s.kv_p, kv_r, s.kv_s, s.kv_h, s.o_b, s.o_h};
   for (int64_t v : all)
     if (v < 0) return set_error(DK_EINVAL, "strides must be non-negative");
-  const int64_t esize = 2;
-  auto aligned16 = [](int64_t elems) { return (elems * 2) % 16 == 0; };
-  if (!aligned16(s.q_b) || !aligned16(s.q_h) || !aligned16(s.kv_p) || !aligned16(kv_r) ||
-      !aligned16(s.kv_s) || !aligned16(s.kv_h))
+  const int64_t esize = p.kv_esize();
+  auto aligned16 = [](int64_t elems, int64_t es) { return (elems * es) % 16 == 0; };
+  if (!aligned16(s.q_b, 2) || !aligned16(s.q_h, 2) || !aligned16(s.kv_p, esize) ||
+      !aligned16(kv_r, esize) || !aligned16(s.kv_s, esize) || !aligned16(s.kv_h, esize))
     return set_error(DK_EUNSUPPORTED,
-                     "q and kv_data strides must be multiples of 8 elements (16-byte rows); "
-                     "pass contiguous tensors");
+                     "q and kv_data strides must be multiples of 16 bytes (8 fp16/bf16 or 16 "
+                     "fp8 elements); pass contiguous tensors");
   if (((uintptr_t)p.q % 16) != 0 || ((uintptr_t)p.kv % 16) != 0 ||
       ((uintptr_t)p.v % 16) != 0)
     return set_error(DK_EUNSUPPORTED, "q and the K/V caches must be 16-byte aligned");

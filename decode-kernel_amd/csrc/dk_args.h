@@ -14,6 +14,11 @@ constexpr int kPageSize = 16;        // tokens per page (reference: PAGE_SIZE=16
 constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid (wavefronts)
 constexpr int kDefaultWavesPerCU = 2;
 constexpr int kDefaultWavesPerGroup = 2;
+// An fp8 page carries half the bytes for the same per-token arithmetic, so one wavefront
+// per SIMD is needed to keep HBM busy (measured: 93 us with 4 wavefronts per group vs
+// 162 us with 2 at B=32 ctx=8192 32/8/128)
+constexpr int kDefaultWavesPerCUKv8 = 4;
+constexpr int kDefaultWavesPerGroupKv8 = 4;
 
 // Everything a launch needs that is known on the host.
 struct Problem {
@@ -28,6 +33,7 @@ struct Problem {
   size_t workspace_bytes = 0;
   int32_t batch = 0, hq = 0, hkv = 0, head_dim = 0, page_size = 0, dtype = 0;
   int64_t num_pages = 0, num_indices = 0;
+  int32_t kv_esize() const { return opt.kv_dtype == DK_KV_FP8_E4M3 ? 1 : 2; }
   dk_strides st{};
   int32_t split = 0;          // 0: balanced persistent mode; >= 1: explicit split
   bool need_out = true;       // false for the pass-1-only entry point
@@ -43,6 +49,7 @@ struct Plan {
   int waves = 0;       // wavefronts per workgroup
   bool mfma = false;   // q.k on MFMA (default: VALU dot2)
   bool balanced = false;
+  bool kv8 = false;    // fp8 cache
   int64_t grid = 0;    // workgroups of pass 1 (balanced: filled in from the device)
 };
 

@@ -91,7 +91,8 @@ struct Pass1Args {
   uint32_t page_extent;               // bytes one kv head's K (or V) rows of a page span (< 2^31)
   int32_t direct;                     // explicit split 1 / balanced: may write the
                                       // normalised output (0: partials only)
-  float kscale;                       // log2(e) / sqrt(head_dim)
+  float kscale;                       // log2(e) * softmax scale (* K dequant scale)
+  float vscale;                       // V dequant scale (1 unless the cache is fp8)
 };
 
 struct MergeArgs {
@@ -118,6 +119,11 @@ struct F16 {
   static __device__ __forceinline__ void store(uint8_t* p, float x) {
     *reinterpret_cast<_Float16*>(p) = (_Float16)x;
   }
+  // two fp8 (E4M3) values, bytes 2*HI and 2*HI+1 of w, widened exactly to an f16 pair
+  template <bool HI>
+  static __device__ __forceinline__ u32 from_fp8(u32 w) {
+    return __builtin_bit_cast(u32, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
   static __device__ __forceinline__ f32x4 mfma_pv(u32x2 a, u32x2 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
                                                  __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
@@ -138,6 +144,10 @@ struct BF16 {
   static __device__ __forceinline__ float dot2(u32 a, u32 b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
                                            __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  template <bool HI>
+  static __device__ __forceinline__ u32 from_fp8(u32 w) {
+    return __builtin_bit_cast(u32, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
   }
   // C += A.B with A 16x16 (rows: lane%16, k: 4 per lane), B 16x16 (k: 4 per lane, cols:
   // lane%16), 4 bf16 per lane in two words each
@@ -257,7 +267,9 @@ constexpr int kBufNT = 2;   // buffer-load cache policy: non-temporal (streamed 
 // NWORDS consecutive words at base + voff + soff (NWORDS in {2, 4, 8}), streaming.
 template <int NWORDS>
 __device__ __forceinline__ void ld_buf(u32* dst, __amdgpu_buffer_rsrc_t r, u32 voff, u32 soff) {
-  if constexpr (NWORDS == 2) {
+  if constexpr (NWORDS == 1) {
+    dst[0] = (u32)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kBufNT);
+  } else if constexpr (NWORDS == 2) {
     const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, kBufNT));
     dst[0] = v[0];
     dst[1] = v[1];
@@ -296,8 +308,11 @@ __device__ __forceinline__ int seq_begin(const Pass1Args& a, int b) {
 }
 
 // ---------------------------------------------------------------- per-wavefront decoder
-template <class T, int D, int G, bool MFMA>
+// T: element type of q and out (and of the cache unless KV8); KV8: the cache holds fp8
+// (E4M3) values, widened to T in registers after the loads.
+template <class T, int D, int G, bool MFMA, bool KV8 = false>
 struct Wave {
+  static_assert(!(MFMA && KV8), "fp8 pages use the VALU q.k layout");
   static constexpr int GQ = G < 4 ? G : 4;   // heads per column set
   static constexpr int NS = G / GQ;          // column sets (G = 8 -> 2)
   static constexpr int DPL = D / 16;         // V (and VALU-path K) dims per lane
@@ -305,11 +320,14 @@ struct Wave {
   static constexpr int KW = D / 8;           // K words per lane per page (both paths)
   static constexpr int VW = 4 * VWT;         // V words per lane per page
   static constexpr int NMF = D / 32;         // MFMAs per head set per page
+  static constexpr int KB = KV8 ? D / 16 : KW;   // words of a page buffer as loaded (K)
+  static constexpr int VB = KV8 ? D / 16 : VW;   // (V)
+  static constexpr int EB = KV8 ? 1 : 2;         // bytes per cache element
 
   int r16, c;
   u32 koff, voff, tok_s, extent;
   int64_t kv_v;
-  float kscale;
+  float kscale, vscale;
   u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, dims 32i+8r16..
   u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
   float acc[G][DPL];      // after reduce_rows: head h, dim c*DPL + j (every lane row)
@@ -322,11 +340,12 @@ struct Wave {
     r16 = lane >> 4;
     c = lane & 15;
     tok_s = (u32)a.kv_s;
-    koff = MFMA ? (u32)(c * a.kv_s + 16 * r16) : (u32)(4 * r16 * a.kv_s + 2 * DPL * c);
-    voff = (u32)(4 * r16 * a.kv_s + 2 * DPL * c);
+    koff = MFMA ? (u32)(c * a.kv_s + 16 * r16) : (u32)(4 * r16 * a.kv_s + EB * DPL * c);
+    voff = (u32)(4 * r16 * a.kv_s + EB * DPL * c);
     extent = a.page_extent;
     kv_v = a.kv_v;
     kscale = a.kscale;
+    vscale = a.vscale;
   }
 
   // q rows of the G heads starting at qbase (q_h bytes apart).
@@ -360,20 +379,39 @@ struct Wave {
   // pg: base of this kv head's slice of a page (page base + kvh * kv_h). Buffer loads:
   // the address is the page base (scalar) + a per-lane offset + a per-row scalar offset.
   // live == false: a zero-extent descriptor, the loads return zeros without touching memory
-  __device__ __forceinline__ void load_page(u32 (&kb)[KW], u32 (&vb)[VW], const uint8_t* pg,
+  __device__ __forceinline__ void load_page(u32 (&kb)[KB], u32 (&vb)[VB], const uint8_t* pg,
                                             bool live = true) const {
     const u32 ext = live ? extent : 0u;
     const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, ext);
     const __amdgpu_buffer_rsrc_t rv = page_rsrc(pg + kv_v, ext);
+    constexpr int TW = KB / 4;   // words per token per lane as loaded
     if constexpr (MFMA) {
 #pragma unroll
       for (int i = 0; i < NMF; ++i) ld_buf<4>(&kb[4 * i], rk, koff, 64 * i);
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ld_buf<VWT>(&kb[r * VWT], rk, koff, r * tok_s);
+      for (int r = 0; r < 4; ++r) ld_buf<TW>(&kb[r * TW], rk, koff, r * tok_s);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ld_buf<VWT>(&vb[r * VWT], rv, voff, r * tok_s);
+    for (int r = 0; r < 4; ++r) ld_buf<TW>(&vb[r * TW], rv, voff, r * tok_s);
+  }
+
+  // One loaded page: fp8 buffers are widened to T pairs first (word u of a token's fp8
+  // dims 4u..4u+3 becomes words 2u, 2u+1), then compute_page.
+  __device__ __forceinline__ void consume(const u32 (&kb)[KB], u32 (&vb)[VB], int valid) {
+    if constexpr (KV8) {
+      u32 kw[KW], vw[VW];
+#pragma unroll
+      for (int i = 0; i < KB; ++i) {
+        kw[2 * i] = T::template from_fp8<false>(kb[i]);
+        kw[2 * i + 1] = T::template from_fp8<true>(kb[i]);
+        vw[2 * i] = T::template from_fp8<false>(vb[i]);
+        vw[2 * i + 1] = T::template from_fp8<true>(vb[i]);
+      }
+      compute_page(kw, vw, valid);
+    } else {
+      compute_page(kb, vb, valid);
+    }
   }
 
   // Scores of tokens 4*r16 + r for head ss*GQ + c%GQ from per-lane partials of the G
@@ -533,7 +571,7 @@ struct Wave {
 #pragma unroll
       for (int g = 0; g < GQ; ++g)
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] = cv[ss][j][g];
+        for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] = cv[ss][j][g] * vscale;
   }
 
   // After reduce_rows every lane holds every head's sums. Lane row r16 stores heads
@@ -627,14 +665,26 @@ struct Wave {
 #ifndef DK_PREFETCH_DEPTH
 #define DK_PREFETCH_DEPTH 0
 #endif
-template <int D>
-constexpr int prefetch_depth() { return DK_PREFETCH_DEPTH ? DK_PREFETCH_DEPTH : (D <= 128 ? 2 : 1); }
+#ifndef DK_PREFETCH_DEPTH_KV8
+#define DK_PREFETCH_DEPTH_KV8 0
+#endif
+// Pages in flight per wavefront. An fp8 page is half the bytes of a 16-bit one, so the
+// fp8 path keeps twice the pages in flight for the same bytes (and the same registers).
+template <int D, bool KV8>
+constexpr int prefetch_depth() {
+  if constexpr (KV8)
+    return DK_PREFETCH_DEPTH_KV8 ? DK_PREFETCH_DEPTH_KV8 : (D <= 128 ? 4 : 2);
+  else
+    return DK_PREFETCH_DEPTH ? DK_PREFETCH_DEPTH : (D <= 128 ? 2 : 1);
+}
 
 // Resident wavefronts per SIMD the register allocator is held to: the page buffers
-// (D/4 words each), G*D/16 accumulators and the q operand must fit without spilling.
-template <int D, int G>
+// (D/8 words per page for 16-bit elements, D/16 for fp8), G*D/16 accumulators and the q
+// operand must fit without spilling.
+template <int D, int G, bool KV8>
 constexpr int min_waves_per_simd() {
-  return (D >= 256 || prefetch_depth<D>() > 2) ? 1 : (D * G >= 1024 ? 1 : 2);
+  constexpr int buffer_words = (prefetch_depth<D, KV8>() + 1) * (KV8 ? D / 16 : D / 8);
+  return (D >= 256 || buffer_words > 3 * 128 / 8) ? 1 : (D * G >= 1024 ? 1 : 2);
 }
 
 // Pages [first, first + n) of one (sequence, kv head), streamed through register buffers:
@@ -645,43 +695,43 @@ constexpr int min_waves_per_simd() {
 // hold (or be loading) page 0; page(i) is the base address of page i, valid(i) its valid
 // token count.
 template <int DEPTH, class W, class PageFn, class ValidFn>
-__device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KW], u32 (&va)[W::VW],
+__device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[W::VB],
                                              int n, PageFn page, ValidFn valid) {
-  u32 kb[W::KW], vb[W::VW];
+  u32 kb[W::KB], vb[W::VB];
   if constexpr (DEPTH == 1) {
     int k = 0;
     for (; k + 2 < n; k += 2) {
       wv.load_page(kb, vb, page(k + 1));
-      wv.compute_page(ka, va, valid(k));
+      wv.consume(ka, va, valid(k));
       wv.load_page(ka, va, page(k + 2));
-      wv.compute_page(kb, vb, valid(k + 1));
+      wv.consume(kb, vb, valid(k + 1));
     }
     if (k + 1 < n) {
       wv.load_page(kb, vb, page(k + 1));
-      wv.compute_page(ka, va, valid(k));
-      wv.compute_page(kb, vb, valid(k + 1));
+      wv.consume(ka, va, valid(k));
+      wv.consume(kb, vb, valid(k + 1));
     } else if (k < n) {
-      wv.compute_page(ka, va, valid(k));
+      wv.consume(ka, va, valid(k));
     }
   } else {
-    u32 kc[W::KW], vc[W::VW];
+    u32 kc[W::KB], vc[W::VB];
     if (n > 1) wv.load_page(kb, vb, page(1));
     int k = 0;
     for (; k + 4 < n; k += 3) {
       wv.load_page(kc, vc, page(k + 2));
-      wv.compute_page(ka, va, valid(k));
+      wv.consume(ka, va, valid(k));
       wv.load_page(ka, va, page(k + 3));
-      wv.compute_page(kb, vb, valid(k + 1));
+      wv.consume(kb, vb, valid(k + 1));
       wv.load_page(kb, vb, page(k + 4));
-      wv.compute_page(kc, vc, valid(k + 2));
+      wv.consume(kc, vc, valid(k + 2));
     }
     const int r = n - k;   // 1..4 pages left; buffers a, b hold pages k, k+1
     if (r >= 3) wv.load_page(kc, vc, page(k + 2));
-    if (r >= 1) wv.compute_page(ka, va, valid(k));
+    if (r >= 1) wv.consume(ka, va, valid(k));
     if (r >= 4) wv.load_page(ka, va, page(k + 3));
-    if (r >= 2) wv.compute_page(kb, vb, valid(k + 1));
-    if (r >= 3) wv.compute_page(kc, vc, valid(k + 2));
-    if (r >= 4) wv.compute_page(ka, va, valid(k + 3));
+    if (r >= 2) wv.consume(kb, vb, valid(k + 1));
+    if (r >= 3) wv.consume(kc, vc, valid(k + 2));
+    if (r >= 4) wv.consume(ka, va, valid(k + 3));
   }
 }
 
@@ -692,7 +742,7 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KW], u32 (&va)[
 template <int DEPTH, class W, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_ring(W& wv, int n, PageFn page, ValidFn valid) {
   constexpr int NB = DEPTH + 1;
-  u32 kb[NB][W::KW], vb[NB][W::VW];
+  u32 kb[NB][W::KB], vb[NB][W::VB];
 #pragma unroll
   for (int j = 0; j < DEPTH; ++j) wv.load_page(kb[j], vb[j], page(min(j, n - 1)), j < n);
   for (int k = 0; k < n; k += NB) {
@@ -700,7 +750,7 @@ __device__ __forceinline__ void stream_ring(W& wv, int n, PageFn page, ValidFn v
     for (int j = 0; j < NB; ++j) {
       const int ld = k + j + DEPTH;
       wv.load_page(kb[(j + DEPTH) % NB], vb[(j + DEPTH) % NB], page(min(ld, n - 1)), ld < n);
-      if (k + j < n) wv.compute_page(kb[j], vb[j], valid(k + j));
+      if (k + j < n) wv.consume(kb[j], vb[j], valid(k + j));
     }
   }
 }
@@ -775,27 +825,28 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
 }
 
 // Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages.
-template <int D, class WV, class PageFn, class ValidFn>
+template <int D, bool KV8, class WV, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n, PageFn page,
                                                    ValidFn valid) {
   const int nk = n > w ? (n - w + NW - 1) / NW : 0;
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
-    if constexpr (prefetch_depth<D>() <= 2) {
-      u32 ka[WV::KW], va[WV::VW];
+    constexpr int depth = prefetch_depth<D, KV8>();
+    if constexpr (depth <= 2) {
+      u32 ka[WV::KB], va[WV::VB];
       wv.load_page(ka, va, pk(0));
-      stream_pages<prefetch_depth<D>()>(wv, ka, va, nk, pk, vk);
+      stream_pages<depth>(wv, ka, va, nk, pk, vk);
     } else {
-      stream_ring<prefetch_depth<D>()>(wv, nk, pk, vk);
+      stream_ring<depth>(wv, nk, pk, vk);
     }
   }
 }
 
 // ---------------------------------------------------------------- pass 1, explicit split
-template <class T, int D, int G, int NW, bool MFMA>
-__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_split(Pass1Args a) {
-  using WV = Wave<T, D, G, MFMA>;
+template <class T, int D, int G, int NW, bool MFMA, bool KV8>
+__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_split(Pass1Args a) {
+  using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
   WV wv;
   wv.init(a);
@@ -826,7 +877,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
     return kvh_base + (int64_t)pid * a.kv_p;
   };
   auto valid = [&](int i) -> int { return p0 + i == npages - 1 ? valid_last : kPage; };
-  stream_interleaved<D>(wv, NW, w, n, page, valid);
+  stream_interleaved<D, KV8>(wv, NW, w, n, page, valid);
   wv.reduce_rows();
   combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
@@ -844,9 +895,9 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
 // by a single segment is written out directly (when a.direct); otherwise the segment is
 // stored as a partial at slot hc * (Wg + batch) + j + b (unique, < HC * (Wg + batch)) for the
 // merge kernel.
-template <class T, int D, int G, int NW, bool MFMA>
-__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass1_balanced(Pass1Args a) {
-  using WV = Wave<T, D, G, MFMA>;
+template <class T, int D, int G, int NW, bool MFMA, bool KV8>
+__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_balanced(Pass1Args a) {
+  using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
   WV wv;
   wv.init(a);
@@ -892,7 +943,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G>())) void dk_pass
       return kvh_base + (int64_t)pid * a.kv_p;
     };
     auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
-    stream_interleaved<D>(wv, NW, w, n, page, valid);
+    stream_interleaved<D, KV8>(wv, NW, w, n, page, valid);
     wv.reduce_rows();
 
     const int start = seq0 - base;

@@ -17,7 +17,9 @@ LIB_PATH = Path(os.environ.get("DK_DECODE_LIB", HERE / "libdk_decode.so"))
 
 DK_F16 = 0
 DK_BF16 = 1
-ABI_VERSION = 1
+DK_KV_SAME = 0
+DK_KV_FP8_E4M3 = 2
+ABI_VERSION = 2
 
 DK_OK = 0
 DK_EINVAL = -1
@@ -48,7 +50,8 @@ class DkOptions(ctypes.Structure):
     _fields_ = [("qk_path", ctypes.c_int32), ("waves_per_group", ctypes.c_int32),
                 ("waves_per_cu", ctypes.c_int32), ("schedule", ctypes.c_int32),
                 ("max_pages_per_seq", ctypes.c_int32), ("sm_scale", ctypes.c_float),
-                ("reserved", ctypes.c_int32 * 2)]
+                ("kv_dtype", ctypes.c_int32), ("k_scale", ctypes.c_float),
+                ("v_scale", ctypes.c_float), ("reserved", ctypes.c_int32 * 3)]
 
 
 _P = ctypes.c_void_p
@@ -166,9 +169,13 @@ SCHEDULE_ONE_PASS = 2
 
 def options(qk_path: int = 0, waves_per_group: int = 0, waves_per_cu: int = 0,
             schedule: int = SCHEDULE_AUTO, max_pages_per_seq: int = 0,
-            sm_scale: float = 0.0) -> DkOptions:
+            sm_scale: float = 0.0, kv_dtype: int = DK_KV_SAME, k_scale: float = 0.0,
+            v_scale: float = 0.0) -> DkOptions:
     o = DkOptions()
     o.sm_scale = sm_scale
+    o.kv_dtype = kv_dtype
+    o.k_scale = k_scale
+    o.v_scale = v_scale
     o.qk_path = qk_path
     o.waves_per_group = waves_per_group
     o.waves_per_cu = waves_per_cu

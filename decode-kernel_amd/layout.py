@@ -162,12 +162,14 @@ def seq_lens(kv_indptr: torch.Tensor, kv_last_page_len: torch.Tensor, page_size:
 
 
 def attention_bytes(batch: int, context_length, num_q_heads: int, num_kv_heads: int,
-                    head_dim: int, elem_bytes: int = 2, page_size: int = 16) -> int:
+                    head_dim: int, elem_bytes: int = 2, page_size: int = 16,
+                    kv_elem_bytes: int = 0) -> int:
     """Algorithmic HBM bytes of one decode call: K and V of the valid tokens, q read and
     the output written (the reference's bytes model, bench/microbench_cuda.py:114-121),
-    plus the int32 page tables. `context_length` is an int or a per-sequence list."""
+    plus the int32 page tables. `context_length` is an int or a per-sequence list;
+    kv_elem_bytes is the cache's element size when it differs from q's (1 for fp8)."""
     lens = [context_length] * batch if isinstance(context_length, int) else list(context_length)
-    kv = sum(lens) * num_kv_heads * head_dim * elem_bytes * 2
+    kv = sum(lens) * num_kv_heads * head_dim * (kv_elem_bytes or elem_bytes) * 2
     qo = 2 * batch * num_q_heads * head_dim * elem_bytes
     tables = 4 * (batch + 1) + 4 * sum(math.ceil(n / page_size) for n in lens) + 4 * batch
     return kv + qo + tables

@@ -38,11 +38,17 @@
 extern "C" {
 #endif
 
-#define DK_ABI_VERSION 1
+#define DK_ABI_VERSION 2
 
 /* Element type of q / kv_data / out. The reference is fp16 only
  * (src/cuda_/attention_ext.cu:507,550); bf16 is an extension. */
 typedef enum { DK_F16 = 0, DK_BF16 = 1 } dk_dtype;
+
+/* Element type of the KV cache when it differs from q / out (dk_options.kv_dtype):
+ * OCP FP8 E4M3 (torch.float8_e4m3fn), dequantised as value * k_scale / v_scale. No
+ * counterpart in the reference (fp16 cache only). */
+#define DK_KV_SAME 0
+#define DK_KV_FP8_E4M3 2
 
 /* Error codes (< 0). */
 enum {
@@ -78,7 +84,12 @@ typedef struct {
                               Too small a value affects speed only, never results.       */
   float sm_scale;          /* softmax scale applied to q.k; 0 = 1/sqrt(head_dim), the
                               reference's fixed scale (attention_ext.cu:79-80)             */
-  int32_t reserved[2];     /* must be 0                                                     */
+  int32_t kv_dtype;        /* DK_KV_SAME (0): the cache has q's type; DK_KV_FP8_E4M3: fp8
+                              (strides still in elements, now bytes; VALU q.k only)       */
+  float k_scale;           /* fp8 cache: K = k_scale * stored value (0 = 1); must be 0
+                              for a cache of q's type                                     */
+  float v_scale;           /* fp8 cache: V = v_scale * stored value (0 = 1); likewise     */
+  int32_t reserved[3];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */

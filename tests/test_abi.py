@@ -99,6 +99,18 @@ def _call(lib, **kw):
     (dict(opts=dk_lib.options(waves_per_cu=40)), dk_lib.DK_EINVAL, "waves_per_cu"),
     (dict(opts=dk_lib.options(max_pages_per_seq=-1)), dk_lib.DK_EINVAL, "max_pages_per_seq"),
     (dict(opts=dk_lib.options(schedule=3)), dk_lib.DK_EINVAL, "schedule"),
+    (dict(opts=dk_lib.options(kv_dtype=1)), dk_lib.DK_EINVAL, "kv_dtype"),
+    (dict(opts=dk_lib.options(k_scale=2.0)), dk_lib.DK_EINVAL, "fp8 cache only"),
+    (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, v_scale=-1.0)),
+     dk_lib.DK_EINVAL, "v_scale"),
+    (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, k_scale=float("inf"))),
+     dk_lib.DK_EINVAL, "k_scale"),
+    (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, qk_path=1)),
+     dk_lib.DK_EUNSUPPORTED, "VALU"),
+    # an fp8 cache's strides are bytes: 8 elements is no longer a 16-byte row
+    (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3),
+          strides=dk_lib.DkStrides(32 * 128, 128, 2 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128 + 8,
+                                   128, 32 * 128, 128)), dk_lib.DK_EUNSUPPORTED, "strides"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(kw, code, needle):
     lib = dk_lib.load()
@@ -212,8 +224,9 @@ def test_plan_hint_reads_host_indptr_only():
 
 def test_options_struct_matches_header():
     # dk_options: qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq
-    # (int32), sm_scale (float), reserved[2] (int32): 32 bytes
-    assert ctypes.sizeof(dk_lib.DkOptions) == 32
+    # (int32), sm_scale (float), kv_dtype (int32), k_scale, v_scale (float), reserved[3]
+    # (int32): 48 bytes
+    assert ctypes.sizeof(dk_lib.DkOptions) == 48
     fields = [(f[0], f[1]) for f in dk_lib.DkOptions._fields_]
     hdr = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     body = hdr[hdr.index("int32_t qk_path"):hdr.index("} dk_options;")]

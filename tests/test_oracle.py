@@ -383,3 +383,54 @@ def test_planted_rope_sign_mistake_is_caught_by_transformers():
     bad[:, 4:] = x[:, 4:] * np.cos(ang) - x[:, :4] * np.sin(ang)
     assert np.abs(bad - _hf_rope(x, 9, inv)).max() > 1e-2
     np.testing.assert_allclose(oapp.rope(x, 9, inv), _hf_rope(x, 9, inv), atol=1e-12)
+
+
+# ---- fp8 (E4M3) cache format: oracle/fp8.py
+
+def test_fp8_known_answers():
+    from oracle import fp8
+    known = {0x38: 1.0, 0x7E: 448.0, 0xFE: -448.0, 0x08: 2.0 ** -6, 0x01: 2.0 ** -9,
+             0x07: 7 * 2.0 ** -9, 0x40: 2.0, 0x3C: 1.5, 0x00: 0.0, 0xB8: -1.0}
+    for code, want in known.items():
+        assert fp8.decode(code) == want, hex(code)
+    assert np.signbit(fp8.decode(0x80)) and fp8.decode(0x80) == 0.0
+    vals = fp8.decode(np.arange(256))
+    assert np.isnan(vals).sum() == 2 and np.isnan(vals[0x7F]) and np.isnan(vals[0xFF])
+    assert np.isfinite(vals).sum() == 254 and np.nanmax(vals) == 448.0
+    # the non-negative finite codes are monotone: encode's search relies on it
+    assert np.all(np.diff(vals[:0x7F]) > 0)
+
+
+def test_fp8_decode_matches_torch_all_codes():
+    from oracle import fp8
+    codes = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(codes).view(torch.float8_e4m3fn).double().numpy()
+    d = fp8.decode(codes)
+    fin = np.isfinite(t)
+    assert np.array_equal(np.isnan(t), np.isnan(d))
+    assert np.array_equal(t[fin], d[fin]) and np.array_equal(np.signbit(t[fin]),
+                                                             np.signbit(d[fin]))
+
+
+def test_fp8_encode_matches_torch_rounding():
+    from oracle import fp8
+    fin = np.unique(fp8.decode(np.arange(0x7F)))
+    mids = (fin[1:] + fin[:-1]) / 2                  # every tie
+    x = np.concatenate([fin, -fin, mids, -mids, np.linspace(-520, 520, 100001),
+                        np.array([448, 449, 463.9, 464, 464.1, 480, 1e9, -464, -470, np.nan,
+                                  -0.0, 2.0 ** -10, 2.0 ** -11, 3 * 2.0 ** -11])])
+    x = x.astype(np.float32)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(fp8.encode(x), want)
+    # round trip of every finite code
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    assert np.array_equal(fp8.encode(fp8.decode(codes)), codes)
+
+
+def test_planted_fp8_bias_mistake_is_caught_by_torch():
+    from oracle import fp8
+    codes = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(codes).view(torch.float8_e4m3fn).double().numpy()
+    wrong = fp8.decode(codes) * 2.0                  # exponent bias 6 instead of 7
+    fin = np.isfinite(t)
+    assert not np.array_equal(t[fin], wrong[fin])
