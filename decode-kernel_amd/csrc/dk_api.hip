@@ -36,11 +36,8 @@ int cu_count(int device) {
 }
 
 const void* pass1_fn(int dtype, const Plan& pl, int d) {
-  if (pl.kv8)
-    return dtype == DK_F16 ? pass1_symbol_kv8<F16>(d, pl.heads, pl.waves, pl.balanced)
-                           : pass1_symbol_kv8<BF16>(d, pl.heads, pl.waves, pl.balanced);
-  return dtype == DK_F16 ? pass1_symbol<F16>(d, pl.heads, pl.waves, pl.mfma, pl.balanced)
-                         : pass1_symbol<BF16>(d, pl.heads, pl.waves, pl.mfma, pl.balanced);
+  return dtype == DK_F16 ? pass1_symbol<F16>(d, pl.heads, pl.waves, pl.mfma, pl.kv8, pl.balanced)
+                         : pass1_symbol<BF16>(d, pl.heads, pl.waves, pl.mfma, pl.kv8, pl.balanced);
 }
 
 // Resident pass-1 workgroups per compute unit (occupancy calculator).

@@ -9,12 +9,14 @@
 //   rotate-half pairs (i, i + D/2) (Llama / GPT-NeoX) or interleaved pairs (2i, 2i + 1)
 //   (GPT-J), angle = position * inv_freq[i], y0 = x0 cos - x1 sin, y1 = x1 cos + x0 sin,
 // computed in fp32 and rounded once to the cache type. inv_freq carries any frequency
-// scaling (e.g. Llama 3's); without it the rows are copied unrotated.
+// scaling (e.g. Llama 3's); without it the rows are copied unrotated. An fp8 (OCP E4M3)
+// cache stores RNE(clamp(x / scale, -448, 448)) of each fp32 value x (NaN stays NaN).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
 #include <algorithm>
+#include <cmath>
 
 #include "dk_args.h"
 #include "dk_decode.h"
@@ -38,19 +40,37 @@ struct AppendArgs {
   int64_t q_b, q_h, n_b, n_h, kv_p, kv_s, kv_h;   // bytes
   int32_t batch, hq, hkv, d, num_indices, rope_style;
   uint32_t num_pages;
+  float k_scale, v_scale;     // fp8 cache: stored = value / scale
 };
 
 template <class E>
 struct Elem;
 template <>
 struct Elem<_Float16> {
+  static constexpr int kBytes = 2;
   static __device__ float load(const uint8_t* p) { return (float)*(const _Float16*)p; }
-  static __device__ void store(uint8_t* p, float x) { *(_Float16*)p = (_Float16)x; }
+  __device__ void store(uint8_t* p, float x) const { *(_Float16*)p = (_Float16)x; }
 };
 template <>
 struct Elem<__bf16> {
+  static constexpr int kBytes = 2;
   static __device__ float load(const uint8_t* p) { return (float)*(const __bf16*)p; }
-  static __device__ void store(uint8_t* p, float x) { *(__bf16*)p = (__bf16)x; }
+  __device__ void store(uint8_t* p, float x) const { *(__bf16*)p = (__bf16)x; }
+};
+
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+// OCP E4M3 store of x / scale: round to nearest even, clamped to +-448 (the largest
+// finite value) so that no finite input becomes NaN; NaN stays NaN.
+struct Fp8Store {
+  static constexpr int kBytes = 1;
+  float scale;
+  __device__ void store(uint8_t* p, float x) const {
+    float y = x / scale;
+    y = y != y ? y : fminf(fmaxf(y, -448.f), 448.f);
+    const short2_t r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(short2_t{0, 0}, y, 0.f, 1.f, false);
+    *p = (uint8_t)(r[0] & 0xff);
+  }
 };
 
 __device__ __forceinline__ void pair_of(int i, int half, int style, int* i0, int* i1) {
@@ -63,11 +83,12 @@ __device__ __forceinline__ void pair_of(int i, int half, int style, int* i0, int
   }
 }
 
-// Rows of `heads` heads from src (head h at src + h * s_h) rotated into dst (dst + h * d_h);
-// src and dst may alias (q in place: each pair is read before it is written by one thread).
-template <class E>
+// Rows of `heads` heads from src (head h at src + h * s_h) rotated into dst (dst + h * d_h,
+// elements stored by `out`); src and dst may alias (q in place: each pair is read before
+// it is written by one thread).
+template <class E, class Out>
 __device__ void rotate_rows(uint8_t* dst, int64_t d_h, const uint8_t* src, int64_t s_h, int heads,
-                            int d, int style, const float* inv_freq, float pos) {
+                            int d, int style, const float* inv_freq, float pos, Out out) {
   const int half = d / 2;
   for (int idx = threadIdx.x; idx < heads * half; idx += kAppendThreads) {
     const int h = idx / half, i = idx % half;
@@ -82,12 +103,12 @@ __device__ void rotate_rows(uint8_t* dst, int64_t d_h, const uint8_t* src, int64
       y0 = x0 * c - x1 * s;
       y1 = x1 * c + x0 * s;
     }
-    Elem<E>::store(dst + h * d_h + 2 * i0, y0);
-    Elem<E>::store(dst + h * d_h + 2 * i1, y1);
+    out.store(dst + h * d_h + Out::kBytes * i0, y0);
+    out.store(dst + h * d_h + Out::kBytes * i1, y1);
   }
 }
 
-template <class E>
+template <class E, bool KV8>
 __global__ __launch_bounds__(kAppendThreads) void dk_append_kv_kernel(AppendArgs a) {
   const int b = blockIdx.x;
   const int s0 = min(max(a.indptr[b], 0), a.num_indices);
@@ -100,29 +121,41 @@ __global__ __launch_bounds__(kAppendThreads) void dk_append_kv_kernel(AppendArgs
   uint8_t* krow = a.k_cache + (int64_t)page * a.kv_p + (int64_t)slot * a.kv_s;
   const uint8_t* kn = a.k_new + (int64_t)b * a.n_b;
   const uint8_t* vn = a.v_new + (int64_t)b * a.n_b;
-  rotate_rows<E>(krow, a.kv_h, kn, a.n_h, a.hkv, a.d, a.rope_style, a.inv_freq, pos);
   uint8_t* vrow = krow + a.v_off;
-  for (int idx = threadIdx.x; idx < a.hkv * a.d; idx += kAppendThreads) {
-    const int h = idx / a.d, i = idx % a.d;
-    *(uint16_t*)(vrow + h * a.kv_h + 2 * i) = *(const uint16_t*)(vn + h * a.n_h + 2 * i);
+  if constexpr (KV8) {
+    rotate_rows<E>(krow, a.kv_h, kn, a.n_h, a.hkv, a.d, a.rope_style, a.inv_freq, pos,
+                   Fp8Store{a.k_scale});
+    const Fp8Store vs{a.v_scale};
+    for (int idx = threadIdx.x; idx < a.hkv * a.d; idx += kAppendThreads) {
+      const int h = idx / a.d, i = idx % a.d;
+      vs.store(vrow + h * a.kv_h + i, Elem<E>::load(vn + h * a.n_h + 2 * i));
+    }
+  } else {
+    rotate_rows<E>(krow, a.kv_h, kn, a.n_h, a.hkv, a.d, a.rope_style, a.inv_freq, pos,
+                   Elem<E>{});
+    for (int idx = threadIdx.x; idx < a.hkv * a.d; idx += kAppendThreads) {
+      const int h = idx / a.d, i = idx % a.d;
+      *(uint16_t*)(vrow + h * a.kv_h + 2 * i) = *(const uint16_t*)(vn + h * a.n_h + 2 * i);
+    }
   }
   if (a.q && a.inv_freq) {
     uint8_t* qb = a.q + (int64_t)b * a.q_b;
-    rotate_rows<E>(qb, a.q_h, qb, a.q_h, a.hq, a.d, a.rope_style, a.inv_freq, pos);
+    rotate_rows<E>(qb, a.q_h, qb, a.q_h, a.hq, a.d, a.rope_style, a.inv_freq, pos, Elem<E>{});
   }
 }
 
 }  // namespace
 }  // namespace dk
 
-extern "C" int dk_append_kv(void* q, const void* k_new, const void* v_new, int64_t new_b,
-                            int64_t new_h, void* k_cache, void* v_cache,
-                            const int32_t* kv_indptr, const int32_t* kv_indices,
-                            const int32_t* kv_last_page_len, const int32_t* positions,
-                            const float* inv_freq, int32_t rope_style, int32_t batch,
-                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                            int32_t page_size, int64_t num_pages, int64_t num_indices,
-                            int32_t dtype, const dk_strides* strides, void* hip_stream) {
+static int append_impl(void* q, const void* k_new, const void* v_new, int64_t new_b,
+                       int64_t new_h, void* k_cache, void* v_cache,
+                       const int32_t* kv_indptr, const int32_t* kv_indices,
+                       const int32_t* kv_last_page_len, const int32_t* positions,
+                       const float* inv_freq, int32_t rope_style, int32_t batch,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int32_t page_size, int64_t num_pages, int64_t num_indices,
+                       int32_t dtype, bool kv8, float k_scale, float v_scale,
+                       const dk_strides* strides, void* hip_stream) {
   dk::clear_error();
   if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 ||
@@ -132,6 +165,9 @@ extern "C" int dk_append_kv(void* q, const void* k_new, const void* v_new, int64
     return dk::set_error(DK_EINVAL, "page_size must be 16; got %d", page_size);
   if (dtype != DK_F16 && dtype != DK_BF16)
     return dk::set_error(DK_EINVAL, "dtype must be DK_F16 or DK_BF16; got %d", dtype);
+  if (kv8 && (!(k_scale > 0.f) || !(v_scale > 0.f) || !std::isfinite(k_scale) ||
+              !std::isfinite(v_scale)))
+    return dk::set_error(DK_EINVAL, "k_scale and v_scale must be finite and > 0");
   if (rope_style != 0 && rope_style != 1)
     return dk::set_error(DK_EINVAL, "rope_style must be 0 (rotate half) or 1 (interleaved)");
   if (num_indices < 0 || num_indices > INT32_MAX || num_pages < 0)
@@ -151,8 +187,9 @@ extern "C" int dk_append_kv(void* q, const void* k_new, const void* v_new, int64
   a.k_new = static_cast<const uint8_t*>(k_new);
   a.v_new = static_cast<const uint8_t*>(v_new);
   a.k_cache = static_cast<uint8_t*>(k_cache);
+  const int64_t kes = kv8 ? 1 : 2;   // cache element bytes
   a.v_off = v_cache ? (int64_t)(static_cast<uint8_t*>(v_cache) - static_cast<uint8_t*>(k_cache))
-                    : s.kv_r * 2;
+                    : s.kv_r * kes;
   a.indptr = kv_indptr;
   a.indices = kv_indices;
   a.last_len = kv_last_page_len;
@@ -162,9 +199,11 @@ extern "C" int dk_append_kv(void* q, const void* k_new, const void* v_new, int64
   a.q_h = s.q_h * 2;
   a.n_b = new_b * 2;
   a.n_h = new_h * 2;
-  a.kv_p = s.kv_p * 2;
-  a.kv_s = s.kv_s * 2;
-  a.kv_h = s.kv_h * 2;
+  a.kv_p = s.kv_p * kes;
+  a.kv_s = s.kv_s * kes;
+  a.kv_h = s.kv_h * kes;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   a.batch = batch;
   a.hq = num_q_heads;
   a.hkv = num_kv_heads;
@@ -173,10 +212,42 @@ extern "C" int dk_append_kv(void* q, const void* k_new, const void* v_new, int64
   a.rope_style = rope_style;
   a.num_pages = (uint32_t)std::min<int64_t>(num_pages, (int64_t)1 << 31);
   void* args[] = {&a};
-  const void* fn = dtype == DK_F16 ? (const void*)dk::dk_append_kv_kernel<_Float16>
-                                   : (const void*)dk::dk_append_kv_kernel<__bf16>;
+  const void* fn =
+      kv8 ? (dtype == DK_F16 ? (const void*)dk::dk_append_kv_kernel<_Float16, true>
+                             : (const void*)dk::dk_append_kv_kernel<__bf16, true>)
+          : (dtype == DK_F16 ? (const void*)dk::dk_append_kv_kernel<_Float16, false>
+                             : (const void*)dk::dk_append_kv_kernel<__bf16, false>);
   const hipError_t e = hipLaunchKernel(fn, dim3(batch), dim3(dk::kAppendThreads), args, 0,
                                        static_cast<hipStream_t>(hip_stream));
   if (e != hipSuccess) return dk::set_error((int)e, "append launch: %s", hipGetErrorString(e));
   return DK_OK;
+}
+
+extern "C" int dk_append_kv(void* q, const void* k_new, const void* v_new, int64_t new_b,
+                            int64_t new_h, void* k_cache, void* v_cache,
+                            const int32_t* kv_indptr, const int32_t* kv_indices,
+                            const int32_t* kv_last_page_len, const int32_t* positions,
+                            const float* inv_freq, int32_t rope_style, int32_t batch,
+                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t page_size, int64_t num_pages, int64_t num_indices,
+                            int32_t dtype, const dk_strides* strides, void* hip_stream) {
+  return append_impl(q, k_new, v_new, new_b, new_h, k_cache, v_cache, kv_indptr, kv_indices,
+                     kv_last_page_len, positions, inv_freq, rope_style, batch, num_q_heads,
+                     num_kv_heads, head_dim, page_size, num_pages, num_indices, dtype, false,
+                     0.f, 0.f, strides, hip_stream);
+}
+
+extern "C" int dk_append_kv_fp8(void* q, const void* k_new, const void* v_new, int64_t new_b,
+                                int64_t new_h, void* k_cache, void* v_cache,
+                                const int32_t* kv_indptr, const int32_t* kv_indices,
+                                const int32_t* kv_last_page_len, const int32_t* positions,
+                                const float* inv_freq, int32_t rope_style, int32_t batch,
+                                int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t page_size, int64_t num_pages, int64_t num_indices,
+                                int32_t dtype, float k_scale, float v_scale,
+                                const dk_strides* strides, void* hip_stream) {
+  return append_impl(q, k_new, v_new, new_b, new_h, k_cache, v_cache, kv_indptr, kv_indices,
+                     kv_last_page_len, positions, inv_freq, rope_style, batch, num_q_heads,
+                     num_kv_heads, head_dim, page_size, num_pages, num_indices, dtype, true,
+                     k_scale, v_scale, strides, hip_stream);
 }

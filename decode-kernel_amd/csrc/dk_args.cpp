@@ -151,8 +151,6 @@ int validate(const Problem& p) {
     return set_error(DK_EINVAL, "options.k_scale and v_scale must be finite and >= 0");
   if (o.kv_dtype == DK_KV_SAME && (o.k_scale != 0.f || o.v_scale != 0.f))
     return set_error(DK_EINVAL, "options.k_scale and v_scale apply to an fp8 cache only");
-  if (o.kv_dtype == DK_KV_FP8_E4M3 && o.qk_path == 1)
-    return set_error(DK_EUNSUPPORTED, "an fp8 cache supports the VALU q.k path only");
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything

@@ -1,0 +1,7 @@
+// fp16 q/out over an fp16 cache, q.k on the matrix cores. Instantiation of that
+// symbol table (each table is its own translation unit, compiled in parallel).
+#include "dk_launch.h"
+
+namespace dk {
+template const void* pass1_symbol_16<F16, true>(int, int, int, bool);
+}  // namespace dk

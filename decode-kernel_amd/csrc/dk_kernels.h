@@ -312,7 +312,6 @@ __device__ __forceinline__ int seq_begin(const Pass1Args& a, int b) {
 // (E4M3) values, widened to T in registers after the loads.
 template <class T, int D, int G, bool MFMA, bool KV8 = false>
 struct Wave {
-  static_assert(!(MFMA && KV8), "fp8 pages use the VALU q.k layout");
   static constexpr int GQ = G < 4 ? G : 4;   // heads per column set
   static constexpr int NS = G / GQ;          // column sets (G = 8 -> 2)
   static constexpr int DPL = D / 16;         // V (and VALU-path K) dims per lane
@@ -323,12 +322,16 @@ struct Wave {
   static constexpr int KB = KV8 ? D / 16 : KW;   // words of a page buffer as loaded (K)
   static constexpr int VB = KV8 ? D / 16 : VW;   // (V)
   static constexpr int EB = KV8 ? 1 : 2;         // bytes per cache element
+  // MFMA q.k: 16-byte K loads per lane, token c, bytes 16*r16 + 64*i of the row; an fp8
+  // load holds the dims of two MFMAs (D/64 loads), a 16-bit load those of one (D/32)
+  static constexpr int NKL = KV8 ? D / 64 : NMF;
 
   int r16, c;
   u32 koff, voff, tok_s, extent;
   int64_t kv_v;
   float kscale, vscale;
-  u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, dims 32i+8r16..
+  u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, the dims of
+                                             // the K operand of MFMA i (see q_dim0)
   u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
   float acc[G][DPL];      // after reduce_rows: head h, dim c*DPL + j (every lane row)
   f32x4 cv[NS][DPL];      // while pages stream: the P.V accumulators as MFMA C vectors,
@@ -348,14 +351,21 @@ struct Wave {
     vscale = a.vscale;
   }
 
+  // MFMA q.k: first of the 8 dims lane row r16 supplies to MFMA i (k = 8*r16..8*r16+7).
+  // 16-bit cache: load i holds dims 32i + 8r16 .. +7. fp8 cache: load j = i/2 holds dims
+  // 64j + 16r16 .. +15, widened in order, so MFMA 2j takes the first 8 and 2j+1 the rest.
+  __device__ __forceinline__ int q_dim0(int i) const {
+    return KV8 ? 64 * (i >> 1) + 16 * r16 + 8 * (i & 1) : 32 * i + 8 * r16;
+  }
+
   // q rows of the G heads starting at qbase (q_h bytes apart).
   __device__ __forceinline__ void load_q(const uint8_t* qbase, int64_t q_h) {
     if constexpr (MFMA) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
-        const uint8_t* qp = qbase + (int64_t)(ss * GQ + c % GQ) * q_h + 16 * r16;
+        const uint8_t* qp = qbase + (int64_t)(ss * GQ + c % GQ) * q_h;
 #pragma unroll
-        for (int i = 0; i < NMF; ++i) ld_words_cached<4>(&qw[ss][4 * i], qp + 64 * i);
+        for (int i = 0; i < NMF; ++i) ld_words_cached<4>(&qw[ss][4 * i], qp + 2 * q_dim0(i));
       }
     } else {
 #pragma unroll
@@ -387,7 +397,7 @@ struct Wave {
     constexpr int TW = KB / 4;   // words per token per lane as loaded
     if constexpr (MFMA) {
 #pragma unroll
-      for (int i = 0; i < NMF; ++i) ld_buf<4>(&kb[4 * i], rk, koff, 64 * i);
+      for (int i = 0; i < NKL; ++i) ld_buf<4>(&kb[4 * i], rk, koff, 64 * i);
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) ld_buf<TW>(&kb[r * TW], rk, koff, r * tok_s);

@@ -17,19 +17,28 @@ struct Pass1Launch {
   hipStream_t stream = nullptr;
 };
 
-// Kernel symbol for (head_dim, heads, waves, path, mode) over a 16-bit cache, and over an
-// fp8 cache (VALU q.k only); nullptr if not instantiated.
-template <class T>
-const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool balanced);
-template <class T>
+// Kernel symbol for (head_dim, heads, waves, mode) with q.k on the matrix cores (M) or
+// the VALU, over a 16-bit cache and over an fp8 cache; nullptr if not instantiated. Each
+// (element type, cache type, M) table is instantiated in its own translation unit.
+template <class T, bool M>
+const void* pass1_symbol_16(int d, int heads, int waves, bool balanced);
+template <class T, bool M>
 const void* pass1_symbol_kv8(int d, int heads, int waves, bool balanced);
 template <class T>
 const void* merge_symbol(int d, bool balanced);
 
 template <class T>
+const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool kv8, bool balanced) {
+  if (kv8)
+    return mfma ? pass1_symbol_kv8<T, true>(d, heads, waves, balanced)
+                : pass1_symbol_kv8<T, false>(d, heads, waves, balanced);
+  return mfma ? pass1_symbol_16<T, true>(d, heads, waves, balanced)
+              : pass1_symbol_16<T, false>(d, heads, waves, balanced);
+}
+
+template <class T>
 hipError_t launch_pass1(const Pass1Args& a, const Pass1Launch& L) {
-  const void* fn = L.kv8 ? (L.mfma ? nullptr : pass1_symbol_kv8<T>(L.d, L.heads, L.waves, L.balanced))
-                         : pass1_symbol<T>(L.d, L.heads, L.waves, L.mfma, L.balanced);
+  const void* fn = pass1_symbol<T>(L.d, L.heads, L.waves, L.mfma, L.kv8, L.balanced);
   if (!fn) return hipErrorInvalidDeviceFunction;
   Pass1Args arg = a;
   void* args[] = {&arg};
@@ -53,57 +62,47 @@ const void* pass1_sym(bool balanced) {
                   : reinterpret_cast<const void*>(&dk_pass1_split<T, D, G, NW, M, KV8>);
 }
 
-template <class T, int D, int G, int NW, bool KV8>
-const void* pass1_sym_m(bool mfma, bool balanced) {
-  if constexpr (KV8) {
-    return mfma ? nullptr : pass1_sym<T, D, G, NW, false, true>(balanced);
-  } else {
-    return mfma ? pass1_sym<T, D, G, NW, true, false>(balanced)
-                : pass1_sym<T, D, G, NW, false, false>(balanced);
-  }
-}
-
-template <class T, int D, int G, bool KV8>
-const void* pass1_sym_w(int waves, bool mfma, bool balanced) {
+template <class T, int D, int G, bool M, bool KV8>
+const void* pass1_sym_w(int waves, bool balanced) {
   switch (waves) {
-    case 1: return pass1_sym_m<T, D, G, 1, KV8>(mfma, balanced);
-    case 2: return pass1_sym_m<T, D, G, 2, KV8>(mfma, balanced);
-    case 4: return pass1_sym_m<T, D, G, 4, KV8>(mfma, balanced);
+    case 1: return pass1_sym<T, D, G, 1, M, KV8>(balanced);
+    case 2: return pass1_sym<T, D, G, 2, M, KV8>(balanced);
+    case 4: return pass1_sym<T, D, G, 4, M, KV8>(balanced);
     default: return nullptr;
   }
 }
 
-template <class T, int D, bool KV8>
-const void* pass1_sym_g(int heads, int waves, bool mfma, bool balanced) {
+template <class T, int D, bool M, bool KV8>
+const void* pass1_sym_g(int heads, int waves, bool balanced) {
   switch (heads) {
-    case 1: return pass1_sym_w<T, D, 1, KV8>(waves, mfma, balanced);
-    case 2: return pass1_sym_w<T, D, 2, KV8>(waves, mfma, balanced);
-    case 4: return pass1_sym_w<T, D, 4, KV8>(waves, mfma, balanced);
+    case 1: return pass1_sym_w<T, D, 1, M, KV8>(waves, balanced);
+    case 2: return pass1_sym_w<T, D, 2, M, KV8>(waves, balanced);
+    case 4: return pass1_sym_w<T, D, 4, M, KV8>(waves, balanced);
     case 8:
-      if constexpr (D <= 128) return pass1_sym_w<T, D, 8, KV8>(waves, mfma, balanced);
+      if constexpr (D <= 128) return pass1_sym_w<T, D, 8, M, KV8>(waves, balanced);
       return nullptr;
     default: return nullptr;
   }
 }
 
-template <class T, bool KV8>
-const void* pass1_symbol_t(int d, int heads, int waves, bool mfma, bool balanced) {
+template <class T, bool M, bool KV8>
+const void* pass1_symbol_t(int d, int heads, int waves, bool balanced) {
   switch (d) {
-    case 64: return pass1_sym_g<T, 64, KV8>(heads, waves, mfma, balanced);
-    case 128: return pass1_sym_g<T, 128, KV8>(heads, waves, mfma, balanced);
-    case 256: return pass1_sym_g<T, 256, KV8>(heads, waves, mfma, balanced);
+    case 64: return pass1_sym_g<T, 64, M, KV8>(heads, waves, balanced);
+    case 128: return pass1_sym_g<T, 128, M, KV8>(heads, waves, balanced);
+    case 256: return pass1_sym_g<T, 256, M, KV8>(heads, waves, balanced);
     default: return nullptr;
   }
 }
 
-template <class T>
-const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool balanced) {
-  return pass1_symbol_t<T, false>(d, heads, waves, mfma, balanced);
+template <class T, bool M>
+const void* pass1_symbol_16(int d, int heads, int waves, bool balanced) {
+  return pass1_symbol_t<T, M, false>(d, heads, waves, balanced);
 }
 
-template <class T>
+template <class T, bool M>
 const void* pass1_symbol_kv8(int d, int heads, int waves, bool balanced) {
-  return pass1_symbol_t<T, true>(d, heads, waves, false, balanced);
+  return pass1_symbol_t<T, M, true>(d, heads, waves, balanced);
 }
 
 template <class T>
@@ -119,13 +118,15 @@ const void* merge_symbol(int d, bool balanced) {
   }
 }
 
-// Explicit instantiation declarations (definitions in dk_f16.hip / dk_bf16.hip and
-// dk_f16_kv8.hip / dk_bf16_kv8.hip).
-extern template const void* pass1_symbol<F16>(int, int, int, bool, bool);
-extern template const void* pass1_symbol<BF16>(int, int, int, bool, bool);
-extern template const void* pass1_symbol_kv8<F16>(int, int, int, bool);
-extern template const void* pass1_symbol_kv8<BF16>(int, int, int, bool);
-extern template const void* merge_symbol<F16>(int, bool);
-extern template const void* merge_symbol<BF16>(int, bool);
+// Explicit instantiation declarations (definitions in dk_{f16,bf16}[_kv8][_mfma].hip).
+#define DK_DECLARE_TABLES(T)                                                          \
+  extern template const void* pass1_symbol_16<T, false>(int, int, int, bool);        \
+  extern template const void* pass1_symbol_16<T, true>(int, int, int, bool);         \
+  extern template const void* pass1_symbol_kv8<T, false>(int, int, int, bool);       \
+  extern template const void* pass1_symbol_kv8<T, true>(int, int, int, bool);        \
+  extern template const void* merge_symbol<T>(int, bool);
+DK_DECLARE_TABLES(F16)
+DK_DECLARE_TABLES(BF16)
+#undef DK_DECLARE_TABLES
 
 }  // namespace dk

@@ -36,8 +36,9 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-HIP_SOURCES = ("dk_api.hip", "dk_f16.hip", "dk_bf16.hip", "dk_f16_kv8.hip", "dk_bf16_kv8.hip",
-               "dk_paging.hip", "dk_append.hip")
+HIP_SOURCES = ("dk_api.hip", "dk_f16.hip", "dk_bf16.hip", "dk_f16_mfma.hip", "dk_bf16_mfma.hip",
+               "dk_f16_kv8.hip", "dk_bf16_kv8.hip", "dk_f16_kv8_mfma.hip",
+               "dk_bf16_kv8_mfma.hip", "dk_paging.hip", "dk_append.hip")
 
 
 # Per-kernel resource report of the device compiler (VGPRs, scratch, occupancy).

@@ -85,6 +85,10 @@ SIGNATURES = {
     "dk_append_kv": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I32,
                                     _I32, _I32, _I32, _I32, _I32, _I64, _I64, _I32,
                                     ctypes.POINTER(DkStrides), _P]),
+    "dk_append_kv_fp8": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
+                                        _I32, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _I32,
+                                        ctypes.c_float, ctypes.c_float,
+                                        ctypes.POINTER(DkStrides), _P]),
     "dk_decode_partials": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _I32, _I32, _I32, _I32,
                                           _I32, _I64, _I64, _I32, ctypes.POINTER(DkStrides),
                                           _I32, ctypes.POINTER(DkOptions), _P]),

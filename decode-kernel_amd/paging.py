@@ -9,6 +9,7 @@ trip. Tokens are assumed to sit in 16-token pages: token t of a request at slot
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Optional
 
 import torch
@@ -76,7 +77,8 @@ def rope_inv_freq(head_dim: int, theta: float = 10000.0, device="cuda") -> torch
 def append_kv(q: Optional[torch.Tensor], k_new: torch.Tensor, v_new: torch.Tensor, kv_data,
               kv_indptr: torch.Tensor, kv_indices: torch.Tensor, kv_last_page_len: torch.Tensor,
               inv_freq: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
-              rope_style: int = 0) -> None:
+              rope_style: int = 0, k_scale: Optional[float] = None,
+              v_scale: Optional[float] = None) -> None:
     """Write each sequence's new token into the paged cache (dk_append_kv), in place.
 
     The token's slot is the last one the page table describes (grow the table first).
@@ -86,20 +88,37 @@ def append_kv(q: Optional[torch.Tensor], k_new: torch.Tensor, v_new: torch.Tenso
     inv_freq (head_dim/2,) fp32 on the device, or None for no rotation; positions (batch,)
     int32, or None for each token's index in its sequence; rope_style 0 = rotate-half
     pairs (i, i + D/2) (Llama), 1 = interleaved pairs (2i, 2i + 1).
+    A torch.float8_e4m3fn cache (q, k_new, v_new fp16 or bf16) stores each element as
+    RNE(clamp(x / scale, -448, 448)) with k_scale for K and v_scale for V (None = 1), the
+    scales decode_attention then takes.
     """
     import attention                     # local: attention imports nothing from here
     kv = attention._kv_layout(kv_data)
     batch, hkv, d = k_new.shape
-    if v_new.shape != k_new.shape or k_new.dtype != kv.dtype or v_new.dtype != kv.dtype:
+    kv8 = kv.dtype == attention.KV_FP8
+    act = k_new.dtype if kv8 else kv.dtype          # type of q, k_new and v_new
+    if kv8 and act not in (torch.float16, torch.bfloat16):
+        raise DecodeArgumentError("over an fp8 cache k_new and v_new must be fp16 or bf16")
+    if v_new.shape != k_new.shape or k_new.dtype != act or v_new.dtype != act:
         raise DecodeArgumentError("k_new and v_new must be (batch, num_kv_heads, head_dim) in "
-                                  "the cache's dtype")
+                                  "the cache's dtype (fp16 / bf16 over an fp8 cache)")
+    scales = []
+    for name, x in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if not kv8:
+            if x not in (None, 1.0):
+                raise DecodeArgumentError(f"{name} applies to a torch.float8_e4m3fn cache only")
+            continue
+        x = 1.0 if x is None else float(x)
+        if not math.isfinite(x) or x <= 0.0:
+            raise DecodeArgumentError(f"{name} must be finite and > 0, got {x}")
+        scales.append(x)
     if v_new.stride() != k_new.stride() or k_new.stride(2) != 1:
         raise DecodeArgumentError("k_new and v_new need equal strides and a unit head_dim stride")
     if hkv != kv.hkv or d != kv.d or kv.page_size != PAGE_SIZE or kv.d_stride != 1:
         raise DecodeArgumentError("k_new does not match the cache's heads / head_dim")
     if q is not None and (q.dim() != 3 or q.shape[0] != batch or q.shape[2] != d or
-                          q.dtype != kv.dtype or q.stride(2) != 1):
-        raise DecodeArgumentError("q must be (batch, num_q_heads, head_dim) in the cache dtype")
+                          q.dtype != act or q.stride(2) != 1):
+        raise DecodeArgumentError("q must be (batch, num_q_heads, head_dim) in k_new's dtype")
     if inv_freq is not None and (inv_freq.dtype != torch.float32 or inv_freq.numel() != d // 2
                                  or not inv_freq.is_contiguous()):
         raise DecodeArgumentError("inv_freq must be a contiguous fp32 tensor of head_dim/2")
@@ -109,14 +128,18 @@ def append_kv(q: Optional[torch.Tensor], k_new: torch.Tensor, v_new: torch.Tenso
     if q is not None:
         s.q_b, s.q_h = q.stride(0), q.stride(1)
     s.kv_p, s.kv_r, s.kv_s, s.kv_h = kv.strides
-    code = dk_lib.DK_F16 if kv.dtype == torch.float16 else dk_lib.DK_BF16
+    code = dk_lib.DK_F16 if act == torch.float16 else dk_lib.DK_BF16
     ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
+    lib = dk_lib.load()
     with torch.cuda.device(k_new.device):
         stream = torch.cuda.current_stream(k_new.device).cuda_stream
-        rc = dk_lib.load().dk_append_kv(
-            ptr(q), k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
-            kv.k.data_ptr(), ptr(kv.v), kv_indptr.data_ptr(), kv_indices.data_ptr(),
-            kv_last_page_len.data_ptr(), ptr(positions), ptr(inv_freq), rope_style, batch,
-            q.shape[1] if q is not None else 1, hkv, d, PAGE_SIZE, kv.num_pages,
-            kv_indices.shape[0], code, ctypes.byref(s), stream)
+        args = (ptr(q), k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+                kv.k.data_ptr(), ptr(kv.v), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                kv_last_page_len.data_ptr(), ptr(positions), ptr(inv_freq), rope_style, batch,
+                q.shape[1] if q is not None else 1, hkv, d, PAGE_SIZE, kv.num_pages,
+                kv_indices.shape[0], code)
+        if kv8:
+            rc = lib.dk_append_kv_fp8(*args, *scales, ctypes.byref(s), stream)
+        else:
+            rc = lib.dk_append_kv(*args, ctypes.byref(s), stream)
     dk_lib.check(rc, "append_kv")

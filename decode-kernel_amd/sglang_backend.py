@@ -15,6 +15,9 @@ Two entry styles are provided:
   is_prefill=False)` (integration/sglang_backend.py:85-101), for callers that already
   hold FlashInfer page tables.
 
+An fp8_e4m3 KV cache (SGLang stores it as uint8 and hands out float8_e4m3fn views) is
+read with the layer's k_scale / v_scale, which the pool also divides by when it writes.
+
 Registration mirrors the reference (:112-137): `register_backend()` or the environment
 variable SGLANG_ATTENTION_BACKEND=split_kv_hip. SGLang is imported lazily; without it the
 class derives from a stub so that the module imports (and is tested) anywhere.
@@ -72,6 +75,7 @@ class SplitKVHipBackend(_import_sglang_base()):
         self.split_kv = DEFAULT_SPLIT_KV if split_kv is None else split_kv
         self.forward_metadata: Optional[DecodeMetadata] = None
         self._workspace: Optional[torch.Tensor] = None
+        self._scales: dict = {}           # layer_id -> (k_scale, v_scale) of an fp8 pool
 
     @classmethod
     def name(cls) -> str:
@@ -102,27 +106,56 @@ class SplitKVHipBackend(_import_sglang_base()):
             raise NotImplementedError("logit soft-capping is not supported by this kernel")
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
-            pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
+            self._save(pool, layer, forward_batch.out_cache_loc, k, v)
         md = self.forward_metadata
         if md is None:
             raise RuntimeError("init_forward_metadata must run before forward_decode")
         hq, d = layer.tp_q_head_num, layer.head_dim
         kc, vc = self._paged_views(pool, layer.layer_id)
         qv = q.reshape(-1, hq, d)
+        scales = {}
+        if kc.dtype == torch.float8_e4m3fn:      # SGLang's fp8_e4m3 KV cache
+            scales = dict(zip(("k_scale", "v_scale"), self._kv_scales(layer)))
         out = decode_attention(
             qv, (kc, vc), md.kv_indptr, md.kv_indices, md.kv_last_page_len,
             split_kv=self.split_kv, workspace=self._workspace_for(qv, kc.shape[2]),
-            max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d))
+            max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d), **scales)
         return out.view(-1, hq * d)
+
+    @staticmethod
+    def _save(pool, layer, loc, k, v):
+        """The pool's own write (SGLang quantises to an fp8 pool with the layer's scales)."""
+        ks, vs = getattr(layer, "k_scale", None), getattr(layer, "v_scale", None)
+        if ks is None and vs is None:
+            pool.set_kv_buffer(layer, loc, k, v)
+        else:
+            pool.set_kv_buffer(layer, loc, k, v, ks, vs)
+
+    def _kv_scales(self, layer):
+        """(k_scale, v_scale) floats of a layer (1.0 when unset), read once per layer:
+        `k_scale_float` when the model loader set it, else `k_scale` (float or tensor)."""
+        key = getattr(layer, "layer_id", id(layer))
+        if key not in self._scales:
+            vals = []
+            for name in ("k_scale", "v_scale"):
+                x = getattr(layer, name + "_float", None)
+                if x is None:
+                    x = getattr(layer, name, None)
+                if isinstance(x, torch.Tensor):
+                    x = float(x.detach().float().reshape(-1)[0].item())
+                vals.append(1.0 if x is None else float(x))
+            self._scales[key] = tuple(vals)
+        return self._scales[key]
 
     def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
         """Prefill / extend: causal attention of the new tokens over each request's cached
         prefix and themselves, with PyTorch SDPA per request (outside the decode path)."""
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
-            pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
+            self._save(pool, layer, forward_batch.out_cache_loc, k, v)
         hq, hkv, d = layer.tp_q_head_num, layer.tp_k_head_num, layer.head_dim
         kb, vb = pool.get_key_buffer(layer.layer_id), pool.get_value_buffer(layer.layer_id)
+        ks, vs = self._kv_scales(layer) if kb.dtype == torch.float8_e4m3fn else (1.0, 1.0)
         req_to_token = forward_batch.req_to_token_pool.req_to_token
         qv = q.reshape(-1, hq, d)
         out = torch.empty_like(qv)
@@ -133,8 +166,8 @@ class SplitKVHipBackend(_import_sglang_base()):
         for row, n_new, n_all in zip(rows, list(ext), list(lens)):
             n_new, n_all = int(n_new), int(n_all)
             slots = req_to_token[row, :n_all].long()
-            kk = kb[slots].float().transpose(0, 1)           # (hkv, n_all, d)
-            vv = vb[slots].float().transpose(0, 1)
+            kk = kb[slots].float().transpose(0, 1) * ks      # (hkv, n_all, d)
+            vv = vb[slots].float().transpose(0, 1) * vs
             qq = qv[start:start + n_new].float().transpose(0, 1)   # (hq, n_new, d)
             g = hq // hkv
             kk = kk.repeat_interleave(g, dim=0)

@@ -218,6 +218,20 @@ int dk_append_kv(void* q, const void* k_new, const void* v_new, int64_t new_b, i
                  int32_t page_size, int64_t num_pages, int64_t num_indices, int32_t dtype,
                  const dk_strides* strides, void* hip_stream);
 
+/* dk_append_kv into an fp8 (OCP E4M3) cache: q, k_new and v_new have type `dtype`
+ * (DK_F16 / DK_BF16); each cached element is RNE(clamp(x / scale, -448, 448)) of the
+ * fp32 value x (rotated K with k_scale, V with v_scale; both finite and > 0; NaN stays
+ * NaN), the inverse of dk_options.k_scale / v_scale in the decode call. Cache strides in
+ * elements (= bytes). No counterpart in the reference (fp16 cache only). */
+int dk_append_kv_fp8(void* q, const void* k_new, const void* v_new, int64_t new_b,
+                     int64_t new_h, void* k_cache, void* v_cache, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                     const int32_t* positions, const float* inv_freq, int32_t rope_style,
+                     int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t page_size, int64_t num_pages,
+                     int64_t num_indices, int32_t dtype, float k_scale, float v_scale,
+                     const dk_strides* strides, void* hip_stream);
+
 /* Pass 1 only: writes partial_O / partial_m / partial_l for split_kv >= 1 splits into
  * the workspace (layout from dk_partials_layout; partial_m is the split's max of
  * q.k*scale, -1e9 for an empty split, partial_l = sum exp(score - partial_m),

@@ -63,6 +63,18 @@ def encode(x) -> np.ndarray:
     return out | np.where(np.signbit(x), 0x80, 0).astype(np.uint8)
 
 
+def encode_saturating(x) -> np.ndarray:
+    """encode() of x clamped to [-448, 448] (NaN stays NaN): the cache-write rounding."""
+    return encode(np.clip(np.asarray(x, np.float64), -MAX, MAX))
+
+
+def signed_rank(codes) -> np.ndarray:
+    """Position of each finite code on the number line in code steps (+-0 -> 0), so two
+    codes are neighbours iff their ranks differ by 1."""
+    c = np.asarray(codes, np.uint8).astype(np.int64)
+    return np.where(c & 0x80, -(c & 0x7F), c & 0x7F)
+
+
 def dequantize(codes, scale: float) -> np.ndarray:
     """float32 scale * decode(codes), the values the kernel attends over."""
     return (decode(codes) * np.float64(scale)).astype(np.float32)

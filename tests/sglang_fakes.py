@@ -22,31 +22,41 @@ class Mode:
 
 
 class TokenPool:
-    """MHATokenToKVPool-like: k_buffer[layer] / v_buffer[layer] of (slots, Hkv, D)."""
+    """MHATokenToKVPool-like: k_buffer[layer] / v_buffer[layer] of (slots, Hkv, D). An fp8
+    pool stores uint8 and hands out float8_e4m3fn views; set_kv_buffer divides by the
+    layer's scales and casts, as SGLang's pool does."""
 
     def __init__(self, slots, layers, hkv, d, dtype, device, gen):
-        self.k_buffer = [torch.randn(slots, hkv, d, generator=gen, device=device).to(dtype)
-                         for _ in range(layers)]
-        self.v_buffer = [torch.randn(slots, hkv, d, generator=gen, device=device).to(dtype)
-                         for _ in range(layers)]
+        self.dtype = dtype
+        self.store_dtype = torch.uint8 if dtype == torch.float8_e4m3fn else dtype
+        mk = lambda: torch.randn(slots, hkv, d, generator=gen, device=device).to(dtype)  # noqa: E731
+        self.k_buffer = [mk().view(self.store_dtype) for _ in range(layers)]
+        self.v_buffer = [mk().view(self.store_dtype) for _ in range(layers)]
 
     def get_key_buffer(self, layer_id):
-        return self.k_buffer[layer_id]
+        return self.k_buffer[layer_id].view(self.dtype)
 
     def get_value_buffer(self, layer_id):
-        return self.v_buffer[layer_id]
+        return self.v_buffer[layer_id].view(self.dtype)
 
     def get_kv_buffer(self, layer_id):
-        return self.k_buffer[layer_id], self.v_buffer[layer_id]
+        return self.get_key_buffer(layer_id), self.get_value_buffer(layer_id)
 
-    def set_kv_buffer(self, layer, loc, cache_k, cache_v):
+    def set_kv_buffer(self, layer, loc, cache_k, cache_v, k_scale=None, v_scale=None):
         kb, vb = self.k_buffer[layer.layer_id], self.v_buffer[layer.layer_id]
-        kb[loc.long()] = cache_k.view(-1, kb.shape[1], kb.shape[2]).to(kb.dtype)
-        vb[loc.long()] = cache_v.view(-1, vb.shape[1], vb.shape[2]).to(vb.dtype)
+        if cache_k.dtype != self.dtype:
+            if k_scale is not None:
+                cache_k = cache_k / k_scale
+            if v_scale is not None:
+                cache_v = cache_v / v_scale
+            cache_k, cache_v = cache_k.to(self.dtype), cache_v.to(self.dtype)
+        kb[loc.long()] = cache_k.reshape(-1, kb.shape[1], kb.shape[2]).view(self.store_dtype)
+        vb[loc.long()] = cache_v.reshape(-1, vb.shape[1], vb.shape[2]).view(self.store_dtype)
 
 
 def make_batch(lens, hq=32, hkv=8, d=128, layers=2, dtype=torch.float16, device="cuda",
-               seed=0, pool_pages=None, rows=None, decode=True):
+               seed=0, pool_pages=None, rows=None, decode=True, kv_dtype=None, k_scale=None,
+               v_scale=None):
     """Requests of `lens` tokens (the decode token included) with pages drawn from a
     shuffled free list; returns (forward_batch, layer list, pool, req_to_token)."""
     gen = torch.Generator(device="cpu")
@@ -65,7 +75,7 @@ def make_batch(lens, hq=32, hkv=8, d=128, layers=2, dtype=torch.float16, device=
                 req_to_token[r, t] = page * PAGE + t % PAGE
     dgen = torch.Generator(device=device)
     dgen.manual_seed(seed + 1)
-    pool = TokenPool(pool_pages * PAGE, layers, hkv, d, dtype, device, dgen)
+    pool = TokenPool(pool_pages * PAGE, layers, hkv, d, kv_dtype or dtype, device, dgen)
     seq_lens = torch.tensor(lens, dtype=torch.int64)
     out_cache_loc = torch.tensor([int(req_to_token[r, n - 1]) for r, n in zip(row_ids, lens)],
                                  dtype=torch.int64)
@@ -78,5 +88,6 @@ def make_batch(lens, hq=32, hkv=8, d=128, layers=2, dtype=torch.float16, device=
         token_to_kv_pool=pool)
     layer_objs = [SimpleNamespace(layer_id=i, tp_q_head_num=hq, tp_k_head_num=hkv,
                                   tp_v_head_num=hkv, head_dim=d, scaling=d ** -0.5,
-                                  logit_cap=0.0) for i in range(layers)]
+                                  logit_cap=0.0, k_scale=k_scale, v_scale=v_scale)
+                  for i in range(layers)]
     return fb, layer_objs, pool, req_to_token

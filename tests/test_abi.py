@@ -105,8 +105,6 @@ def _call(lib, **kw):
      dk_lib.DK_EINVAL, "v_scale"),
     (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, k_scale=float("inf"))),
      dk_lib.DK_EINVAL, "k_scale"),
-    (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, qk_path=1)),
-     dk_lib.DK_EUNSUPPORTED, "VALU"),
     # an fp8 cache's strides are bytes: 8 elements is no longer a 16-byte row
     (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3),
           strides=dk_lib.DkStrides(32 * 128, 128, 2 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128 + 8,

@@ -434,3 +434,43 @@ def test_planted_fp8_bias_mistake_is_caught_by_torch():
     wrong = fp8.decode(codes) * 2.0                  # exponent bias 6 instead of 7
     fin = np.isfinite(t)
     assert not np.array_equal(t[fin], wrong[fin])
+
+
+def test_fp8_saturating_encode_matches_torch_clamp_then_convert():
+    from oracle import fp8
+    x = np.concatenate([np.linspace(-600, 600, 20001), [np.inf, -np.inf, np.nan, 464.0, -470.0]])
+    x = x.astype(np.float32)
+    want = torch.from_numpy(x).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert np.array_equal(fp8.encode_saturating(x), want.numpy())
+    ranks = fp8.signed_rank(np.arange(256, dtype=np.uint8))
+    vals = fp8.decode(np.arange(256, dtype=np.uint8))
+    fin = np.isfinite(vals)
+    # rank order is value order (ties only between +0 and -0)
+    order = np.argsort(vals[fin], kind="stable")
+    assert np.all(np.diff(ranks[fin][order]) >= 0)
+
+
+def test_fp8_append_oracle_matches_float_append_then_torch_quantization():
+    from oracle import append as oapp
+    rng = np.random.default_rng(4)
+    pages, hkv, d = 6, 2, 16
+    codes = rng.integers(0, 256, (pages, 2, 16, hkv, d)).astype(np.uint8)
+    q = rng.standard_normal((2, 4, d)).astype(np.float32)
+    k_new = (rng.standard_normal((2, hkv, d)) * 300).astype(np.float32)   # some clamp
+    v_new = rng.standard_normal((2, hkv, d)).astype(np.float32)
+    indptr, ids, last = np.array([0, 2, 5]), np.array([3, 1, 0, 5, 2]), np.array([7, 16])
+    inv = 1.0 / (10000.0 ** (np.arange(0, d, 2) / d))
+    got, qo = oapp.append_kv_fp8(codes, q, k_new, v_new, indptr, ids, last, 0.5, 0.25,
+                                 inv_freq=inv)
+    flt, q_want = oapp.append_kv(np.zeros((pages, 2, 16, hkv, d), np.float32), q, k_new, v_new,
+                                 indptr, ids, last, inv_freq=inv)
+    np.testing.assert_array_equal(qo, q_want)
+    for page, slot in ((1, 6), (2, 15)):
+        for r, sc in ((0, 0.5), (1, 0.25)):
+            x = torch.from_numpy(flt[page, r, slot].astype(np.float32)) / np.float32(sc)
+            want = x.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            np.testing.assert_array_equal(got[page, r, slot], want)
+    untouched = np.ones((pages, 16), bool)
+    untouched[1, 6] = untouched[2, 15] = False
+    g, c = got.transpose(0, 2, 1, 3, 4), codes.transpose(0, 2, 1, 3, 4)   # (pages, 16, ...)
+    np.testing.assert_array_equal(g[untouched], c[untouched])

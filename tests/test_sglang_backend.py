@@ -178,3 +178,39 @@ def test_sm_scale_matches_prescaled_q(scale):
                                          to_np(indptr), to_np(ids), to_np(last))
     mx, mean = err_stats(out, want)
     assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fp8_pool_decode_step_through_the_adapter(dtype):
+    # SGLang's fp8_e4m3 KV cache: the pool quantises k / k_scale and v / v_scale on write;
+    # the adapter attends with the same scales
+    from oracle import fp8
+    lens = [1, 17, 300, 16, 1000, 33]
+    ks, vs = 0.5, 0.25
+    fb, layers, pool, r2t = make_batch(lens, dtype=dtype, seed=4, kv_dtype=torch.float8_e4m3fn,
+                                       k_scale=ks, v_scale=vs)
+    rows = fb.req_pool_indices.tolist()
+    backend = sglang_backend.SplitKVHipBackend(split_kv=0)
+    backend.init_forward_metadata(fb)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(6)
+    for layer in layers:
+        print(f"[case] adapter fp8 pool {dtype} layer={layer.layer_id}", flush=True)
+        q = torch.randn(len(lens), 32 * 128, generator=g, device=DEV).to(dtype)
+        k = torch.randn(len(lens), 8 * 128, generator=g, device=DEV).to(dtype)
+        v = torch.randn(len(lens), 8 * 128, generator=g, device=DEV).to(dtype)
+        out = backend.forward_decode(q, k, v, layer, fb)
+        torch.cuda.synchronize()
+        kb = pool.get_key_buffer(layer.layer_id)
+        assert kb.dtype == torch.float8_e4m3fn
+        codes = np.stack([pool.k_buffer[layer.layer_id].cpu().numpy(),
+                          pool.v_buffer[layer.layer_id].cpu().numpy()], axis=1)   # (slots, 2, ..)
+        pages = codes.shape[0] // 16
+        codes = codes[:pages * 16].reshape(pages, 16, 2, 8, 128).transpose(0, 2, 1, 3, 4)
+        deq = np.stack([fp8.dequantize(codes[:, 0], ks), fp8.dequantize(codes[:, 1], vs)], 1)
+        indptr, indices, last = ptab.build_page_table(r2t.numpy(), rows, lens)
+        want = ref.reference_attention_paged(to_np(q.view(-1, 32, 128)).astype(np.float32),
+                                             deq, indptr, indices, last)
+        mx, mean = err_stats(out.view(-1, 32, 128), want)
+        assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
