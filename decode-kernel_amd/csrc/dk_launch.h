@@ -1,6 +1,6 @@
 // dk_launch.h — host-side selection and launch of the decode kernels for one element type.
-// dk_f16.hip and dk_bf16.hip instantiate these templates (compiled in parallel);
-// dk_api.hip calls them.
+// dk_{f16,bf16}[_kv8][_mfma].hip instantiate the symbol tables (one translation unit per
+// element type, cache type and q.k path, compiled in parallel); dk_api.hip calls them.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -72,9 +72,10 @@ typedef struct {
 typedef struct {
   int32_t qk_path;         /* 0 = default (VALU dot2), 1 = MFMA q.k, 2 = VALU q.k;
                               P.V always runs on MFMA                                      */
-  int32_t waves_per_group; /* 0 = default (2); 1, 2 or 4 wavefronts per workgroup          */
+  int32_t waves_per_group; /* 0 = default (2; 4 with an fp8 cache); 1, 2 or 4 wavefronts
+                              per workgroup                                               */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
-                              schedules aim for (0 = default, 2)                            */
+                              schedules aim for (0 = default: 2; 4 with an fp8 cache)     */
   int32_t schedule;        /* split_kv == 0: 0 = automatic, 1 = balanced, 2 = one workgroup
                               per (sequence, kv head) (split_kv == 1)                       */
   int32_t max_pages_per_seq; /* plan hint for split_kv == 0: the most pages any sequence
@@ -85,7 +86,7 @@ typedef struct {
   float sm_scale;          /* softmax scale applied to q.k; 0 = 1/sqrt(head_dim), the
                               reference's fixed scale (attention_ext.cu:79-80)             */
   int32_t kv_dtype;        /* DK_KV_SAME (0): the cache has q's type; DK_KV_FP8_E4M3: fp8
-                              (strides still in elements, now bytes; VALU q.k only)       */
+                              (strides still in elements, now bytes)                      */
   float k_scale;           /* fp8 cache: K = k_scale * stored value (0 = 1); must be 0
                               for a cache of q's type                                     */
   float v_scale;           /* fp8 cache: V = v_scale * stored value (0 = 1); likewise     */
