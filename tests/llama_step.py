@@ -12,6 +12,10 @@ Two runs of the same step:
     output is also checked against the oracle on the same inputs;
   * `cpu_step()`: everything in fp32 on the CPU with the oracle (oracle/append.py,
     oracle/reference.py).
+With `kv_scale` set, the caches are fp8 (E4M3) with that scale for K and V: the history is
+quantised once, the GPU step writes the new token with the quantising append, and the CPU
+step quantises it the same way (oracle append_kv_fp8) and attends over the dequantised
+cache.
 """
 from __future__ import annotations
 
@@ -72,10 +76,10 @@ def make_model(cfg: Cfg, seed: int = 0, device="cuda"):
     return dict(embed=w(cfg.vocab, cfg.hidden), layers=layers)
 
 
-def make_cache(cfg: Cfg, seed: int = 1, device="cuda"):
-    """Per-layer combined caches (pages, 2, 16, Hkv, D) bf16 holding ctx - 1 history tokens
-    per sequence on a permuted page pool, and the page table already grown by the new
-    token's slot (position ctx - 1)."""
+def make_cache(cfg: Cfg, seed: int = 1, device="cuda", kv_scale=None):
+    """Per-layer combined caches (pages, 2, 16, Hkv, D) bf16 (or fp8 E4M3 codes of
+    value / kv_scale) holding ctx - 1 history tokens per sequence on a permuted page pool,
+    and the page table already grown by the new token's slot (position ctx - 1)."""
     pages_per_seq = math.ceil(cfg.ctx / PAGE)
     n_pages = cfg.batch * pages_per_seq
     gen = torch.Generator(device="cpu")
@@ -87,19 +91,32 @@ def make_cache(cfg: Cfg, seed: int = 1, device="cuda"):
     g.manual_seed(seed)
     caches = [torch.randn(n_pages, 2, PAGE, cfg.hkv, cfg.d, generator=g,
                           device=device).to(torch.bfloat16) for _ in range(cfg.layers)]
+    if kv_scale is not None:
+        caches = [(c.float() / kv_scale).clamp(-448, 448).to(torch.float8_e4m3fn)
+                  for c in caches]
     return caches, indptr.to(device), perm.to(device), last.to(device)
+
+
+def _cache_np(cache, kv_scale):
+    """float32 values of a cache (dequantised when it is fp8)."""
+    if cache.dtype == torch.float8_e4m3fn:
+        from oracle import fp8
+        return fp8.dequantize(cache.view(torch.uint8).cpu().numpy(), kv_scale)
+    return to_np(cache)
 
 
 def _rms(x, eps):
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
 
 
-def gpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq, check_rows=None):
+def gpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq, check_rows=None,
+             kv_scale=None):
     """Logits (batch, vocab) fp32 of the bf16 decode step on the device, and, for the
     sequences in check_rows, each layer's max-abs error of the HIP attention against the
     oracle on the same inputs."""
     hint = attention.plan_hint(indptr.cpu())
     inv = torch.as_tensor(inv_freq, device=tokens.device)
+    sc = {} if kv_scale is None else dict(k_scale=kv_scale, v_scale=kv_scale)
     h = model["embed"][tokens].float()
     errs = []
     for li, L in enumerate(model["layers"]):
@@ -107,11 +124,12 @@ def gpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq, check_rows
         q = (x @ L["wq"].T).view(-1, cfg.hq, cfg.d)
         k = (x @ L["wk"].T).view(-1, cfg.hkv, cfg.d)
         v = (x @ L["wv"].T).view(-1, cfg.hkv, cfg.d)
-        paging.append_kv(q, k, v, caches[li], indptr, ids, last, inv_freq=inv)
+        paging.append_kv(q, k, v, caches[li], indptr, ids, last, inv_freq=inv, **sc)
         o = attention.decode_attention(q, caches[li], indptr, ids, last, split_kv=0,
-                                       max_pages_per_seq=hint)
+                                       max_pages_per_seq=hint, **sc)
         if check_rows is not None:
-            want = ref.reference_attention_paged(to_np(q), to_np(caches[li]), to_np(indptr),
+            want = ref.reference_attention_paged(to_np(q), _cache_np(caches[li], kv_scale),
+                                                 to_np(indptr),
                                                  to_np(ids), to_np(last),
                                                  batch_subset=check_rows)
             got = to_np(o)[list(check_rows)].astype(np.float64)
@@ -124,7 +142,7 @@ def gpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq, check_rows
     return logits, errs
 
 
-def cpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq):
+def cpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq, kv_scale=None):
     """Logits (batch, vocab) of the same step in fp32 on the CPU with the oracle."""
     ip, ix, ll = to_np(indptr), to_np(ids), to_np(last)
     f = lambda t: t.float().cpu()  # noqa: E731
@@ -134,7 +152,15 @@ def cpu_step(cfg, model, caches, indptr, ids, last, tokens, inv_freq):
         q = (x @ f(L["wq"]).T).view(-1, cfg.hq, cfg.d).numpy()
         k = (x @ f(L["wk"]).T).view(-1, cfg.hkv, cfg.d).numpy()
         v = (x @ f(L["wv"]).T).view(-1, cfg.hkv, cfg.d).numpy()
-        kv_np, q_np = oapp.append_kv(to_np(caches[li]), q, k, v, ip, ix, ll, inv_freq=inv_freq)
+        if kv_scale is None:
+            kv_np, q_np = oapp.append_kv(to_np(caches[li]), q, k, v, ip, ix, ll,
+                                         inv_freq=inv_freq)
+        else:
+            from oracle import fp8
+            codes, q_np = oapp.append_kv_fp8(caches[li].view(torch.uint8).cpu().numpy(), q, k,
+                                             v, ip, ix, ll, kv_scale, kv_scale,
+                                             inv_freq=inv_freq)
+            kv_np = fp8.dequantize(codes, kv_scale)
         o = ref.reference_attention_paged(q_np.astype(np.float32), kv_np.astype(np.float32),
                                           ip, ix, ll)
         h = h + torch.from_numpy(np.ascontiguousarray(o, np.float32)).reshape(-1, cfg.hq * cfg.d) @ f(L["wo"]).T
