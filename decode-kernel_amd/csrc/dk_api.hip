@@ -63,11 +63,11 @@ int explicit_split(const Problem& p, int device) {
 }
 
 // Wavefronts per compute unit the balanced schedule keeps resident. Two measured best on
-// MI355X at every decode shape tried with a 16-bit cache (each wavefront keeps two pages
-// of loads in flight); four with an fp8 cache.
+// MI355X at every decode shape tried with rows of 256 bytes or more (each wavefront keeps
+// two pages of loads in flight); four with narrower rows (fp8 cache, or D = 64).
 int waves_per_cu(const Problem& p) {
   if (p.opt.waves_per_cu) return p.opt.waves_per_cu;
-  return p.opt.kv_dtype == DK_KV_FP8_E4M3 ? kDefaultWavesPerCUKv8 : kDefaultWavesPerCU;
+  return p.narrow_rows() ? kDefaultWavesPerCUNarrow : kDefaultWavesPerCU;
 }
 
 // Workgroups of the balanced grid: about waves_per_cu wavefronts per compute unit, a

@@ -41,7 +41,7 @@ void clear_error() { g_error.clear(); }
 const char* last_error() { return g_error.c_str(); }
 
 int heads_per_group(int group, int head_dim) {
-  const int cap = head_dim >= 256 ? 4 : 8;
+  const int cap = head_dim >= 256 ? 4 : 8;   // 8 heads at D = 256 would spill registers
   for (int h = cap; h > 1; h >>= 1)
     if (group % h == 0) return h;
   return 1;
@@ -94,7 +94,8 @@ Plan make_plan(const Problem& p) {
   pl.pairs_per_seq = p.hkv * pl.chunks;
   const bool kv8 = p.opt.kv_dtype == DK_KV_FP8_E4M3;
   pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group
-                                   : (kv8 ? kDefaultWavesPerGroupKv8 : kDefaultWavesPerGroup);
+                                   : (p.narrow_rows() ? kDefaultWavesPerGroupNarrow
+                                                      : kDefaultWavesPerGroup);
   // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
   // 64-byte row segments on the NHD layout (measured for both fp16 and bf16)
   pl.mfma = p.opt.qk_path == 1;

@@ -14,11 +14,13 @@ constexpr int kPageSize = 16;        // tokens per page (reference: PAGE_SIZE=16
 constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid (wavefronts)
 constexpr int kDefaultWavesPerCU = 2;
 constexpr int kDefaultWavesPerGroup = 2;
-// An fp8 page carries half the bytes for the same per-token arithmetic, so one wavefront
-// per SIMD is needed to keep HBM busy (measured: 93 us with 4 wavefronts per group vs
-// 162 us with 2 at B=32 ctx=8192 32/8/128)
-constexpr int kDefaultWavesPerCUKv8 = 4;
-constexpr int kDefaultWavesPerGroupKv8 = 4;
+// Rows of at most 128 bytes per kv head (fp8 at D <= 128, fp16/bf16 at D = 64) carry half
+// the bytes of a page for about the same per-token arithmetic, so one wavefront per SIMD
+// is needed to keep HBM busy (measured at B=32 ctx=8192: fp8 D=128 93 us with 4
+// wavefronts per group vs 162 with 2; fp16 D=64 92 vs 122)
+constexpr int kDefaultWavesPerCUNarrow = 4;
+constexpr int kDefaultWavesPerGroupNarrow = 4;
+constexpr int kNarrowRowBytes = 128;
 
 // Everything a launch needs that is known on the host.
 struct Problem {
@@ -34,6 +36,8 @@ struct Problem {
   int32_t batch = 0, hq = 0, hkv = 0, head_dim = 0, page_size = 0, dtype = 0;
   int64_t num_pages = 0, num_indices = 0;
   int32_t kv_esize() const { return opt.kv_dtype == DK_KV_FP8_E4M3 ? 1 : 2; }
+  // a kv head's row of one token is at most kNarrowRowBytes
+  bool narrow_rows() const { return (int64_t)head_dim * kv_esize() <= kNarrowRowBytes; }
   dk_strides st{};
   int32_t split = 0;          // 0: balanced persistent mode; >= 1: explicit split
   bool need_out = true;       // false for the pass-1-only entry point
