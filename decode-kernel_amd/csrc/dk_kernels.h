@@ -977,17 +977,27 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
 
 // ---------------------------------------------------------------- pass 2
 // Partial k of a row: O at po + k * stride_rows * D, m and l at pm / pl + k * stride_rows.
-// One wavefront per row, lanes over the D dims (E = D/64 each). The slots' loads are
-// issued kU at a time before any is consumed, so a row with many slots costs a few
-// memory round trips rather than one per slot.
+// One wavefront per row, lanes over the D dims (E = D/64 each). The O loads of the first
+// kU slots are issued before the m / l loads and the max, so a row with up to kU slots
+// costs one memory round trip; more slots are loaded kU at a time.
 template <class T, int D>
 __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const float* po,
                                           const float* pm, const float* pl, int nslots,
                                           int64_t stride_rows) {
   constexpr int E = D / 64;
-  constexpr int kU = E <= 2 ? 16 : 8;
+  constexpr int kU = E <= 2 ? 32 : 16;
   typedef float vecE __attribute__((ext_vector_type(E)));
   const int lane = threadIdx.x & 63;
+  const float* o = po + lane * E;
+  auto o_at = [&](int k) { return *reinterpret_cast<const vecE*>(o + (int64_t)k * stride_rows * D); };
+  // first batch of O (uniform guards: no load past the row's last slot)
+  const int cnt0 = min(nslots, kU);
+  vecE v0[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    v0[u] = vecE{};
+    if (u < cnt0) v0[u] = o_at(u);
+  }
   // the first 64 slots' m and l stay in registers (one slot per lane)
   float pm0 = kNegInf, pl0 = 0.f;
   if (lane < nslots) {
@@ -1009,18 +1019,20 @@ __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const flo
       L += wgt * lk;
     }
     const int cnt = min(64, nslots - k0);
-    const float* o = po + (int64_t)k0 * stride_rows * D + lane * E;
     int j = 0;
+    if (k0 == 0) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, u) * v0[u];   // zero past cnt0
+      j = cnt0;
+    }
     for (; j + kU <= cnt; j += kU) {
       vecE v[kU];
 #pragma unroll
-      for (int u = 0; u < kU; ++u)
-        v[u] = *reinterpret_cast<const vecE*>(o + (int64_t)(j + u) * stride_rows * D);
+      for (int u = 0; u < kU; ++u) v[u] = o_at(k0 + j + u);
 #pragma unroll
       for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, j + u) * v[u];
     }
-    for (; j < cnt; ++j)
-      acc += readlane_f(wgt, j) * *reinterpret_cast<const vecE*>(o + (int64_t)j * stride_rows * D);
+    for (; j < cnt; ++j) acc += readlane_f(wgt, j) * o_at(k0 + j);
   }
   L = wave_sum(L);
   const int b = row / m.hq, qh = row % m.hq;
