@@ -63,11 +63,12 @@ int explicit_split(const Problem& p, int device) {
 }
 
 // Wavefronts per compute unit the balanced schedule keeps resident. Two measured best on
-// MI355X at every decode shape tried with rows of 256 bytes or more (each wavefront keeps
-// two pages of loads in flight); four with narrower rows (fp8 cache, or D = 64).
-int waves_per_cu(const Problem& p) {
+// MI355X at every decode shape tried with rows of 256 bytes or more and up to 4 q heads
+// per wavefront (each wavefront keeps two pages of loads in flight); four with narrower
+// rows (fp8 cache, or D = 64) or 8 q heads per wavefront (twice the work per page).
+int waves_per_cu(const Problem& p, const Plan& pl) {
   if (p.opt.waves_per_cu) return p.opt.waves_per_cu;
-  return p.narrow_rows() ? kDefaultWavesPerCUNarrow : kDefaultWavesPerCU;
+  return p.narrow_rows() || pl.heads >= 8 ? kDefaultWavesPerCUNarrow : kDefaultWavesPerCU;
 }
 
 // Workgroups of the balanced grid: about waves_per_cu wavefronts per compute unit, a
@@ -75,7 +76,7 @@ int waves_per_cu(const Problem& p) {
 int64_t balanced_groups(const Problem& p, const Plan& pl, int cus) {
   const int64_t hc = pl.pairs_per_seq;
   const int64_t max_groups = std::max<int64_t>(hc, kMaxWaves / pl.waves / hc * hc);
-  const int64_t groups = std::max<int64_t>(1, (int64_t)cus * waves_per_cu(p) / pl.waves);
+  const int64_t groups = std::max<int64_t>(1, (int64_t)cus * waves_per_cu(p, pl) / pl.waves);
   return std::min(max_groups, std::max(hc, (groups + hc / 2) / hc * hc));
 }
 
@@ -158,6 +159,7 @@ int run(Problem p, bool do_merge, void* stream) {
   a.hkv = p.hkv;
   a.group = pl.group;
   a.chunks = pl.chunks;
+  a.per = pl.per;
   a.split = std::max(p.split, 1);
   a.num_indices = (int32_t)p.num_indices;
   a.num_pages = (uint32_t)std::min<int64_t>(p.num_pages, (int64_t)1 << 31);
@@ -200,6 +202,9 @@ int run(Problem p, bool do_merge, void* stream) {
     m.num_indices = a.num_indices;
     m.pairs_per_seq = pl.pairs_per_seq;
     m.heads = pl.heads;
+    m.group = pl.group;
+    m.per = pl.per;
+    m.chunks = pl.chunks;
     m.waves_per_pair = waves_per_pair;
     e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)
                           : launch_merge<BF16>(m, p.head_dim, pl.balanced, L.stream);

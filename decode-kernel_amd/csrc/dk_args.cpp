@@ -40,11 +40,15 @@ void clear_error() { g_error.clear(); }
 
 const char* last_error() { return g_error.c_str(); }
 
-int heads_per_group(int group, int head_dim) {
+HeadChunks head_chunks(int group, int head_dim) {
   const int cap = head_dim >= 256 ? 4 : 8;   // 8 heads at D = 256 would spill registers
-  for (int h = cap; h > 1; h >>= 1)
-    if (group % h == 0) return h;
-  return 1;
+  HeadChunks h;
+  const int c0 = (group + cap - 1) / cap;
+  h.per = (group + c0 - 1) / c0;
+  h.chunks = (group + h.per - 1) / h.per;
+  h.heads = 1;
+  while (h.heads < h.per) h.heads <<= 1;
+  return h;
 }
 
 void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,
@@ -61,10 +65,9 @@ int64_t split_rows(int32_t batch, int32_t hq, int32_t split) {
 }
 
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) {
-  const int group = hq / hkv;
-  const int heads = heads_per_group(group, head_dim);
-  const int64_t pairs = (int64_t)batch * hkv * (group / heads);
-  return (kMaxWaves + pairs) * heads;
+  const HeadChunks h = head_chunks(hq / hkv, head_dim);
+  const int64_t pairs = (int64_t)batch * hkv * h.chunks;
+  return (kMaxWaves + pairs) * h.heads;
 }
 
 size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split) {
@@ -89,13 +92,16 @@ int choose_split(int64_t units, int64_t slots, int64_t avg_pages_per_seq, int wa
 Plan make_plan(const Problem& p) {
   Plan pl;
   pl.group = p.hq / p.hkv;
-  pl.heads = heads_per_group(pl.group, p.head_dim);
-  pl.chunks = pl.group / pl.heads;
+  const HeadChunks hc = head_chunks(pl.group, p.head_dim);
+  pl.heads = hc.heads;
+  pl.per = hc.per;
+  pl.chunks = hc.chunks;
   pl.pairs_per_seq = p.hkv * pl.chunks;
   const bool kv8 = p.opt.kv_dtype == DK_KV_FP8_E4M3;
   pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group
-                                   : (p.narrow_rows() ? kDefaultWavesPerGroupNarrow
-                                                      : kDefaultWavesPerGroup);
+                                   : (p.narrow_rows() || pl.heads >= 8
+                                          ? kDefaultWavesPerGroupNarrow
+                                          : kDefaultWavesPerGroup);
   // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
   // 64-byte row segments on the NHD layout (measured for both fp16 and bf16)
   pl.mfma = p.opt.qk_path == 1;

@@ -15,9 +15,10 @@ constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid 
 constexpr int kDefaultWavesPerCU = 2;
 constexpr int kDefaultWavesPerGroup = 2;
 // Rows of at most 128 bytes per kv head (fp8 at D <= 128, fp16/bf16 at D = 64) carry half
-// the bytes of a page for about the same per-token arithmetic, so one wavefront per SIMD
-// is needed to keep HBM busy (measured at B=32 ctx=8192: fp8 D=128 93 us with 4
-// wavefronts per group vs 162 with 2; fp16 D=64 92 vs 122)
+// the bytes of a page for about the same per-token arithmetic, and 8 q heads per
+// wavefront double the arithmetic per byte: then one wavefront per SIMD is needed to keep
+// HBM busy (measured at B=32 ctx=8192 with 4 wavefronts per group vs 2: fp8 D=128 93 vs
+// 162 us; fp16 D=64 92 vs 122; 64 q / 8 kv heads at D=128 172 vs 254)
 constexpr int kDefaultWavesPerCUNarrow = 4;
 constexpr int kDefaultWavesPerGroupNarrow = 4;
 constexpr int kNarrowRowBytes = 128;
@@ -45,10 +46,20 @@ struct Problem {
 };
 
 // Launch shape derived from a problem.
+// A GQA group of `group` q heads is processed in `chunks` chunks of `per` consecutive q
+// heads (the last may hold fewer), each by a wavefront built for `heads` (the power of two
+// >= per; at most 8, 4 at D = 256) whose surplus heads are masked. One chunk whenever the
+// group fits, so every page is read once per kv head (e.g. 5, 6 or 7 q heads per kv head).
+struct HeadChunks {
+  int per = 1, chunks = 1, heads = 1;
+};
+HeadChunks head_chunks(int group, int head_dim);
+
 struct Plan {
   int group = 0;       // hq / hkv
-  int heads = 0;       // q heads handled by one wavefront (1, 2, 4 or 8)
-  int chunks = 0;      // group / heads
+  int heads = 0;       // q heads a wavefront is built for (1, 2, 4 or 8)
+  int per = 0;         // q heads per chunk (<= heads)
+  int chunks = 0;      // ceil(group / per)
   int pairs_per_seq = 0;   // hkv * chunks
   int waves = 0;       // wavefronts per workgroup
   bool mfma = false;   // q.k on MFMA (default: VALU dot2)
@@ -70,7 +81,7 @@ Plan make_plan(const Problem& p);
 
 // Heads per wavefront for a GQA group size (largest power of two <= 8, or <= 4 for
 // head_dim 256, that divides the group).
-int heads_per_group(int group, int head_dim);
+
 
 // fp32 partials: `rows` rows of head_dim floats + m + l, each array 256-byte aligned.
 void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,

@@ -86,6 +86,7 @@ struct Pass1Args {
                                       // same page (in-page offset, or V cache - K cache)
   int32_t kv_s, kv_h;                 // bytes
   int32_t batch, hq, hkv, group, chunks, split;
+  int32_t per;                        // q heads per chunk (the last chunk may have fewer)
   int32_t num_indices;
   uint32_t num_pages;                 // clamp bound for page ids (min(num_pages, 2^31))
   uint32_t page_extent;               // bytes one kv head's K (or V) rows of a page span (< 2^31)
@@ -104,6 +105,7 @@ struct MergeArgs {
   int32_t batch, hq, split;           // explicit split
   const int32_t* indptr;              // balanced: recompute each pair's slots
   int32_t num_indices, pairs_per_seq, heads, waves_per_pair;
+  int32_t group, per, chunks;         // balanced: q head -> (head chunk, slot row)
 };
 
 // ---------------------------------------------------------------- element types
@@ -327,6 +329,7 @@ struct Wave {
   static constexpr int NKL = KV8 ? D / 64 : NMF;
 
   int r16, c;
+  int hv;                 // valid q heads of this chunk (<= G); heads hv.. are masked
   u32 koff, voff, tok_s, extent;
   int64_t kv_v;
   float kscale, vscale;
@@ -358,18 +361,28 @@ struct Wave {
     return KV8 ? 64 * (i >> 1) + 16 * r16 + 8 * (i & 1) : 32 * i + 8 * r16;
   }
 
-  // q rows of the G heads starting at qbase (q_h bytes apart).
+  // q rows of the chunk's valid heads starting at qbase (q_h bytes apart); the rows of
+  // masked heads (h >= hv) are zero and never read.
   __device__ __forceinline__ void load_q(const uint8_t* qbase, int64_t q_h) {
     if constexpr (MFMA) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
-        const uint8_t* qp = qbase + (int64_t)(ss * GQ + c % GQ) * q_h;
+        const int h = ss * GQ + c % GQ;
+        const uint8_t* qp = qbase + (int64_t)h * q_h;
 #pragma unroll
-        for (int i = 0; i < NMF; ++i) ld_words_cached<4>(&qw[ss][4 * i], qp + 2 * q_dim0(i));
+        for (int i = 0; i < KW; ++i) qw[ss][i] = 0u;
+        if (h < hv) {
+#pragma unroll
+          for (int i = 0; i < NMF; ++i) ld_words_cached<4>(&qw[ss][4 * i], qp + 2 * q_dim0(i));
+        }
       }
     } else {
 #pragma unroll
-      for (int h = 0; h < G; ++h) ld_words_cached<VWT>(qv[h], qbase + (int64_t)h * q_h + 2 * DPL * c);
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int q = 0; q < VWT; ++q) qv[h][q] = 0u;
+        if (h < hv) ld_words_cached<VWT>(qv[h], qbase + (int64_t)h * q_h + 2 * DPL * c);
+      }
     }
   }
 
@@ -636,7 +649,7 @@ struct Wave {
       constexpr int k = decltype(kc)::value;
       const int h = 4 * k + r16;
       const float fh = row_head_scalar<k>(f);
-      if (h < G) {
+      if (h < hv) {
         float v[DPL];
 #pragma unroll
         for (int j = 0; j < DPL; ++j) v[j] = row_head<k>(j) * fh;
@@ -646,6 +659,7 @@ struct Wave {
     if (r16 == 0 && c < GQ) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
+        if (ss * GQ + c >= hv) continue;
         const int64_t r = row0 + (int64_t)(ss * GQ + c) * hstride;
         const bool seen = mtrue[ss] > kNegInf;
         a.part_m[r] = seen ? mtrue[ss] * kLn2 : kEmptyM;
@@ -661,7 +675,7 @@ struct Wave {
       const int h = 4 * k + r16;
       const float L = row_head_scalar<k>(lsum);
       const float inv = L > 0.f ? 1.f / L : 0.f;
-      if (h < G) {
+      if (h < hv) {
 #pragma unroll
         for (int j = 0; j < DPL; ++j)
           T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), row_head<k>(j) * inv);
@@ -805,7 +819,7 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += NW * 64) {
+    for (int idx = threadIdx.x; idx < wv.hv * D; idx += NW * 64) {
       const int h = idx / D, d = idx % D;
       float mt = kNegInf;
 #pragma unroll
@@ -877,7 +891,8 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   const int p0 = min(s * pps, npages);
   const int n = max(min(p0 + pps, npages) - p0, 0);
   const int valid_last = min(max(ld_const(a.last_len, b), 0), kPage);
-  const int qh0 = kvh * a.group + hc * G;
+  const int qh0 = kvh * a.group + hc * a.per;
+  wv.hv = min(a.per, a.group - hc * a.per);
 
   wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
   wv.reset();
@@ -939,7 +954,8 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
   const int kvh = hc / a.chunks;
-  const int qh0 = kvh * a.group + (hc % a.chunks) * G;
+  const int qh0 = kvh * a.group + (hc % a.chunks) * a.per;
+  wv.hv = min(a.per, a.group - (hc % a.chunks) * a.per);
   const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
 
   while (true) {
@@ -1061,7 +1077,8 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   const int L = (P + Wg - 1) / Wg;
   const int seq0 = sb(b);
   const int np = max(sb(b + 1), seq0) - seq0;
-  const int hc = qh / G, g = qh % G;
+  const int kvh = qh / m.group, r = qh % m.group;
+  const int hc = kvh * m.chunks + r / m.per, g = r % m.per;   // slot row g of G
   int nslots = 0;
   int64_t r0 = 0;
   if (np > 0 && L > 0) {

@@ -120,6 +120,7 @@ CASES = [
     (5, [0, 16, 17, 255, 1000], 8, 8, 64, torch.float16, "freelist"),
     (2, [700, 33], 16, 2, 256, torch.bfloat16, "permuted"),
     (2, 160, 64, 4, 128, torch.float16, "permuted"),
+    (3, [1, 300, 40], 14, 2, 128, torch.bfloat16, "permuted"),     # 7 q heads per kv head
 ]
 
 

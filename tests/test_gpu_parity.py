@@ -374,6 +374,54 @@ def test_balanced_head_layouts(d, hq, hkv):
         _check(out, want, label=f"d={d} {hq}/{hkv} wpc={wpc}")
 
 
+# GQA groups that are not a power of two, or exceed one chunk: the group is processed in
+# the fewest chunks of at most 8 q heads (4 at D=256), each by a wavefront sized to the
+# next power of two with the surplus heads masked (no q read, no output or partial write)
+PADDED_GROUPS = [(128, 3, 1), (128, 10, 2), (64, 12, 2), (128, 14, 2), (128, 20, 2),
+                 (64, 24, 2), (128, 48, 2), (256, 5, 1), (256, 12, 2)]
+
+
+@pytest.mark.parametrize("d,hq,hkv", PADDED_GROUPS)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_padded_head_chunks(d, hq, hkv, dtype):
+    lens = [1, 300, 17, 129]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        4, lens, hq, hkv, d, dtype=dtype, device=DEV, page_table="permuted", pool_pages=60,
+        seed=d + hq)
+    want = _oracle(q, kv, indptr, ids, last)
+    hint = attention.plan_hint(indptr.cpu())
+    for split, sched, h in ((1, 0, 0), (3, 0, 0), (0, 1, 0), (0, 0, hint)):
+        for path in (1, 2):
+            for waves in (0, 1, 4):
+                label = (f"padded {dtype} d={d} {hq}/{hkv} S={split} sched={sched} "
+                         f"path={path} waves={waves}")
+                _announce(label)
+                out = decode_attention(q, kv, indptr, ids, last, split_kv=split, schedule=sched,
+                                       max_pages_per_seq=h, qk_path=path,
+                                       waves_per_group=waves)
+                torch.cuda.synchronize()
+                _check(out, want, label=label)
+
+
+def test_padded_head_chunks_partials_and_neighbours():
+    # partials of a 5-head group (one chunk of 8, 3 masked) equal the oracle's, and no
+    # masked head's write reaches a neighbouring group's rows: q heads of kv head 1 come
+    # out right although kv head 0's chunk has masked heads right before them
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        2, [500, 61], 10, 2, 128, device=DEV, page_table="permuted", seed=4)
+    for S in (1, 3, 8):
+        _announce(f"padded partials S={S}")
+        po, pm, pl = decode_partials(q, kv, indptr, ids, last, S)
+        torch.cuda.synchronize()
+        O, m, l = skv.split_partials(to_np(q), to_np(kv), to_np(indptr), to_np(ids),
+                                     to_np(last), S)
+        _check_partials(po, pm, pl, O, m, l, q.dtype)
+    out = torch.full_like(q, float("nan"))
+    decode_attention(q, kv, indptr, ids, last, split_kv=0, out=out)
+    torch.cuda.synchronize()
+    _check(out, _oracle(q, kv, indptr, ids, last), label="padded out= over NaN")
+
+
 def test_balanced_pass1_alone_runs():
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         4, 1000, 32, 8, 128, device=DEV, page_table="permuted", seed=5)
