@@ -113,7 +113,7 @@ int run(Problem p, bool do_merge, void* stream) {
     if (auto_one_pass(p, pl, cus)) {
       p.split = 1;
       pl.balanced = false;
-      pl.grid = (int64_t)p.batch * pl.pairs_per_seq;
+      pl.grid = split_grid(p.batch, p.hkv, 1, pl.chunks);
     } else {
       pl.grid = balanced_groups(p, pl, cus);
       waves_per_pair = (int)(pl.grid / pl.pairs_per_seq);
@@ -205,6 +205,7 @@ int run(Problem p, bool do_merge, void* stream) {
     m.group = pl.group;
     m.per = pl.per;
     m.chunks = pl.chunks;
+    m.hkv = p.hkv;
     m.waves_per_pair = waves_per_pair;
     e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)
                           : launch_merge<BF16>(m, p.head_dim, pl.balanced, L.stream);

@@ -89,6 +89,11 @@ int choose_split(int64_t units, int64_t slots, int64_t avg_pages_per_seq, int wa
   return (int)std::min<int64_t>(s, 4096);
 }
 
+int64_t split_grid(int32_t batch, int32_t hkv, int32_t split, int chunks) {
+  const int64_t units = (int64_t)batch * hkv * split;
+  return chunks == 1 ? units : (units + kXcds - 1) / kXcds * kXcds * chunks;
+}
+
 Plan make_plan(const Problem& p) {
   Plan pl;
   pl.group = p.hq / p.hkv;
@@ -107,7 +112,7 @@ Plan make_plan(const Problem& p) {
   pl.mfma = p.opt.qk_path == 1;
   pl.kv8 = kv8;
   pl.balanced = p.split == 0;
-  pl.grid = pl.balanced ? 0 : (int64_t)p.batch * pl.pairs_per_seq * std::max(p.split, 1);
+  pl.grid = pl.balanced ? 0 : split_grid(p.batch, p.hkv, std::max(p.split, 1), pl.chunks);
   return pl;
 }
 

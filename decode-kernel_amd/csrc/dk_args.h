@@ -12,6 +12,7 @@ namespace dk {
 
 constexpr int kPageSize = 16;        // tokens per page (reference: PAGE_SIZE=16, attention_ext.cu:509)
 constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid (wavefronts)
+constexpr int kXcds = 8;             // MI355X: the dispatcher deals workgroups to 8 XCDs in turn
 constexpr int kDefaultWavesPerCU = 2;
 constexpr int kDefaultWavesPerGroup = 2;
 // Rows of at most 128 bytes per kv head (fp8 at D <= 128, fp16/bf16 at D = 64) carry half
@@ -67,6 +68,11 @@ struct Plan {
   bool kv8 = false;    // fp8 cache
   int64_t grid = 0;    // workgroups of pass 1 (balanced: filled in from the device)
 };
+
+// Workgroups of the explicit-split kernel for `split` splits: one per (sequence, kv head,
+// split, head chunk); with several head chunks the count is padded to whole rounds of
+// kXcds so that a pair's chunks can sit kXcds ids apart (one XCD).
+int64_t split_grid(int32_t batch, int32_t hkv, int32_t split, int chunks);
 
 // Records a message for dk_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -38,6 +38,8 @@
 
 #include <utility>
 
+#include "dk_args.h"   // shared constants (kXcds)
+
 namespace dk {
 
 // f(std::integral_constant<int, i>) for i = 0 .. N-1, each i a compile-time constant
@@ -105,7 +107,7 @@ struct MergeArgs {
   int32_t batch, hq, split;           // explicit split
   const int32_t* indptr;              // balanced: recompute each pair's slots
   int32_t num_indices, pairs_per_seq, heads, waves_per_pair;
-  int32_t group, per, chunks;         // balanced: q head -> (head chunk, slot row)
+  int32_t group, per, chunks, hkv;    // balanced: q head -> (head chunk, slot row)
 };
 
 // ---------------------------------------------------------------- element types
@@ -877,9 +879,17 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
 
-  int t = blockIdx.x;
-  const int hc = t % a.chunks;
-  t /= a.chunks;
+  // workgroup -> (head chunk, kv head, split, sequence). The head chunks of one (sequence,
+  // kv head, split) read the same pages: they are placed kXcds workgroup ids apart (the
+  // dispatcher deals workgroups to the XCDs in turn), so they run on one XCD, close in
+  // time, and the later reads of a page can hit that XCD's L2.
+  int hc = 0, t = blockIdx.x;
+  if (a.chunks > 1) {
+    const int x = t % kXcds, y = t / kXcds;
+    hc = y % a.chunks;
+    t = (y / a.chunks) * kXcds + x;
+    if (t >= a.batch * a.hkv * a.split) return;   // padding of the last XCD round
+  }
   const int kvh = t % a.hkv;
   t /= a.hkv;
   const int s = t % a.split;
@@ -953,9 +963,11 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   int pg = u - (seq0 - base);
   if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
-  const int kvh = hc / a.chunks;
-  const int qh0 = kvh * a.group + (hc % a.chunks) * a.per;
-  wv.hv = min(a.per, a.group - (hc % a.chunks) * a.per);
+  // head chunks are chunk-major (hc = chunk * hkv + kv head), so the chunks of one kv head
+  // are hkv workgroup ids apart: on one XCD when hkv is a multiple of kXcds
+  const int kvh = hc % a.hkv, chunk = hc / a.hkv;
+  const int qh0 = kvh * a.group + chunk * a.per;
+  wv.hv = min(a.per, a.group - chunk * a.per);
   const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
 
   while (true) {
@@ -1078,7 +1090,7 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   const int seq0 = sb(b);
   const int np = max(sb(b + 1), seq0) - seq0;
   const int kvh = qh / m.group, r = qh % m.group;
-  const int hc = kvh * m.chunks + r / m.per, g = r % m.per;   // slot row g of G
+  const int hc = (r / m.per) * m.hkv + kvh, g = r % m.per;   // chunk-major; slot row g of G
   int nslots = 0;
   int64_t r0 = 0;
   if (np > 0 && L > 0) {
