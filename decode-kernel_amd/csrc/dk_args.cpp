@@ -40,8 +40,16 @@ void clear_error() { g_error.clear(); }
 
 const char* last_error() { return g_error.c_str(); }
 
-HeadChunks head_chunks(int group, int head_dim) {
-  const int cap = head_dim >= 256 ? 4 : 8;   // 8 heads at D = 256 would spill registers
+int valu_head_cap(int head_dim) { return head_dim >= 256 ? 4 : 8; }
+
+bool qk_on_mfma(int qk_path, int group, int head_dim) {
+  return qk_path == 1 || (qk_path == 0 && group > valu_head_cap(head_dim));
+}
+
+HeadChunks head_chunks(int group, int head_dim, bool mfma) {
+  // VALU q.k: at most 8 heads (4 at D = 256; 8 would spill registers). MFMA q.k: up to 16,
+  // one per MFMA column, in the same registers at any head count
+  const int cap = mfma ? 16 : valu_head_cap(head_dim);
   HeadChunks h;
   const int c0 = (group + cap - 1) / cap;
   h.per = (group + c0 - 1) / c0;
@@ -65,9 +73,14 @@ int64_t split_rows(int32_t batch, int32_t hq, int32_t split) {
 }
 
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) {
-  const HeadChunks h = head_chunks(hq / hkv, head_dim);
-  const int64_t pairs = (int64_t)batch * hkv * h.chunks;
-  return (kMaxWaves + pairs) * h.heads;
+  // enough rows for either q.k path (the path is an option of the call)
+  int64_t rows = 0;
+  for (bool mfma : {false, true}) {
+    const HeadChunks h = head_chunks(hq / hkv, head_dim, mfma);
+    const int64_t pairs = (int64_t)batch * hkv * h.chunks;
+    rows = std::max<int64_t>(rows, (kMaxWaves + pairs) * h.heads);
+  }
+  return rows;
 }
 
 size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split) {
@@ -97,7 +110,11 @@ int64_t split_grid(int32_t batch, int32_t hkv, int32_t split, int chunks) {
 Plan make_plan(const Problem& p) {
   Plan pl;
   pl.group = p.hq / p.hkv;
-  const HeadChunks hc = head_chunks(pl.group, p.head_dim);
+  // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
+  // 64-byte row segments on the NHD layout (measured for both fp16 and bf16); groups too
+  // large for one VALU chunk take the MFMA path, which holds 16 heads per wavefront
+  pl.mfma = qk_on_mfma(p.opt.qk_path, p.hq / p.hkv, p.head_dim);
+  const HeadChunks hc = head_chunks(pl.group, p.head_dim, pl.mfma);
   pl.heads = hc.heads;
   pl.per = hc.per;
   pl.chunks = hc.chunks;
@@ -107,9 +124,6 @@ Plan make_plan(const Problem& p) {
                                    : (p.narrow_rows() || pl.heads >= 8
                                           ? kDefaultWavesPerGroupNarrow
                                           : kDefaultWavesPerGroup);
-  // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
-  // 64-byte row segments on the NHD layout (measured for both fp16 and bf16)
-  pl.mfma = p.opt.qk_path == 1;
   pl.kv8 = kv8;
   pl.balanced = p.split == 0;
   pl.grid = pl.balanced ? 0 : split_grid(p.batch, p.hkv, std::max(p.split, 1), pl.chunks);

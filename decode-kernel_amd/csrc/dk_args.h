@@ -49,12 +49,16 @@ struct Problem {
 // Launch shape derived from a problem.
 // A GQA group of `group` q heads is processed in `chunks` chunks of `per` consecutive q
 // heads (the last may hold fewer), each by a wavefront built for `heads` (the power of two
-// >= per; at most 8, 4 at D = 256) whose surplus heads are masked. One chunk whenever the
+// >= per; at most 8 with VALU q.k (4 at D = 256), 16 with MFMA q.k) whose surplus heads
+// are masked. One chunk whenever the
 // group fits, so every page is read once per kv head (e.g. 5, 6 or 7 q heads per kv head).
 struct HeadChunks {
   int per = 1, chunks = 1, heads = 1;
 };
-HeadChunks head_chunks(int group, int head_dim);
+HeadChunks head_chunks(int group, int head_dim, bool mfma);
+// q.k path of a call: qk_path 1 / 2 force MFMA / VALU; 0 takes the VALU path unless the
+// group exceeds one VALU chunk (8 heads, 4 at D = 256)
+bool qk_on_mfma(int qk_path, int group, int head_dim);
 
 struct Plan {
   int group = 0;       // hq / hkv

@@ -223,6 +223,7 @@ __device__ __forceinline__ float max_xor32(float x) {
 // of a head set), result in all of them.
 template <int GQ>
 __device__ __forceinline__ float allmax_head(float x) {
+  if constexpr (GQ == 16) return max_xor32(max_xor16(x));   // head = lane column
   if constexpr (GQ == 1) {
     x = fmaxf(x, xor1(x));
     x = fmaxf(x, xor2(x));
@@ -316,8 +317,14 @@ __device__ __forceinline__ int seq_begin(const Pass1Args& a, int b) {
 // (E4M3) values, widened to T in registers after the loads.
 template <class T, int D, int G, bool MFMA, bool KV8 = false>
 struct Wave {
-  static constexpr int GQ = G < 4 ? G : 4;   // heads per column set
-  static constexpr int NS = G / GQ;          // column sets (G = 8 -> 2)
+  // WIDE (q.k on MFMA with 8 or 16 heads): the MFMA's 16 columns are 16 distinct q heads,
+  // so lane (r16, c) holds the scores of head c and the P.V accumulators of heads
+  // 4*r16 .. 4*r16+3; registers do not grow with G. Otherwise every lane row holds all
+  // G heads (columns repeat the GQ heads of a set).
+  static constexpr bool WIDE = MFMA && G >= 8;
+  static constexpr int GQ = WIDE ? 16 : (G < 4 ? G : 4);   // heads per column set
+  static constexpr int NS = WIDE ? 1 : G / GQ;             // column sets (G = 8 -> 2)
+  static constexpr int AH = WIDE ? 4 : G;                  // heads held in acc
   static constexpr int DPL = D / 16;         // V (and VALU-path K) dims per lane
   static constexpr int VWT = DPL / 2;        // words per token per lane
   static constexpr int KW = D / 8;           // K words per lane per page (both paths)
@@ -338,7 +345,7 @@ struct Wave {
   u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, the dims of
                                              // the K operand of MFMA i (see q_dim0)
   u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
-  float acc[G][DPL];      // after reduce_rows: head h, dim c*DPL + j (every lane row)
+  float acc[AH][DPL];     // after reduce_rows: head h (WIDE: head 4*r16 + h), dim c*DPL + j
   f32x4 cv[NS][DPL];      // while pages stream: the P.V accumulators as MFMA C vectors,
                           // element g = head ss*GQ + g of dim c*DPL + j
   float mref[NS], mtrue[NS], lsum[NS];
@@ -529,8 +536,13 @@ struct Wave {
         const float al = __builtin_amdgcn_exp2f(mref[ss] - mn);
         lsum[ss] *= al;
         f32x4 ab4 = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (WIDE) {
 #pragma unroll
-        for (int g = 0; g < GQ; ++g) ab4[g] = GQ > 1 ? quad_bcast_i(al, g) : al;
+          for (int i = 0; i < 4; ++i) ab4[i] = col_value(al, i);
+        } else {
+#pragma unroll
+          for (int g = 0; g < GQ; ++g) ab4[g] = GQ > 1 ? quad_bcast_i(al, g) : al;
+        }
 #pragma unroll
         for (int j = 0; j < DPL; ++j) cv[ss][j] *= ab4;
         mref[ss] = mn;
@@ -591,12 +603,26 @@ struct Wave {
       mtrue[ss] = allmax_head<GQ>(mtrue[ss]);
     }
     // the MFMA P.V already summed over all tokens of every lane row
+    if constexpr (WIDE) {
 #pragma unroll
-    for (int ss = 0; ss < NS; ++ss)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int g = 0; g < GQ; ++g)
+        for (int j = 0; j < DPL; ++j) acc[i][j] = cv[0][j][i] * vscale;
+    } else {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] = cv[ss][j][g] * vscale;
+      for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+        for (int g = 0; g < GQ; ++g)
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[ss * GQ + g][j] = cv[ss][j][g] * vscale;
+    }
+  }
+
+  // WIDE: a per-head value x that lives in lane column h (lsum, mref, mtrue of head h),
+  // fetched for this lane row's head 4*r16 + i (all lanes must take part)
+  __device__ __forceinline__ float col_value(float x, int i) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                         (16 * r16 + 4 * r16 + i) << 2, __builtin_bit_cast(int, x)));
   }
 
   // After reduce_rows every lane holds every head's sums. Lane row r16 stores heads
@@ -647,42 +673,76 @@ struct Wave {
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss)
       f[ss] = mtrue[ss] > kNegInf ? __builtin_amdgcn_exp2f(mref[ss] - mtrue[ss]) : 0.f;
-    static_for<KR>([&](auto kc) {
-      constexpr int k = decltype(kc)::value;
-      const int h = 4 * k + r16;
-      const float fh = row_head_scalar<k>(f);
-      if (h < hv) {
-        float v[DPL];
+    if constexpr (WIDE) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) v[j] = row_head<k>(j) * fh;
-        st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * r16 + i;
+        const float fh = col_value(f[0], i);
+        if (h < hv) {
+          float v[DPL];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) v[j] = acc[i][j] * fh;
+          st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
+        }
       }
-    });
-    if (r16 == 0 && c < GQ) {
+      if (r16 == 0 && c < hv) {
+        const int64_t r = row0 + (int64_t)c * hstride;
+        const bool seen = mtrue[0] > kNegInf;
+        a.part_m[r] = seen ? mtrue[0] * kLn2 : kEmptyM;
+        a.part_l[r] = lsum[0] * f[0];
+      }
+    } else {
+      static_for<KR>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int h = 4 * k + r16;
+        const float fh = row_head_scalar<k>(f);
+        if (h < hv) {
+          float v[DPL];
 #pragma unroll
-      for (int ss = 0; ss < NS; ++ss) {
-        if (ss * GQ + c >= hv) continue;
-        const int64_t r = row0 + (int64_t)(ss * GQ + c) * hstride;
-        const bool seen = mtrue[ss] > kNegInf;
-        a.part_m[r] = seen ? mtrue[ss] * kLn2 : kEmptyM;
-        a.part_l[r] = lsum[ss] * f[ss];
+          for (int j = 0; j < DPL; ++j) v[j] = row_head<k>(j) * fh;
+          st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
+        }
+      });
+      if (r16 == 0 && c < GQ) {
+#pragma unroll
+        for (int ss = 0; ss < NS; ++ss) {
+          if (ss * GQ + c >= hv) continue;
+          const int64_t r = row0 + (int64_t)(ss * GQ + c) * hstride;
+          const bool seen = mtrue[ss] > kNegInf;
+          a.part_m[r] = seen ? mtrue[ss] * kLn2 : kEmptyM;
+          a.part_l[r] = lsum[ss] * f[ss];
+        }
       }
     }
   }
 
   // After reduce_rows: normalised output of the G heads (q head h at out + h * o_h).
   __device__ __forceinline__ void store_output(uint8_t* out, int64_t o_h) {
-    static_for<KR>([&](auto kc) {
-      constexpr int k = decltype(kc)::value;
-      const int h = 4 * k + r16;
-      const float L = row_head_scalar<k>(lsum);
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      if (h < hv) {
+    if constexpr (WIDE) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j)
-          T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), row_head<k>(j) * inv);
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * r16 + i;
+        const float L = col_value(lsum[0], i);
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        if (h < hv) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j)
+            T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), acc[i][j] * inv);
+        }
       }
-    });
+    } else {
+      static_for<KR>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int h = 4 * k + r16;
+        const float L = row_head_scalar<k>(lsum);
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        if (h < hv) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j)
+            T::store(out + (int64_t)h * o_h + 2 * (c * DPL + j), row_head<k>(j) * inv);
+        }
+      });
+    }
   }
 };
 
@@ -803,18 +863,30 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
     else wv.store_partial(a, prow0, phstride);
   } else {
     const int w = uniform(threadIdx.x >> 6);
-    static_for<WV::KR>([&](auto kc) {
-      constexpr int k = decltype(kc)::value;
-      const int h = 4 * k + wv.r16;
-      if (h < G) {
+    if constexpr (WV::WIDE) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j)
-          sm.acc[w][h][wv.c * DPL + j] = wv.template row_head<k>(j);
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * wv.r16 + i;
+        if (h < G) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) sm.acc[w][h][wv.c * DPL + j] = wv.acc[i][j];
+        }
       }
-    });
+    } else {
+      static_for<WV::KR>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int h = 4 * k + wv.r16;
+        if (h < G) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j)
+            sm.acc[w][h][wv.c * DPL + j] = wv.template row_head<k>(j);
+        }
+      });
+    }
     if (wv.r16 == 0 && wv.c < GQ) {
 #pragma unroll
       for (int ss = 0; ss < NS; ++ss) {
+        if (ss * GQ + wv.c >= G) continue;
         sm.m[w][ss * GQ + wv.c] = wv.mref[ss];
         sm.mt[w][ss * GQ + wv.c] = wv.mtrue[ss];
         sm.l[w][ss * GQ + wv.c] = wv.lsum[ss];

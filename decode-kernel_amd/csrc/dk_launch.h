@@ -79,8 +79,12 @@ const void* pass1_sym_g(int heads, int waves, bool balanced) {
     case 2: return pass1_sym_w<T, D, 2, M, KV8>(waves, balanced);
     case 4: return pass1_sym_w<T, D, 4, M, KV8>(waves, balanced);
     case 8:
-      // 8 heads at D = 256 do not fit the registers of a wavefront without spilling
-      if constexpr (D <= 128) return pass1_sym_w<T, D, 8, M, KV8>(waves, balanced);
+      // 8 heads at D = 256 on the VALU path do not fit a wavefront's registers; the MFMA
+      // path holds up to 16 heads in the same registers
+      if constexpr (D <= 128 || M) return pass1_sym_w<T, D, 8, M, KV8>(waves, balanced);
+      return nullptr;
+    case 16:
+      if constexpr (M) return pass1_sym_w<T, D, 16, M, KV8>(waves, balanced);
       return nullptr;
     default: return nullptr;
   }

@@ -375,10 +375,13 @@ def test_balanced_head_layouts(d, hq, hkv):
 
 
 # GQA groups that are not a power of two, or exceed one chunk: the group is processed in
-# the fewest chunks of at most 8 q heads (4 at D=256), each by a wavefront sized to the
-# next power of two with the surplus heads masked (no q read, no output or partial write)
+# the fewest chunks of at most 8 q heads (4 at D=256) on the VALU q.k path or 16 on the
+# MFMA path (the default for groups beyond one VALU chunk), each by a wavefront sized to
+# the next power of two with the surplus heads masked (no q read, no output or partial
+# write)
 PADDED_GROUPS = [(128, 3, 1), (128, 10, 2), (64, 12, 2), (128, 14, 2), (128, 20, 2),
-                 (64, 24, 2), (128, 48, 2), (256, 5, 1), (256, 12, 2)]
+                 (64, 24, 2), (128, 48, 2), (256, 5, 1), (256, 12, 2), (128, 32, 1),
+                 (64, 40, 1), (256, 17, 1)]
 
 
 @pytest.mark.parametrize("d,hq,hkv", PADDED_GROUPS)
@@ -391,7 +394,7 @@ def test_padded_head_chunks(d, hq, hkv, dtype):
     want = _oracle(q, kv, indptr, ids, last)
     hint = attention.plan_hint(indptr.cpu())
     for split, sched, h in ((1, 0, 0), (3, 0, 0), (0, 1, 0), (0, 0, hint)):
-        for path in (1, 2):
+        for path in (0, 1, 2):
             for waves in (0, 1, 4):
                 label = (f"padded {dtype} d={d} {hq}/{hkv} S={split} sched={sched} "
                          f"path={path} waves={waves}")
