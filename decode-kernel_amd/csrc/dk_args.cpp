@@ -42,8 +42,13 @@ const char* last_error() { return g_error.c_str(); }
 
 int valu_head_cap(int head_dim) { return head_dim >= 256 ? 4 : 8; }
 
-bool qk_on_mfma(int qk_path, int group, int head_dim) {
-  return qk_path == 1 || (qk_path == 0 && group > valu_head_cap(head_dim));
+bool qk_on_mfma(int qk_path, int group, int head_dim, bool kv8) {
+  // automatic: MFMA once the group exceeds what the VALU path serves best in one chunk --
+  // 8 heads, or 4 at D = 256 and over an fp8 cache (measured at B=32 ctx 8192, one pass:
+  // fp8 40/8 and 64/8 heads 156 us VALU vs 116 MFMA; fp16 64/8 171 vs 185 and at D=64
+  // 103 vs 115, so 16-bit caches keep the VALU path up to 8 heads)
+  const int cap = kv8 ? 4 : valu_head_cap(head_dim);
+  return qk_path == 1 || (qk_path == 0 && group > cap);
 }
 
 HeadChunks head_chunks(int group, int head_dim, bool mfma) {
@@ -113,7 +118,8 @@ Plan make_plan(const Problem& p) {
   // q.k on the VALU by default: its full-row K loads stream faster than the MFMA path's
   // 64-byte row segments on the NHD layout (measured for both fp16 and bf16); groups too
   // large for one VALU chunk take the MFMA path, which holds 16 heads per wavefront
-  pl.mfma = qk_on_mfma(p.opt.qk_path, p.hq / p.hkv, p.head_dim);
+  pl.mfma = qk_on_mfma(p.opt.qk_path, p.hq / p.hkv, p.head_dim,
+                       p.opt.kv_dtype == DK_KV_FP8_E4M3);
   const HeadChunks hc = head_chunks(pl.group, p.head_dim, pl.mfma);
   pl.heads = hc.heads;
   pl.per = hc.per;
