@@ -70,12 +70,13 @@ typedef struct {
 /* Optional tuning knobs (NULL = defaults). No counterpart in the reference, which
  * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
 typedef struct {
-  int32_t qk_path;         /* 0 = default (VALU dot2), 1 = MFMA q.k, 2 = VALU q.k;
-                              P.V always runs on MFMA                                      */
-  int32_t waves_per_group; /* 0 = default (2; 4 with an fp8 cache); 1, 2 or 4 wavefronts
-                              per workgroup                                               */
+  int32_t qk_path;         /* 0 = automatic: VALU dot2 q.k up to 8 q heads per kv head (4 at
+                              D = 256 or over an fp8 cache), MFMA q.k with 16 heads per
+                              wavefront beyond; 1 = MFMA, 2 = VALU; P.V always on MFMA    */
+  int32_t waves_per_group; /* 0 = default: 2, or 4 with kv-head rows of <= 128 bytes (fp8,
+                              or D = 64) or 8+ heads per wavefront; else 1, 2 or 4        */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
-                              schedules aim for (0 = default: 2; 4 with an fp8 cache)     */
+                              schedules aim for (0 = default: 2, or 4 as above)           */
   int32_t schedule;        /* split_kv == 0: 0 = automatic, 1 = balanced, 2 = one workgroup
                               per (sequence, kv head) (split_kv == 1)                       */
   int32_t max_pages_per_seq; /* plan hint for split_kv == 0: the most pages any sequence
