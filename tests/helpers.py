@@ -52,3 +52,17 @@ def err_stats(out: torch.Tensor, ref: np.ndarray):
     o = out.detach().float().cpu().numpy().astype(np.float64)
     d = np.abs(o - np.asarray(ref, np.float64))
     return float(d.max()) if d.size else 0.0, float(d.mean()) if d.size else 0.0
+
+
+def check_partials(po, pm, pl, O, m, l, dtype):
+    """Pass-1 partials vs the exact ones. m is the split max of the scaled scores and l
+    the fp32 sum of exp(s - m). P.V weights p enter the MFMA as hi + lo parts of the
+    element type (relative error 2^-22 for fp16, 2^-17 for bf16), so O is compared
+    through the normalised O / l, with |V| <= ~5 in these inputs."""
+    pm, pl, po = pm.cpu().numpy(), pl.cpu().numpy(), po.cpu().numpy()
+    np.testing.assert_allclose(pm, m, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(pl, l, rtol=1e-5, atol=1e-6)
+    live = l > 0
+    np.testing.assert_allclose(po[live] / pl[live][:, None], O[live] / l[live][:, None],
+                               rtol=0, atol=1e-4 if dtype == torch.float16 else 2e-4)
+    assert (po[~live] == 0).all()

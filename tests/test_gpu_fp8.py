@@ -244,3 +244,24 @@ def test_full_size_fp8_equals_fp16_on_the_same_values(metric_fp8, scales):
             assert bool((diff <= b.float().abs() * 2.0 ** -10 + 2.0 ** -24).all()), (qk, split,
                                                                                       sched)
     del kv16
+
+
+def test_fp8_partials_match_oracle():
+    # pass 1 alone over an fp8 cache: the reference's (O, m, l) partials of the dequantised
+    # values (v_scale multiplies O only; k_scale enters the scores, hence m)
+    from helpers import check_partials
+    from oracle import split_kv as skv
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(2, [500, 61], 8, 2, 128, device=DEV,
+                                                          page_table="permuted", seed=3)
+    ks, vs = 0.5, 0.25
+    codes = _quantize(kv, ks, vs)
+    deq = _dequantize(codes, ks, vs)
+    kv8 = _codes_to_device(codes)
+    for S in (1, 3, 8):
+        _announce(f"fp8 partials S={S}")
+        po, pm, pl = attention.decode_partials(q, kv8, indptr, ids, last, S, k_scale=ks,
+                                               v_scale=vs)
+        torch.cuda.synchronize()
+        O, m, l = skv.split_partials(to_np(q).astype(np.float32), deq, to_np(indptr),
+                                     to_np(ids), to_np(last), S)
+        check_partials(po, pm, pl, O, m, l, q.dtype)

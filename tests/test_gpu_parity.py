@@ -13,21 +13,8 @@ import torch
 
 import attention
 import layout
-
-
-def _check_partials(po, pm, pl, O, m, l, dtype):
-    """Pass-1 partials vs the exact ones. m is the split max of the scaled scores and l
-    the fp32 sum of exp(s - m). P.V weights p enter the MFMA as hi + lo parts of the
-    element type (relative error 2^-22 for fp16, 2^-17 for bf16), so O is compared
-    through the normalised O / l, with |V| <= ~5 in these inputs."""
-    pm, pl, po = pm.cpu().numpy(), pl.cpu().numpy(), po.cpu().numpy()
-    np.testing.assert_allclose(pm, m, rtol=1e-5, atol=1e-5)
-    np.testing.assert_allclose(pl, l, rtol=1e-5, atol=1e-6)
-    live = l > 0
-    np.testing.assert_allclose(po[live] / pl[live][:, None], O[live] / l[live][:, None],
-                               rtol=0, atol=1e-4 if dtype == torch.float16 else 2e-4)
-    assert (po[~live] == 0).all()
 from attention import decode_attention, decode_partials, merge_partials
+from helpers import check_partials as _check_partials
 from helpers import err_stats, golden_to_torch, load_golden, to_np
 from oracle import reference as ref
 from oracle import split_kv as skv
