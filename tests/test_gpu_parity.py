@@ -412,6 +412,23 @@ def test_padded_head_chunks_partials_and_neighbours():
     _check(out, _oracle(q, kv, indptr, ids, last), label="padded out= over NaN")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_hnd_cache_as_a_strided_view(dtype):
+    # FlashInfer's HND layout (pages, 2, kv_heads, 16, head_dim) is the NHD call on the
+    # permuted view: the strides carry the layout, no copy
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        3, [700, 16, 129], 32, 8, 128, dtype=dtype, device=DEV, page_table="permuted", seed=8)
+    want = _oracle(q, kv, indptr, ids, last)
+    hnd = kv.permute(0, 1, 3, 2, 4).contiguous()        # the HND storage of the same values
+    view = hnd.permute(0, 1, 3, 2, 4)                    # seen as NHD
+    assert view.data_ptr() == hnd.data_ptr() and not view.is_contiguous()
+    for split, path in ((1, 0), (0, 0), (4, 1), (0, 2)):
+        _announce(f"HND view {dtype} S={split} path={path}")
+        out = decode_attention(q, view, indptr, ids, last, split_kv=split, qk_path=path)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"HND S={split} path={path}")
+
+
 def test_balanced_pass1_alone_runs():
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         4, 1000, 32, 8, 128, device=DEV, page_table="permuted", seed=5)
