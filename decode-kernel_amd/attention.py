@@ -138,6 +138,16 @@ def _kv_options(kv, k_scale, v_scale):
     return dk_lib.DK_KV_FP8_E4M3, scales[0], scales[1]
 
 
+def _logit_cap(logit_cap) -> float:
+    """logit_cap as dk_options takes it: 0.0 for off (None or 0), else finite and > 0."""
+    if logit_cap is None:
+        return 0.0
+    cap = float(logit_cap)
+    if not math.isfinite(cap) or cap < 0.0:
+        _fail(f"logit_cap must be finite and >= 0 (0 = off), got {logit_cap}")
+    return cap
+
+
 def _strides(q, kv_data, out) -> dk_lib.DkStrides:
     s = dk_lib.DkStrides()
     s.q_b, s.q_h = q.stride(0), q.stride(1)
@@ -196,6 +206,7 @@ def decode_attention(
     sm_scale: Optional[float] = None,
     k_scale: Optional[float] = None,
     v_scale: Optional[float] = None,
+    logit_cap: Optional[float] = None,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
@@ -225,6 +236,9 @@ def decode_attention(
         sm_scale         : softmax scale; None = 1/sqrt(head_dim) as in the reference
         k_scale, v_scale : fp8 cache only: K = k_scale * fp8 value, V = v_scale * fp8 value
                            (per tensor; None = 1)
+        logit_cap        : logit soft-capping: each scaled score s becomes
+                           logit_cap * tanh(s / logit_cap) before the softmax (Gemma 2);
+                           None or 0 = off
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
@@ -233,6 +247,7 @@ def decode_attention(
     if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale == 0.0):
         _fail(f"sm_scale must be finite and non-zero, got {sm_scale}")
     kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
+    cap = _logit_cap(logit_cap)
     lib = dk_lib.load()
     split = resolve_split(split_kv)
     batch, hq, d = q.shape
@@ -257,7 +272,7 @@ def decode_attention(
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
     opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
-                          sm_scale or 0.0, kv_dtype, k_sc, v_sc)
+                          sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap)
     shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
              _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts))
     tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
@@ -276,7 +291,8 @@ def decode_attention(
 
 def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv: int,
                     *, qk_path: int = 0, waves_per_group: int = 0,
-                    k_scale: Optional[float] = None, v_scale: Optional[float] = None):
+                    k_scale: Optional[float] = None, v_scale: Optional[float] = None,
+                    logit_cap: Optional[float] = None):
     """Pass 1 only. Returns (partial_O (B,Hq,S,D), partial_m (B,Hq,S), partial_l (B,Hq,S)),
     fp32, with the semantics of the reference partition kernel
     (src/cuda_/attention_ext.cu:207-349): m is the split's max of q.k*scale (-1e9 when the
@@ -293,7 +309,7 @@ def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_k
     ws = torch.empty(total, dtype=torch.uint8, device=q.device)
     strides = _strides(q, kv_data, None)
     opts = dk_lib.options(qk_path, waves_per_group, kv_dtype=kv_dtype, k_scale=k_sc,
-                          v_scale=v_sc)
+                          v_scale=v_sc, logit_cap=_logit_cap(logit_cap))
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.dk_decode_partials(

@@ -168,8 +168,12 @@ int run(Problem p, bool do_merge, void* stream) {
   a.direct = direct ? 1 : 0;
   const bool kv8 = pl.kv8;
   const float k_scale = kv8 && p.opt.k_scale != 0.f ? p.opt.k_scale : 1.f;
-  a.kscale = kLog2e * k_scale *
-             (p.opt.sm_scale != 0.f ? p.opt.sm_scale : 1.f / sqrtf((float)p.head_dim));
+  const float score_scale =
+      k_scale * (p.opt.sm_scale != 0.f ? p.opt.sm_scale : 1.f / sqrtf((float)p.head_dim));
+  a.kscale = kLog2e * score_scale;
+  // soft-capped scores: log2(e) * cap * tanh(q.k * score_scale / cap)
+  a.cap_in = p.opt.logit_cap > 0.f ? score_scale / p.opt.logit_cap : 0.f;
+  a.cap_out = p.opt.logit_cap > 0.f ? kLog2e * p.opt.logit_cap : 0.f;
   a.vscale = kv8 && p.opt.v_scale != 0.f ? p.opt.v_scale : 1.f;
   // every launch that can store partials has them (or the library is inconsistent)
   if ((pl.balanced || !direct) && (!a.part_o || !a.part_m || !a.part_l))

@@ -183,6 +183,8 @@ int validate(const Problem& p) {
     return set_error(DK_EINVAL, "options.k_scale and v_scale must be finite and >= 0");
   if (o.kv_dtype == DK_KV_SAME && (o.k_scale != 0.f || o.v_scale != 0.f))
     return set_error(DK_EINVAL, "options.k_scale and v_scale apply to an fp8 cache only");
+  if (!std::isfinite(o.logit_cap) || o.logit_cap < 0)
+    return set_error(DK_EINVAL, "options.logit_cap must be finite and >= 0 (0 = off)");
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything

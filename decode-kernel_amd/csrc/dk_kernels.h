@@ -95,6 +95,8 @@ struct Pass1Args {
   int32_t direct;                     // explicit split 1 / balanced: may write the
                                       // normalised output (0: partials only)
   float kscale;                       // log2(e) * softmax scale (* K dequant scale)
+  float cap_in, cap_out;              // logit soft-cap: x = cap_out * tanh(q.k * cap_in)
+                                      // (cap_out == 0: off, x = q.k * kscale)
   float vscale;                       // V dequant scale (1 unless the cache is fp8)
 };
 
@@ -312,6 +314,13 @@ __device__ __forceinline__ int seq_begin(const Pass1Args& a, int b) {
   return min(max(ld_const(a.indptr, b), 0), a.num_indices);
 }
 
+// tanh(y) = 1 - 2 / (e^(2y) + 1): saturates to +-1 for large |y| (e^(2y) overflowing to
+// infinity or underflowing to 0); absolute error a few float ulps
+__device__ __forceinline__ float tanh_approx(float y) {
+  const float e = __builtin_amdgcn_exp2f(y * (2.f * kLog2e));
+  return 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+}
+
 // ---------------------------------------------------------------- per-wavefront decoder
 // T: element type of q and out (and of the cache unless KV8); KV8: the cache holds fp8
 // (E4M3) values, widened to T in registers after the loads.
@@ -341,7 +350,7 @@ struct Wave {
   int hv;                 // valid q heads of this chunk (<= G); heads hv.. are masked
   u32 koff, voff, tok_s, extent;
   int64_t kv_v;
-  float kscale, vscale;
+  float kscale, vscale, cap_in, cap_out;
   u32 qw[MFMA ? NS : 1][MFMA ? KW : 1];      // MFMA: Q^T column s*GQ + c%GQ, the dims of
                                              // the K operand of MFMA i (see q_dim0)
   u32 qv[MFMA ? 1 : G][MFMA ? 1 : VWT];      // VALU: head h, dims c*DPL..
@@ -360,6 +369,8 @@ struct Wave {
     extent = a.page_extent;
     kv_v = a.kv_v;
     kscale = a.kscale;
+    cap_in = a.cap_in;
+    cap_out = a.cap_out;
     vscale = a.vscale;
   }
 
@@ -430,6 +441,7 @@ struct Wave {
 
   // One loaded page: fp8 buffers are widened to T pairs first (word u of a token's fp8
   // dims 4u..4u+3 becomes words 2u, 2u+1), then compute_page.
+  template <bool CAP>
   __device__ __forceinline__ void consume(const u32 (&kb)[KB], u32 (&vb)[VB], int valid) {
     if constexpr (KV8) {
       u32 kw[KW], vw[VW];
@@ -440,9 +452,9 @@ struct Wave {
         vw[2 * i] = T::template from_fp8<false>(vb[i]);
         vw[2 * i + 1] = T::template from_fp8<true>(vb[i]);
       }
-      compute_page(kw, vw, valid);
+      compute_page<CAP>(kw, vw, valid);
     } else {
-      compute_page(kb, vb, valid);
+      compute_page<CAP>(kb, vb, valid);
     }
   }
 
@@ -473,6 +485,9 @@ struct Wave {
   }
 
   // One page: scores, online softmax, P.V. valid < 16 masks tokens >= valid.
+  // CAP: logit soft-capping on (a separate instantiation, so uncapped calls carry no
+  // trace of it)
+  template <bool CAP>
   __device__ __forceinline__ void compute_page(const u32 (&kb)[KW], u32 (&vb)[VW], int valid) {
     float sc[NS][4];
     if constexpr (MFMA) {
@@ -520,11 +535,21 @@ struct Wave {
     }
     // online softmax (log2 domain)
     float x[NS][4], mx[NS];
+#pragma unroll
+    for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[ss][r] = sc[ss][r] * kscale;
+    if constexpr (CAP) {
+      // soft-capped scores (masked tokens stay -inf)
+#pragma unroll
+      for (int ss = 0; ss < NS; ++ss)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          x[ss][r] = sc[ss][r] > kNegInf ? cap_out * tanh_approx(sc[ss][r] * cap_in) : kNegInf;
+    }
     bool need = false;
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[ss][r] = sc[ss][r] * kscale;
       mx[ss] = fmaxf(fmaxf(x[ss][0], x[ss][1]), fmaxf(x[ss][2], x[ss][3]));
       mtrue[ss] = fmaxf(mtrue[ss], mx[ss]);
       need |= mx[ss] > mref[ss] + kSlack;
@@ -781,7 +806,7 @@ constexpr int min_waves_per_simd() {
 // page about to be used; the last pages are peeled off after it. Buffer 0 must already
 // hold (or be loading) page 0; page(i) is the base address of page i, valid(i) its valid
 // token count.
-template <int DEPTH, class W, class PageFn, class ValidFn>
+template <int DEPTH, bool CAP, class W, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[W::VB],
                                              int n, PageFn page, ValidFn valid) {
   u32 kb[W::KB], vb[W::VB];
@@ -789,16 +814,16 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[
     int k = 0;
     for (; k + 2 < n; k += 2) {
       wv.load_page(kb, vb, page(k + 1));
-      wv.consume(ka, va, valid(k));
+      wv.template consume<CAP>(ka, va, valid(k));
       wv.load_page(ka, va, page(k + 2));
-      wv.consume(kb, vb, valid(k + 1));
+      wv.template consume<CAP>(kb, vb, valid(k + 1));
     }
     if (k + 1 < n) {
       wv.load_page(kb, vb, page(k + 1));
-      wv.consume(ka, va, valid(k));
-      wv.consume(kb, vb, valid(k + 1));
+      wv.template consume<CAP>(ka, va, valid(k));
+      wv.template consume<CAP>(kb, vb, valid(k + 1));
     } else if (k < n) {
-      wv.consume(ka, va, valid(k));
+      wv.template consume<CAP>(ka, va, valid(k));
     }
   } else {
     u32 kc[W::KB], vc[W::VB];
@@ -806,19 +831,19 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[
     int k = 0;
     for (; k + 4 < n; k += 3) {
       wv.load_page(kc, vc, page(k + 2));
-      wv.consume(ka, va, valid(k));
+      wv.template consume<CAP>(ka, va, valid(k));
       wv.load_page(ka, va, page(k + 3));
-      wv.consume(kb, vb, valid(k + 1));
+      wv.template consume<CAP>(kb, vb, valid(k + 1));
       wv.load_page(kb, vb, page(k + 4));
-      wv.consume(kc, vc, valid(k + 2));
+      wv.template consume<CAP>(kc, vc, valid(k + 2));
     }
     const int r = n - k;   // 1..4 pages left; buffers a, b hold pages k, k+1
     if (r >= 3) wv.load_page(kc, vc, page(k + 2));
-    if (r >= 1) wv.consume(ka, va, valid(k));
+    if (r >= 1) wv.template consume<CAP>(ka, va, valid(k));
     if (r >= 4) wv.load_page(ka, va, page(k + 3));
-    if (r >= 2) wv.consume(kb, vb, valid(k + 1));
-    if (r >= 3) wv.consume(kc, vc, valid(k + 2));
-    if (r >= 4) wv.consume(ka, va, valid(k + 3));
+    if (r >= 2) wv.template consume<CAP>(kb, vb, valid(k + 1));
+    if (r >= 3) wv.template consume<CAP>(kc, vc, valid(k + 2));
+    if (r >= 4) wv.template consume<CAP>(ka, va, valid(k + 3));
   }
 }
 
@@ -826,7 +851,7 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[
 // step issues one page's loads and computes another, so the wait counters see the same
 // pending loads on every path; steps past the last page load with a zero-extent
 // descriptor (no memory access) and skip the compute.
-template <int DEPTH, class W, class PageFn, class ValidFn>
+template <int DEPTH, bool CAP, class W, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_ring(W& wv, int n, PageFn page, ValidFn valid) {
   constexpr int NB = DEPTH + 1;
   u32 kb[NB][W::KB], vb[NB][W::VB];
@@ -837,7 +862,7 @@ __device__ __forceinline__ void stream_ring(W& wv, int n, PageFn page, ValidFn v
     for (int j = 0; j < NB; ++j) {
       const int ld = k + j + DEPTH;
       wv.load_page(kb[(j + DEPTH) % NB], vb[(j + DEPTH) % NB], page(min(ld, n - 1)), ld < n);
-      if (k + j < n) wv.consume(kb[j], vb[j], valid(k + j));
+      if (k + j < n) wv.template consume<CAP>(kb[j], vb[j], valid(k + j));
     }
   }
 }
@@ -924,7 +949,7 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
 }
 
 // Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages.
-template <int D, bool KV8, class WV, class PageFn, class ValidFn>
+template <int D, bool KV8, bool CAP, class WV, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n, PageFn page,
                                                    ValidFn valid) {
   const int nk = n > w ? (n - w + NW - 1) / NW : 0;
@@ -935,9 +960,9 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
     if constexpr (depth <= 2) {
       u32 ka[WV::KB], va[WV::VB];
       wv.load_page(ka, va, pk(0));
-      stream_pages<depth>(wv, ka, va, nk, pk, vk);
+      stream_pages<depth, CAP>(wv, ka, va, nk, pk, vk);
     } else {
-      stream_ring<depth>(wv, nk, pk, vk);
+      stream_ring<depth, CAP>(wv, nk, pk, vk);
     }
   }
 }
@@ -985,7 +1010,10 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
     return kvh_base + (int64_t)pid * a.kv_p;
   };
   auto valid = [&](int i) -> int { return p0 + i == npages - 1 ? valid_last : kPage; };
-  stream_interleaved<D, KV8>(wv, NW, w, n, page, valid);
+  if (a.cap_out != 0.f)
+    stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
+  else
+    stream_interleaved<D, KV8, false>(wv, NW, w, n, page, valid);
   wv.reduce_rows();
   combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
@@ -1054,7 +1082,10 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
       return kvh_base + (int64_t)pid * a.kv_p;
     };
     auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
-    stream_interleaved<D, KV8>(wv, NW, w, n, page, valid);
+    if (a.cap_out != 0.f)
+      stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
+    else
+      stream_interleaved<D, KV8, false>(wv, NW, w, n, page, valid);
     wv.reduce_rows();
 
     const int start = seq0 - base;

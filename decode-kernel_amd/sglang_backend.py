@@ -102,8 +102,6 @@ class SplitKVHipBackend(_import_sglang_base()):
 
     def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
         """One layer's decode attention; returns (batch, q_heads * head_dim)."""
-        if getattr(layer, "logit_cap", 0) not in (0, 0.0, None):
-            raise NotImplementedError("logit soft-capping is not supported by this kernel")
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
             self._save(pool, layer, forward_batch.out_cache_loc, k, v)
@@ -119,7 +117,8 @@ class SplitKVHipBackend(_import_sglang_base()):
         out = decode_attention(
             qv, (kc, vc), md.kv_indptr, md.kv_indices, md.kv_last_page_len,
             split_kv=self.split_kv, workspace=self._workspace_for(qv, kc.shape[2]),
-            max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d), **scales)
+            max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d),
+            logit_cap=_logit_cap(layer), **scales)
         return out.view(-1, hq * d)
 
     @staticmethod
@@ -175,8 +174,14 @@ class SplitKVHipBackend(_import_sglang_base()):
             # new token i sits at position n_all - n_new + i and sees positions <= it
             pos_q = torch.arange(n_all - n_new, n_all, device=q.device)[:, None]
             mask = torch.arange(n_all, device=q.device)[None, :] <= pos_q
-            o = torch.nn.functional.scaled_dot_product_attention(
-                qq, kk, vv, attn_mask=mask, scale=_scale(layer, d) or 1.0 / math.sqrt(d))
+            scale = _scale(layer, d) or 1.0 / math.sqrt(d)
+            cap = _logit_cap(layer)
+            if cap:      # soft-capped scores: SDPA has no such mode, so attend explicitly
+                s_ = torch.tanh(torch.matmul(qq, kk.transpose(1, 2)) * (scale / cap)) * cap
+                o = torch.matmul(torch.softmax(s_.masked_fill(~mask, float("-inf")), -1), vv)
+            else:
+                o = torch.nn.functional.scaled_dot_product_attention(
+                    qq, kk, vv, attn_mask=mask, scale=scale)
             out[start:start + n_new] = o.transpose(0, 1).to(out.dtype)
             start += n_new
         return out.view(-1, hq * d)
@@ -225,6 +230,12 @@ class SplitKVHipBackend(_import_sglang_base()):
         if ws is None or ws.numel() < need or ws.device != q.device:
             ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
         return ws
+
+
+def _logit_cap(layer) -> Optional[float]:
+    """RadixAttention.logit_cap (Gemma 2's soft-capping), None when off."""
+    cap = getattr(layer, "logit_cap", None)
+    return float(cap) if cap not in (None, 0, 0.0) else None
 
 
 def _scale(layer, d) -> Optional[float]:

@@ -91,7 +91,10 @@ typedef struct {
   float k_scale;           /* fp8 cache: K = k_scale * stored value (0 = 1); must be 0
                               for a cache of q's type                                     */
   float v_scale;           /* fp8 cache: V = v_scale * stored value (0 = 1); likewise     */
-  int32_t reserved[3];     /* must be 0                                                     */
+  float logit_cap;         /* logit soft-capping (Gemma 2 style): each score s = q.k *
+                              sm_scale (* k_scale) becomes logit_cap * tanh(s / logit_cap)
+                              before the softmax; 0 = off. No counterpart in the reference */
+  int32_t reserved[2];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */

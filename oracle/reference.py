@@ -18,7 +18,8 @@ batches. `literal=True` reproduces the padded form.
 Pinned by tests/test_oracle.py against: the hand-worked example of
 writeup/cuda_primer.md:31-43,505-540; closed forms (ctx=1, constant V, equal K);
 torch.nn.functional.scaled_dot_product_attention(enable_gqa=True) in float64;
-brute-force float64 golden fixtures (tests/golden/).
+brute-force float64 golden fixtures (tests/golden/); the soft-capped form against
+transformers' Gemma 2 eager attention (softcap) in float64.
 
 Inputs are numpy arrays: q (B, Hq, D) and kv_data (N_p, 2, P, Hkv, D) as float16 /
 float32 (bfloat16 callers pass float32 upcasts — exact), and int32 page tables.
@@ -68,46 +69,56 @@ def gather_paged_to_dense(kv_data, kv_indptr, kv_indices, kv_last_page_len):
     return K, V
 
 
-def _softmax_attend(qs: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
-    """qs (Hkv, G, D) already scaled; k, v (S, Hkv, D) -> (Hkv, G, D), fp32 throughout."""
+def _softmax_attend(qs: np.ndarray, k: np.ndarray, v: np.ndarray,
+                    logit_cap=None) -> np.ndarray:
+    """qs (Hkv, G, D) already scaled; k, v (S, Hkv, D) -> (Hkv, G, D), fp32 throughout.
+    logit_cap: scores s become cap * tanh(s / cap) before the softmax (an extension)."""
     if k.shape[0] == 0:
         return np.zeros(qs.shape, np.float32)
     kt = np.ascontiguousarray(k.transpose(1, 2, 0))            # (Hkv, D, S)
     scores = np.matmul(qs, kt)                                 # (Hkv, G, S)
+    if logit_cap:
+        cap = np.float32(logit_cap)
+        scores = (cap * np.tanh(scores / cap)).astype(np.float32)
     scores = scores - scores.max(axis=-1, keepdims=True)
     w = np.exp(scores, dtype=np.float32)
     w /= w.sum(axis=-1, keepdims=True, dtype=np.float32)
     return np.matmul(w, np.ascontiguousarray(v.transpose(1, 0, 2)))  # (Hkv, G, D)
 
 
-def reference_attention(Q, K, V, seq_lens=None) -> np.ndarray:
+def reference_attention(Q, K, V, seq_lens=None, sm_scale=None, logit_cap=None) -> np.ndarray:
     """fp32 decode attention with GQA (src/reference.py:61-96).
 
     Q (B, Hq, D); K, V (B, S, Hkv, D). With `seq_lens`, sequence b attends over its first
     seq_lens[b] positions only (a length of 0 gives zeros); without, over all S positions
-    (the reference's unmasked form). Returns (B, Hq, D) float32.
+    (the reference's unmasked form). Returns (B, Hq, D) float32. sm_scale and logit_cap
+    are the extensions of reference_attention_paged.
     """
     Q = np.asarray(Q, dtype=np.float32)
     B, Hq, D = Q.shape
     Hkv = K.shape[2]
     G = Hq // Hkv
-    scale = np.float32(D ** -0.5)
+    scale = np.float32(D ** -0.5 if sm_scale is None else sm_scale)
     out = np.zeros((B, Hq, D), np.float32)
     for b in range(B):
         n = K.shape[1] if seq_lens is None else int(seq_lens[b])
         qs = (Q[b] * scale).reshape(Hkv, G, D)                 # q head h -> kv head h // G
         out[b] = _softmax_attend(qs, np.asarray(K[b, :n], np.float32),
-                                 np.asarray(V[b, :n], np.float32)).reshape(Hq, D)
+                                 np.asarray(V[b, :n], np.float32), logit_cap).reshape(Hq, D)
     return out
 
 
 def reference_attention_paged(Q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
-                              literal: bool = False, batch_subset=None) -> np.ndarray:
+                              literal: bool = False, batch_subset=None, sm_scale=None,
+                              logit_cap=None) -> np.ndarray:
     """Paged decode attention (src/reference.py:99-108), per-sequence masked by default.
 
     literal=True gathers to the zero-padded dense form and attends over all positions,
     exactly as the reference does. batch_subset restricts the work to some sequences
     (the other rows of the result are NaN); it is only meaningful with literal=False.
+    sm_scale (default 1/sqrt(D), the reference's) and logit_cap (scores s -> cap *
+    tanh(s / cap) before the softmax, Gemma 2 style) are extensions beyond the reference,
+    for the masked form only.
     """
     Q = np.asarray(Q, dtype=np.float32)
     if literal:
@@ -117,10 +128,10 @@ def reference_attention_paged(Q, kv_data, kv_indptr, kv_indices, kv_last_page_le
     kv = np.asarray(kv_data)
     Hkv = kv.shape[3]
     G = Hq // Hkv
-    scale = np.float32(D ** -0.5)
+    scale = np.float32(D ** -0.5 if sm_scale is None else sm_scale)
     out = np.full((B, Hq, D), np.nan, np.float32)
     for b in (range(B) if batch_subset is None else batch_subset):
         k, v = _sequence_kv(kv, kv_indptr, kv_indices, kv_last_page_len, b)
         qs = (Q[b] * scale).reshape(Hkv, G, D)
-        out[b] = _softmax_attend(qs, k, v).reshape(Hq, D)
+        out[b] = _softmax_attend(qs, k, v, logit_cap).reshape(Hq, D)
     return out

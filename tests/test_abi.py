@@ -100,6 +100,8 @@ def _call(lib, **kw):
     (dict(opts=dk_lib.options(max_pages_per_seq=-1)), dk_lib.DK_EINVAL, "max_pages_per_seq"),
     (dict(opts=dk_lib.options(schedule=3)), dk_lib.DK_EINVAL, "schedule"),
     (dict(opts=dk_lib.options(kv_dtype=1)), dk_lib.DK_EINVAL, "kv_dtype"),
+    (dict(opts=dk_lib.options(logit_cap=-1.0)), dk_lib.DK_EINVAL, "logit_cap"),
+    (dict(opts=dk_lib.options(logit_cap=float("nan"))), dk_lib.DK_EINVAL, "logit_cap"),
     (dict(opts=dk_lib.options(k_scale=2.0)), dk_lib.DK_EINVAL, "fp8 cache only"),
     (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, v_scale=-1.0)),
      dk_lib.DK_EINVAL, "v_scale"),
@@ -222,8 +224,8 @@ def test_plan_hint_reads_host_indptr_only():
 
 def test_options_struct_matches_header():
     # dk_options: qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq
-    # (int32), sm_scale (float), kv_dtype (int32), k_scale, v_scale (float), reserved[3]
-    # (int32): 48 bytes
+    # (int32), sm_scale (float), kv_dtype (int32), k_scale, v_scale, logit_cap (float),
+    # reserved[2] (int32): 48 bytes
     assert ctypes.sizeof(dk_lib.DkOptions) == 48
     fields = [(f[0], f[1]) for f in dk_lib.DkOptions._fields_]
     hdr = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)

@@ -429,6 +429,35 @@ def test_hnd_cache_as_a_strided_view(dtype):
         _check(out, want, label=f"HND S={split} path={path}")
 
 
+# logit soft-capping (Gemma 2: cap 50 on the scaled scores; smaller caps make it bite on
+# these inputs) with the model's own softmax scale
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d,hq,hkv,cap,sm", [(256, 16, 8, 1.5, 256 ** -0.5),
+                                             (128, 32, 16, 2.0, 144 ** -0.5),
+                                             (128, 32, 8, 50.0, 0.3), (64, 40, 4, 1.0, None)])
+def test_logit_softcap(dtype, d, hq, hkv, cap, sm):
+    lens = [1, 300, 17, 129]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        4, lens, hq, hkv, d, dtype=dtype, device=DEV, page_table="permuted", pool_pages=60,
+        seed=d + hq + 1)
+    q = (q.float() * 2).to(dtype)                           # scores large enough to cap
+    args = (to_np(q), to_np(kv), to_np(indptr), to_np(ids), to_np(last))
+    want = ref.reference_attention_paged(*args, sm_scale=sm, logit_cap=cap)
+    plain = ref.reference_attention_paged(*args, sm_scale=sm)
+    if cap < 10:
+        assert np.abs(want - plain).max() > 2e-2            # the cap changes the result
+    hint = attention.plan_hint(indptr.cpu())
+    for split, sched, h in ((1, 0, 0), (3, 0, 0), (0, 1, 0), (0, 0, hint)):
+        for path in (0, 1, 2):
+            label = f"softcap {dtype} d={d} {hq}/{hkv} cap={cap} S={split} sched={sched} path={path}"
+            _announce(label)
+            out = decode_attention(q, kv, indptr, ids, last, split_kv=split, schedule=sched,
+                                   max_pages_per_seq=h, qk_path=path, sm_scale=sm,
+                                   logit_cap=cap)
+            torch.cuda.synchronize()
+            _check(out, want, label=label)
+
+
 def test_balanced_pass1_alone_runs():
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         4, 1000, 32, 8, 128, device=DEV, page_table="permuted", seed=5)

@@ -474,3 +474,47 @@ def test_fp8_append_oracle_matches_float_append_then_torch_quantization():
     untouched[1, 6] = untouched[2, 15] = False
     g, c = got.transpose(0, 2, 1, 3, 4), codes.transpose(0, 2, 1, 3, 4)   # (pages, 16, ...)
     np.testing.assert_array_equal(g[untouched], c[untouched])
+
+
+# ---- logit soft-capping and sm_scale (extensions of the oracle)
+
+@pytest.mark.parametrize("cap,scale", [(None, None), (1.5, None), (50.0, 0.0625), (0.7, 0.2)])
+def test_softcap_matches_transformers_gemma2(cap, scale):
+    from types import SimpleNamespace
+    from transformers.models.gemma2.modeling_gemma2 import eager_attention_forward
+    lens = [1, 16, 37]
+    q, kv, indptr, ids, last = _paged(lens, 8, 2, 64, 16, seed=12, pool=8, dtype=np.float32)
+    q = q * 3                                                  # scores large enough to cap
+    got = ref.reference_attention_paged(q, kv, indptr, ids, last, sm_scale=scale,
+                                        logit_cap=cap)
+    module = SimpleNamespace(head_dim=64, num_key_value_groups=4, training=False)
+    for b, n in enumerate(lens):
+        k, v = ref._sequence_kv(kv, indptr, ids, last, b)
+        qt = torch.from_numpy(q[b].astype(np.float64))[None, :, None, :]      # (1, Hq, 1, D)
+        kt = torch.from_numpy(k.astype(np.float64)).permute(1, 0, 2)[None]   # (1, Hkv, S, D)
+        vt = torch.from_numpy(v.astype(np.float64)).permute(1, 0, 2)[None]
+        want, _ = eager_attention_forward(module, qt, kt, vt, None, scaling=scale,
+                                          softcap=cap)
+        np.testing.assert_allclose(got[b], want[0, 0].numpy(), rtol=2e-5, atol=2e-6)
+
+
+def test_planted_softcap_mistake_is_caught_by_transformers():
+    # capping the unscaled q.k and scaling afterwards (a plausible slip) must fail the pin
+    from types import SimpleNamespace
+    from transformers.models.gemma2.modeling_gemma2 import eager_attention_forward
+    q, kv, indptr, ids, last = _paged([40], 4, 1, 64, 16, seed=2, dtype=np.float32)
+    q = q * 3
+    k, v = ref._sequence_kv(kv, indptr, ids, last, 0)
+    cap, scale = 1.5, 64 ** -0.5
+    raw = q[0].astype(np.float64) @ k[:, 0].T.astype(np.float64)          # (Hq, S)
+    s_wrong = scale * cap * np.tanh(raw / cap)
+    w = np.exp(s_wrong - s_wrong.max(-1, keepdims=True))
+    wrong = (w / w.sum(-1, keepdims=True)) @ v[:, 0].astype(np.float64)
+    module = SimpleNamespace(head_dim=64, num_key_value_groups=4, training=False)
+    qt = torch.from_numpy(q[0].astype(np.float64))[None, :, None, :]
+    kt = torch.from_numpy(k.astype(np.float64)).permute(1, 0, 2)[None]
+    vt = torch.from_numpy(v.astype(np.float64)).permute(1, 0, 2)[None]
+    want, _ = eager_attention_forward(module, qt, kt, vt, None, scaling=scale, softcap=cap)
+    assert np.abs(wrong - want[0, 0].numpy()).max() > 1e-2
+    good = ref.reference_attention_paged(q, kv, indptr, ids, last, logit_cap=cap)[0]
+    np.testing.assert_allclose(good, want[0, 0].numpy(), rtol=2e-5, atol=2e-6)
