@@ -1,8 +1,11 @@
-// bf16 q/out over an bf16 cache, q.k on the VALU; and the bf16 merge kernels. Instantiation of that
-// symbol table (each table is its own translation unit, compiled in parallel).
+// bf16 q/out over an bf16 cache, q.k on the VALU: the pass-1 kernels of one head_dim (DK_HEAD_DIM, set by the build: 64, 128
+// or 256) and their symbol table.
 #include "dk_launch.h"
 
+#ifndef DK_HEAD_DIM
+#error "compile once per head_dim with -DDK_HEAD_DIM=64, 128 or 256"
+#endif
+
 namespace dk {
-template const void* pass1_symbol_16<BF16, false>(int, int, int, bool);
-template const void* merge_symbol<BF16>(int, bool);
+template const void* pass1_sym_g<BF16, DK_HEAD_DIM, false, false>(int, int, bool);
 }  // namespace dk

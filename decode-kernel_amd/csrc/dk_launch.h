@@ -1,6 +1,6 @@
 // dk_launch.h — host-side selection and launch of the decode kernels for one element type.
-// dk_{f16,bf16}[_kv8][_mfma].hip instantiate the symbol tables (one translation unit per
-// element type, cache type and q.k path, compiled in parallel); dk_api.hip calls them.
+// dk_{f16,bf16}[_kv8][_mfma].hip instantiate the per-head_dim symbol tables (see the end
+// of this file); dk_api.hip dispatches to them.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,8 +18,7 @@ struct Pass1Launch {
 };
 
 // Kernel symbol for (head_dim, heads, waves, mode) with q.k on the matrix cores (M) or
-// the VALU, over a 16-bit cache and over an fp8 cache; nullptr if not instantiated. Each
-// (element type, cache type, M) table is instantiated in its own translation unit.
+// the VALU, over a 16-bit cache and over an fp8 cache; nullptr if not instantiated.
 template <class T, bool M>
 const void* pass1_symbol_16(int d, int heads, int waves, bool balanced);
 template <class T, bool M>
@@ -123,15 +122,25 @@ const void* merge_symbol(int d, bool balanced) {
   }
 }
 
-// Explicit instantiation declarations (definitions in dk_{f16,bf16}[_kv8][_mfma].hip).
-#define DK_DECLARE_TABLES(T)                                                          \
-  extern template const void* pass1_symbol_16<T, false>(int, int, int, bool);        \
-  extern template const void* pass1_symbol_16<T, true>(int, int, int, bool);         \
-  extern template const void* pass1_symbol_kv8<T, false>(int, int, int, bool);       \
-  extern template const void* pass1_symbol_kv8<T, true>(int, int, int, bool);        \
-  extern template const void* merge_symbol<T>(int, bool);
+// The kernels of one (element type, cache type, q.k path, head_dim) are instantiated by
+// one translation unit: dk_{f16,bf16}[_kv8][_mfma].hip compiled once per head_dim
+// (-DDK_HEAD_DIM=64 / 128 / 256), so the 24 units compile in parallel. Everything else
+// (the dispatch above, the merge kernels) is instantiated where it is used (dk_api.hip).
+#define DK_DECLARE_TABLE(T, D, M, KV8) \
+  extern template const void* pass1_sym_g<T, D, M, KV8>(int, int, bool);
+#define DK_DECLARE_TABLES_D(T, D)      \
+  DK_DECLARE_TABLE(T, D, false, false) \
+  DK_DECLARE_TABLE(T, D, true, false)  \
+  DK_DECLARE_TABLE(T, D, false, true)  \
+  DK_DECLARE_TABLE(T, D, true, true)
+#define DK_DECLARE_TABLES(T) \
+  DK_DECLARE_TABLES_D(T, 64) \
+  DK_DECLARE_TABLES_D(T, 128) \
+  DK_DECLARE_TABLES_D(T, 256)
 DK_DECLARE_TABLES(F16)
 DK_DECLARE_TABLES(BF16)
 #undef DK_DECLARE_TABLES
+#undef DK_DECLARE_TABLES_D
+#undef DK_DECLARE_TABLE
 
 }  // namespace dk

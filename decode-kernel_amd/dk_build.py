@@ -36,9 +36,12 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-HIP_SOURCES = ("dk_api.hip", "dk_f16.hip", "dk_bf16.hip", "dk_f16_mfma.hip", "dk_bf16_mfma.hip",
-               "dk_f16_kv8.hip", "dk_bf16_kv8.hip", "dk_f16_kv8_mfma.hip",
-               "dk_bf16_kv8_mfma.hip", "dk_paging.hip", "dk_append.hip")
+HIP_SOURCES = ("dk_api.hip", "dk_paging.hip", "dk_append.hip")
+# pass-1 kernel tables: each compiled once per head_dim (-DDK_HEAD_DIM=...)
+KERNEL_SOURCES = ("dk_f16.hip", "dk_bf16.hip", "dk_f16_mfma.hip", "dk_bf16_mfma.hip",
+                  "dk_f16_kv8.hip", "dk_bf16_kv8.hip", "dk_f16_kv8_mfma.hip",
+                  "dk_bf16_kv8_mfma.hip")
+HEAD_DIMS = (64, 128, 256)
 
 
 # Per-kernel resource report of the device compiler (VGPRs, scratch, occupancy).
@@ -68,19 +71,33 @@ def kernel_resources(out: str) -> dict:
     return res
 
 
+def _jobs() -> int:
+    """Parallel compiles: MAX_JOBS if set, else the CPU count (at most 16)."""
+    env = os.environ.get("MAX_JOBS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, min(16, os.cpu_count() or 1))
+
+
 def _run_all(cmds: list[list[str]]) -> str:
-    """Run compile commands in parallel; raise with the output of the first failure.
+    """Run compile commands, _jobs() at a time; raise with the output of the first failure.
     Returns the concatenated raw output (for the resource remarks)."""
-    procs = [(c, subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True))
-             for c in cmds]
+    from concurrent.futures import ThreadPoolExecutor
+
+    def run(c):
+        p = subprocess.run(c, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        return p.returncode, p.stdout
+
+    with ThreadPoolExecutor(max_workers=_jobs()) as pool:
+        results = list(pool.map(run, cmds))
+    procs = [(c, r) for c, r in zip(cmds, results)]
     failed = None
     raw = []
-    for cmd, proc in procs:
-        text = proc.communicate()[0]
+    for cmd, (returncode, text) in procs:
         raw.append(text)
         out = _filter(text)
-        if proc.returncode != 0 and failed is None:
-            failed = f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}"
+        if returncode != 0 and failed is None:
+            failed = f"build step failed ({returncode}): {' '.join(cmd)}\n{out}"
         elif out.strip():
             print(out, file=sys.stderr)
     if failed:
@@ -106,6 +123,12 @@ def build(verbose: bool = False, defines: tuple = (), out: Path = LIB_PATH,
         objs.append(obj)
         cmds.append([hipcc, *HIP_FLAGS, *dflags, RESOURCE_FLAG, f"-I{INCLUDE}", "-c",
                      str(CSRC / src), "-o", str(obj)])
+    for src in KERNEL_SOURCES:
+        for d in HEAD_DIMS:
+            obj = build_dir / f"{Path(src).stem}.d{d}.o"
+            objs.append(obj)
+            cmds.append([hipcc, *HIP_FLAGS, *dflags, f"-DDK_HEAD_DIM={d}", RESOURCE_FLAG,
+                         f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)])
     res = kernel_resources(_run_all(cmds))
     (build_dir / "kernel_resources.txt").write_text("".join(
         f"{k} VGPRs={v.get('VGPRs')} scratch={v.get('ScratchSize')} "
