@@ -44,11 +44,12 @@ int valu_head_cap(int head_dim) { return head_dim >= 256 ? 4 : 8; }
 
 bool qk_on_mfma(int qk_path, int group, int head_dim, bool kv8) {
   // automatic: MFMA once the group exceeds what the VALU path serves best in one chunk --
-  // 8 heads, or 4 at D = 256 and over an fp8 cache (measured at B=32 ctx 8192, one pass:
-  // fp8 40/8 and 64/8 heads 156 us VALU vs 116 MFMA; fp16 64/8 171 vs 185 and at D=64
-  // 103 vs 115, so 16-bit caches keep the VALU path up to 8 heads)
+  // 8 heads, or 4 at D = 256 and over an fp8 cache -- and for fp8 at D = 256 (measured at
+  // B=32 ctx 8192: fp8 40/8 and 64/8 heads 156 us VALU vs 116 MFMA; fp8 D=256 16/4
+  // 131 vs 103; fp16 64/8 171 vs 185, at D=64 103 vs 115 and at D=256 16/4 188 vs 196,
+  // so 16-bit caches keep the VALU path up to 8 heads)
   const int cap = kv8 ? 4 : valu_head_cap(head_dim);
-  return qk_path == 1 || (qk_path == 0 && group > cap);
+  return qk_path == 1 || (qk_path == 0 && (group > cap || (kv8 && head_dim >= 256)));
 }
 
 HeadChunks head_chunks(int group, int head_dim, bool mfma) {

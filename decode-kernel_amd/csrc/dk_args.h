@@ -57,7 +57,7 @@ struct HeadChunks {
 };
 HeadChunks head_chunks(int group, int head_dim, bool mfma);
 // q.k path of a call: qk_path 1 / 2 force MFMA / VALU; 0 takes the VALU path unless the
-// group exceeds 8 heads (4 at D = 256 or over an fp8 cache)
+// group exceeds 8 heads (4 at D = 256 or over an fp8 cache) or the cache is fp8 at D = 256
 bool qk_on_mfma(int qk_path, int group, int head_dim, bool kv8);
 
 struct Plan {
