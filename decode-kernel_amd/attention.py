@@ -148,6 +148,15 @@ def _logit_cap(logit_cap) -> float:
     return cap
 
 
+def _window(window) -> int:
+    """window as dk_options takes it: 0 for all tokens (None or 0), else >= 1."""
+    if window is None:
+        return 0
+    if isinstance(window, bool) or not isinstance(window, int) or window < 0:
+        _fail(f"window must be an int >= 0 (0 = all tokens), got {window!r}")
+    return window
+
+
 def _strides(q, kv_data, out) -> dk_lib.DkStrides:
     s = dk_lib.DkStrides()
     s.q_b, s.q_h = q.stride(0), q.stride(1)
@@ -207,6 +216,7 @@ def decode_attention(
     k_scale: Optional[float] = None,
     v_scale: Optional[float] = None,
     logit_cap: Optional[float] = None,
+    window: Optional[int] = None,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
@@ -239,6 +249,9 @@ def decode_attention(
         logit_cap        : logit soft-capping: each scaled score s becomes
                            logit_cap * tanh(s / logit_cap) before the softmax (Gemma 2);
                            None or 0 = off
+        window           : sliding window: attend to the last `window` tokens of each
+                           sequence (the new one and window - 1 before it; Mistral,
+                           Gemma); None or 0 = all tokens
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
@@ -248,6 +261,7 @@ def decode_attention(
         _fail(f"sm_scale must be finite and non-zero, got {sm_scale}")
     kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
     cap = _logit_cap(logit_cap)
+    win = _window(window)
     lib = dk_lib.load()
     split = resolve_split(split_kv)
     batch, hq, d = q.shape
@@ -272,7 +286,7 @@ def decode_attention(
     ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
     strides = _strides(q, kv_data, out)
     opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
-                          sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap)
+                          sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap, win)
     shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
              _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts))
     tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
@@ -292,7 +306,7 @@ def decode_attention(
 def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv: int,
                     *, qk_path: int = 0, waves_per_group: int = 0,
                     k_scale: Optional[float] = None, v_scale: Optional[float] = None,
-                    logit_cap: Optional[float] = None):
+                    logit_cap: Optional[float] = None, window: Optional[int] = None):
     """Pass 1 only. Returns (partial_O (B,Hq,S,D), partial_m (B,Hq,S), partial_l (B,Hq,S)),
     fp32, with the semantics of the reference partition kernel
     (src/cuda_/attention_ext.cu:207-349): m is the split's max of q.k*scale (-1e9 when the
@@ -309,7 +323,8 @@ def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_k
     ws = torch.empty(total, dtype=torch.uint8, device=q.device)
     strides = _strides(q, kv_data, None)
     opts = dk_lib.options(qk_path, waves_per_group, kv_dtype=kv_dtype, k_scale=k_sc,
-                          v_scale=v_sc, logit_cap=_logit_cap(logit_cap))
+                          v_scale=v_sc, logit_cap=_logit_cap(logit_cap),
+                          window=_window(window))
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.dk_decode_partials(

@@ -106,6 +106,31 @@ int run(Problem p, bool do_merge, void* stream) {
   if (rc != DK_OK || p.batch == 0) return rc;
   Plan pl = make_plan(p);
   int waves_per_pair = 0;   // balanced: workgroups per head chunk
+  if (pl.balanced && p.opt.window > 0) {
+    // a sliding window bounds every sequence's pages: explicit splits of the window's
+    // pages, as many as fill the device and fit the workspace
+    if (!p.need_out)
+      return set_error(DK_EUNSUPPORTED, "pass 1 alone with a sliding window needs an explicit "
+                                        "split_kv");
+    const int dev = current_device(-1);
+    const int cus = cu_count(dev);
+    if (cus <= 0) return hip_fail(hipErrorNoDevice, "compute-unit count");
+    Problem q = p;
+    q.split = 1;
+    const Plan p1 = make_plan(q);
+    const int64_t avg = p.batch > 0 ? p.num_indices / p.batch : 0;
+    const int64_t win_pages = p.opt.window / kPageSize + 2;
+    int s = choose_split((int64_t)p.batch * p1.pairs_per_seq,
+                         (int64_t)cus * resident_groups(p.dtype, p1, p.head_dim),
+                         std::min(avg, win_pages), p1.waves);
+    for (; s > 1; --s) {
+      size_t o, m, l, total;
+      partials_layout_rows(split_rows(p.batch, p.hq, s), p.head_dim, &o, &m, &l, &total);
+      if (total <= p.workspace_bytes) break;
+    }
+    p.split = s;
+    pl = make_plan(p);
+  }
   if (pl.balanced) {
     const int dev = current_device(-1);
     const int cus = cu_count(dev);
@@ -160,6 +185,7 @@ int run(Problem p, bool do_merge, void* stream) {
   a.group = pl.group;
   a.chunks = pl.chunks;
   a.per = pl.per;
+  a.window = p.opt.window;
   a.split = std::max(p.split, 1);
   a.num_indices = (int32_t)p.num_indices;
   a.num_pages = (uint32_t)std::min<int64_t>(p.num_pages, (int64_t)1 << 31);

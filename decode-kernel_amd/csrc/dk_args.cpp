@@ -184,6 +184,9 @@ int validate(const Problem& p) {
     return set_error(DK_EINVAL, "options.k_scale and v_scale must be finite and >= 0");
   if (o.kv_dtype == DK_KV_SAME && (o.k_scale != 0.f || o.v_scale != 0.f))
     return set_error(DK_EINVAL, "options.k_scale and v_scale apply to an fp8 cache only");
+  if (o.window < 0)
+    return set_error(DK_EINVAL, "options.window must be >= 0 (0 = the whole sequence); got %d",
+                     o.window);
   if (!std::isfinite(o.logit_cap) || o.logit_cap < 0)
     return set_error(DK_EINVAL, "options.logit_cap must be finite and >= 0 (0 = off)");
   for (int r : o.reserved)

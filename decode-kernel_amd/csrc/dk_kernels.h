@@ -89,6 +89,8 @@ struct Pass1Args {
   int32_t kv_s, kv_h;                 // bytes
   int32_t batch, hq, hkv, group, chunks, split;
   int32_t per;                        // q heads per chunk (the last chunk may have fewer)
+  int32_t window;                     // > 0: attend to each sequence's last `window` tokens
+                                      // (explicit-split kernel only)
   int32_t num_indices;
   uint32_t num_pages;                 // clamp bound for page ids (min(num_pages, 2^31))
   uint32_t page_extent;               // bytes one kv head's K (or V) rows of a page span (< 2^31)
@@ -521,12 +523,14 @@ struct Wave {
         }
       }
     }
-    // last page of a sequence: tokens >= valid are masked by selection (never by
-    // multiplying), so stale or NaN bytes in the page tail cannot reach the output
-    if (valid < kPage) {
+    // `valid` = hi | lo << 8: tokens [lo, hi) of the page are attended. Others (the tail
+    // of a sequence's last page, or before a sliding window's first token) are masked by
+    // selection (never by multiplying), so stale or NaN bytes cannot reach the output
+    const int hi = valid & 0xff, lo = valid >> 8;
+    if (hi < kPage || lo > 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool dead = 4 * r16 + r >= valid;
+        const bool dead = 4 * r16 + r >= hi || 4 * r16 + r < lo;
 #pragma unroll
         for (int ss = 0; ss < NS; ++ss) sc[ss][r] = dead ? kNegInf : sc[ss][r];
 #pragma unroll
@@ -994,10 +998,18 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
 
   const int seq0 = seq_begin(a, b);
   const int npages = max(seq_begin(a, b + 1), seq0) - seq0;
-  const int pps = (npages + a.split - 1) / a.split;          // attention_ext.cu:249-252
-  const int p0 = min(s * pps, npages);
-  const int n = max(min(p0 + pps, npages) - p0, 0);
   const int valid_last = min(max(ld_const(a.last_len, b), 0), kPage);
+  // sliding window: pages from the one holding the window's first token
+  int first_page = 0, first_tok = 0;
+  if (a.window > 0 && npages > 0) {
+    const int t0 = max((npages - 1) * kPage + valid_last - a.window, 0);
+    first_page = t0 / kPage;
+    first_tok = t0 % kPage;
+  }
+  const int npw = npages - first_page;
+  const int pps = (npw + a.split - 1) / a.split;             // attention_ext.cu:249-252
+  const int p0 = first_page + min(s * pps, npw);
+  const int n = max(min(p0 + pps, npages) - p0, 0);
   const int qh0 = kvh * a.group + hc * a.per;
   wv.hv = min(a.per, a.group - hc * a.per);
 
@@ -1009,7 +1021,10 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
     pid = pid < a.num_pages ? pid : 0u;
     return kvh_base + (int64_t)pid * a.kv_p;
   };
-  auto valid = [&](int i) -> int { return p0 + i == npages - 1 ? valid_last : kPage; };
+  auto valid = [&](int i) -> int {
+    const int pg = p0 + i;
+    return (pg == npages - 1 ? valid_last : kPage) | (pg == first_page ? first_tok << 8 : 0);
+  };
   if (a.cap_out != 0.f)
     stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
   else

@@ -52,7 +52,7 @@ class DkOptions(ctypes.Structure):
                 ("max_pages_per_seq", ctypes.c_int32), ("sm_scale", ctypes.c_float),
                 ("kv_dtype", ctypes.c_int32), ("k_scale", ctypes.c_float),
                 ("v_scale", ctypes.c_float), ("logit_cap", ctypes.c_float),
-                ("reserved", ctypes.c_int32 * 2)]
+                ("window", ctypes.c_int32), ("reserved", ctypes.c_int32 * 1)]
 
 
 _P = ctypes.c_void_p
@@ -175,9 +175,10 @@ SCHEDULE_ONE_PASS = 2
 def options(qk_path: int = 0, waves_per_group: int = 0, waves_per_cu: int = 0,
             schedule: int = SCHEDULE_AUTO, max_pages_per_seq: int = 0,
             sm_scale: float = 0.0, kv_dtype: int = DK_KV_SAME, k_scale: float = 0.0,
-            v_scale: float = 0.0, logit_cap: float = 0.0) -> DkOptions:
+            v_scale: float = 0.0, logit_cap: float = 0.0, window: int = 0) -> DkOptions:
     o = DkOptions()
     o.logit_cap = logit_cap
+    o.window = window
     o.sm_scale = sm_scale
     o.kv_dtype = kv_dtype
     o.k_scale = k_scale

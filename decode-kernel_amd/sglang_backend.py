@@ -118,7 +118,7 @@ class SplitKVHipBackend(_import_sglang_base()):
             qv, (kc, vc), md.kv_indptr, md.kv_indices, md.kv_last_page_len,
             split_kv=self.split_kv, workspace=self._workspace_for(qv, kc.shape[2]),
             max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d),
-            logit_cap=_logit_cap(layer), **scales)
+            logit_cap=_logit_cap(layer), window=_window(layer), **scales)
         return out.view(-1, hq * d)
 
     @staticmethod
@@ -173,7 +173,11 @@ class SplitKVHipBackend(_import_sglang_base()):
             vv = vv.repeat_interleave(g, dim=0)
             # new token i sits at position n_all - n_new + i and sees positions <= it
             pos_q = torch.arange(n_all - n_new, n_all, device=q.device)[:, None]
-            mask = torch.arange(n_all, device=q.device)[None, :] <= pos_q
+            kpos = torch.arange(n_all, device=q.device)[None, :]
+            mask = kpos <= pos_q
+            win = _window(layer)
+            if win:                                   # sliding window: the last `win` keys
+                mask &= kpos > pos_q - win
             scale = _scale(layer, d) or 1.0 / math.sqrt(d)
             cap = _logit_cap(layer)
             if cap:      # soft-capped scores: SDPA has no such mode, so attend explicitly
@@ -230,6 +234,13 @@ class SplitKVHipBackend(_import_sglang_base()):
         if ws is None or ws.numel() < need or ws.device != q.device:
             ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
         return ws
+
+
+def _window(layer) -> Optional[int]:
+    """RadixAttention.sliding_window_size (FlashInfer's window_left: the new token attends
+    to itself and that many before it; -1 or None = no window) as a token count."""
+    w = getattr(layer, "sliding_window_size", None)
+    return int(w) + 1 if w is not None and int(w) >= 0 else None
 
 
 def _logit_cap(layer) -> Optional[float]:

@@ -95,7 +95,11 @@ typedef struct {
   float logit_cap;         /* logit soft-capping (Gemma 2 style): each score s = q.k *
                               sm_scale (* k_scale) becomes logit_cap * tanh(s / logit_cap)
                               before the softmax; 0 = off. No counterpart in the reference */
-  int32_t reserved[2];     /* must be 0                                                     */
+  int32_t window;          /* sliding window: attend to the last `window` tokens of each
+                              sequence (the new token and window - 1 before it); 0 = the
+                              whole sequence. split_kv 0 then picks explicit splits of the
+                              window's pages. No counterpart in the reference             */
+  int32_t reserved[1];     /* must be 0                                                     */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */

@@ -110,15 +110,16 @@ def reference_attention(Q, K, V, seq_lens=None, sm_scale=None, logit_cap=None) -
 
 def reference_attention_paged(Q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
                               literal: bool = False, batch_subset=None, sm_scale=None,
-                              logit_cap=None) -> np.ndarray:
+                              logit_cap=None, window=None) -> np.ndarray:
     """Paged decode attention (src/reference.py:99-108), per-sequence masked by default.
 
     literal=True gathers to the zero-padded dense form and attends over all positions,
     exactly as the reference does. batch_subset restricts the work to some sequences
     (the other rows of the result are NaN); it is only meaningful with literal=False.
-    sm_scale (default 1/sqrt(D), the reference's) and logit_cap (scores s -> cap *
-    tanh(s / cap) before the softmax, Gemma 2 style) are extensions beyond the reference,
-    for the masked form only.
+    sm_scale (default 1/sqrt(D), the reference's), logit_cap (scores s -> cap *
+    tanh(s / cap) before the softmax, Gemma 2 style) and window (attend to each
+    sequence's last `window` tokens only) are extensions beyond the reference, for the
+    masked form only.
     """
     Q = np.asarray(Q, dtype=np.float32)
     if literal:
@@ -132,6 +133,8 @@ def reference_attention_paged(Q, kv_data, kv_indptr, kv_indices, kv_last_page_le
     out = np.full((B, Hq, D), np.nan, np.float32)
     for b in (range(B) if batch_subset is None else batch_subset):
         k, v = _sequence_kv(kv, kv_indptr, kv_indices, kv_last_page_len, b)
+        if window:
+            k, v = k[-window:], v[-window:]
         qs = (Q[b] * scale).reshape(Hkv, G, D)
         out[b] = _softmax_attend(qs, k, v, logit_cap).reshape(Hq, D)
     return out

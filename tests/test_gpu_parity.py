@@ -458,6 +458,46 @@ def test_logit_softcap(dtype, d, hq, hkv, cap, sm):
             _check(out, want, label=label)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("window", [1, 5, 16, 17, 100, 4096, 100000])
+def test_sliding_window(dtype, window):
+    lens = [1, 16, 17, 300, 2047, 0, 5000]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        7, lens, 32, 8, 128, dtype=dtype, device=DEV, page_table="freelist", pool_pages=600,
+        seed=window % 97)
+    args = (to_np(q), to_np(kv), to_np(indptr), to_np(ids), to_np(last))
+    want = ref.reference_attention_paged(*args, window=window)
+    want[5] = 0                                        # the empty sequence
+    hint = attention.plan_hint(indptr.cpu())
+    for split, path in ((1, 0), (3, 0), (0, 0), (0, 1), (8, 2)):
+        label = f"window={window} {dtype} S={split} path={path}"
+        _announce(label)
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=split, qk_path=path,
+                               max_pages_per_seq=hint, window=window)
+        torch.cuda.synchronize()
+        _check(out, want, label=label)
+
+
+def test_sliding_window_with_softcap_and_partials():
+    lens = [700, 33, 160]
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        3, lens, 16, 8, 256, device=DEV, page_table="permuted", seed=31)
+    q = (q.float() * 2).half()
+    args = (to_np(q), to_np(kv), to_np(indptr), to_np(ids), to_np(last))
+    want = ref.reference_attention_paged(*args, window=129, logit_cap=2.0, sm_scale=0.05)
+    _announce("window + softcap")
+    out = decode_attention(q, kv, indptr, ids, last, split_kv=0, window=129, logit_cap=2.0,
+                           sm_scale=0.05)
+    torch.cuda.synchronize()
+    _check(out, want, label="window + softcap")
+    # pass 1 alone over the window's pages, merged by pass 2, equals the full call
+    po, pm, pl = decode_partials(q, kv, indptr, ids, last, 4, window=129, logit_cap=2.0)
+    merged = merge_partials(po, pm, pl, dtype=q.dtype)
+    full = decode_attention(q, kv, indptr, ids, last, split_kv=4, window=129, logit_cap=2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(merged, full)
+
+
 def test_balanced_pass1_alone_runs():
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         4, 1000, 32, 8, 128, device=DEV, page_table="permuted", seed=5)

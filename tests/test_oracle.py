@@ -518,3 +518,36 @@ def test_planted_softcap_mistake_is_caught_by_transformers():
     assert np.abs(wrong - want[0, 0].numpy()).max() > 1e-2
     good = ref.reference_attention_paged(q, kv, indptr, ids, last, logit_cap=cap)[0]
     np.testing.assert_allclose(good, want[0, 0].numpy(), rtol=2e-5, atol=2e-6)
+
+
+# ---- sliding window (an extension of the oracle)
+
+def _repage_last(kv, indptr, ids, last, b, window, P=16):
+    """The last `window` tokens of sequence b copied into a fresh pool whose pages start at
+    the window's first token (different page boundaries from the source)."""
+    k, v = ref._sequence_kv(kv, indptr, ids, last, b)
+    k, v = k[-window:], v[-window:]
+    n = k.shape[0]
+    pages = -(-n // P)
+    pool = np.zeros((pages, 2, P) + k.shape[1:], np.float32)
+    for t in range(n):
+        pool[t // P, 0, t % P], pool[t // P, 1, t % P] = k[t], v[t]
+    return pool, np.array([0, pages]), np.arange(pages), np.array([n - (pages - 1) * P])
+
+
+@pytest.mark.parametrize("window", [1, 5, 16, 17, 100, 5000])
+def test_window_equals_attention_over_the_last_tokens(window):
+    lens = [1, 16, 17, 300, 1000]
+    q, kv, indptr, ids, last = _paged(lens, 8, 2, 64, 16, seed=21, pool=100, dtype=np.float32)
+    got = ref.reference_attention_paged(q, kv, indptr, ids, last, window=window)
+    for b, n in enumerate(lens):
+        pool, ip, ix, ll = _repage_last(kv, indptr, ids, last, b, window)
+        want = ref.reference_attention_paged(q[b:b + 1], pool, ip, ix, ll)
+        np.testing.assert_allclose(got[b], want[0], rtol=1e-6, atol=1e-6)
+    if window >= max(lens):
+        np.testing.assert_array_equal(got, ref.reference_attention_paged(q, kv, indptr, ids, last))
+    if window == 1:                                  # only the new token: its V exactly
+        for b in range(len(lens)):
+            _, v = ref._sequence_kv(kv, indptr, ids, last, b)
+            np.testing.assert_allclose(got[b].reshape(2, 4, 64), np.repeat(v[-1][:, None], 4, 1),
+                                       rtol=1e-6, atol=1e-7)

@@ -217,16 +217,17 @@ def test_fp8_pool_decode_step_through_the_adapter(dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cap", [None, 2.0])
-def test_softcap_layer_decode_and_extend(cap):
-    # a Gemma-2-like layer (own softmax scale, logit soft-capping) through both entry
-    # points: decode on the HIP kernel, extend on the explicit PyTorch path
+@pytest.mark.parametrize("cap,win", [(None, None), (2.0, None), (None, 9), (2.0, 20)])
+def test_softcap_layer_decode_and_extend(cap, win):
+    # a Gemma-2-like layer (own softmax scale, logit soft-capping, sliding window) through
+    # both entry points: decode on the HIP kernel, extend on the explicit PyTorch path
     lens = [5, 40, 17]
     n_new = [5, 3, 1]
     fb, layers, pool, r2t = make_batch(lens, layers=1, seed=7, decode=False)
     layer = layers[0]
     layer.scaling = 0.11
     layer.logit_cap = cap
+    layer.sliding_window_size = -1 if win is None else win - 1     # SGLang's window_left
     rows = fb.req_pool_indices.tolist()
     g = torch.Generator(device=DEV)
     g.manual_seed(8)
@@ -239,7 +240,7 @@ def test_softcap_layer_decode_and_extend(cap):
     k = torch.randn(T, 8 * 128, generator=g, device=DEV).half()
     v = torch.randn(T, 8 * 128, generator=g, device=DEV).half()
     backend = sglang_backend.SplitKVHipBackend()
-    print(f"[case] softcap layer extend cap={cap}", flush=True)
+    print(f"[case] softcap layer extend cap={cap} window={win}", flush=True)
     out = backend.forward_extend(q, k, v, layer, fb)
     torch.cuda.synchronize()
     kb, vb = to_np(pool.get_key_buffer(0)), to_np(pool.get_value_buffer(0))
@@ -247,7 +248,7 @@ def test_softcap_layer_decode_and_extend(cap):
     for r, n, m in zip(rows, lens, n_new):
         for i in range(m):
             p = n - m + i
-            slots = r2t[r, :p + 1].long().numpy()
+            slots = r2t[r, :p + 1].long().numpy()[-(win or p + 1):]
             want = ref.reference_attention(to_np(q[start + i].view(1, 32, 128)),
                                            kb[slots][None], vb[slots][None],
                                            sm_scale=0.11, logit_cap=cap)
@@ -255,7 +256,7 @@ def test_softcap_layer_decode_and_extend(cap):
             assert mx <= 1e-2, (r, i, mx)
         start += m
     # decode: one more step for every request through the kernel
-    print(f"[case] softcap layer decode cap={cap}", flush=True)
+    print(f"[case] softcap layer decode cap={cap} window={win}", flush=True)
     fb.forward_mode = type(fb.forward_mode)(True)
     backend.init_forward_metadata(fb)
     qd = (torch.randn(len(lens), 32 * 128, generator=g, device=DEV) * 2).half()
@@ -263,6 +264,7 @@ def test_softcap_layer_decode_and_extend(cap):
     torch.cuda.synchronize()
     indptr, indices, last = ptab.build_page_table(r2t.numpy(), rows, lens)
     want = ref.reference_attention_paged(to_np(qd.view(-1, 32, 128)), _pool_as_combined(pool, 0),
-                                         indptr, indices, last, sm_scale=0.11, logit_cap=cap)
+                                         indptr, indices, last, sm_scale=0.11, logit_cap=cap,
+                                         window=win)
     mx, mean = err_stats(o.view(-1, 32, 128), want)
     assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
