@@ -27,7 +27,7 @@ def page_capacity(seq_lens_sum: int, batch: int) -> int:
 
 def build_page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
                      seq_lens: torch.Tensor, capacity: Optional[int] = None,
-                     seq_lens_sum: Optional[int] = None):
+                     seq_lens_sum: Optional[int] = None, out=None):
     """(kv_indptr (B+1,), kv_indices (capacity,), kv_last_page_len (B,)) int32 on the device.
 
     req_to_token     : (rows, max_tokens) int32 cache slot of each request's tokens
@@ -36,6 +36,10 @@ def build_page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
     capacity         : size of kv_indices; default page_capacity(seq_lens_sum, B), with
                        seq_lens_sum (a host integer) required then. Entries past the
                        table's total are left uninitialised.
+    out              : optional persistent (kv_indptr, kv_indices, kv_last_page_len)
+                       buffers to fill in place (at least B + 1, capacity and B entries),
+                       e.g. for tables a captured HIP graph reads; capacity defaults to
+                       the kv_indices buffer's size then
     """
     if req_to_token.dtype != torch.int32 or req_to_token.dim() != 2:
         raise DecodeArgumentError("req_to_token must be a 2-D int32 tensor")
@@ -45,18 +49,29 @@ def build_page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
     batch = int(seq_lens.shape[0])
     if req_pool_indices.shape[0] != batch:
         raise DecodeArgumentError("req_pool_indices and seq_lens must have one entry per request")
-    if capacity is None:
+    if out is not None:
+        kv_indptr, kv_indices, kv_last = out
+        if capacity is None:
+            capacity = kv_indices.numel()
+        if (kv_indptr.numel() < batch + 1 or kv_indices.numel() < capacity or
+                kv_last.numel() < batch or
+                any(t.dtype != torch.int32 or t.device != dev or not t.is_contiguous()
+                    for t in out)):
+            raise DecodeArgumentError("out buffers must be contiguous int32 on the table's "
+                                      "device, with B + 1, capacity and B entries")
+    elif capacity is None:
         if seq_lens_sum is None:
             raise DecodeArgumentError("give capacity or seq_lens_sum (a host integer)")
         capacity = page_capacity(seq_lens_sum, batch)
     rpi = req_pool_indices.to(device=dev, dtype=torch.int32).contiguous()
     lens = seq_lens.to(device=dev, dtype=torch.int32).contiguous()
-    kv_indptr = torch.empty(batch + 1, dtype=torch.int32, device=dev)
-    kv_indices = torch.empty(max(int(capacity), 1), dtype=torch.int32, device=dev)
-    kv_last = torch.empty(batch, dtype=torch.int32, device=dev)
+    if out is None:
+        kv_indptr = torch.empty(batch + 1, dtype=torch.int32, device=dev)
+        kv_indices = torch.empty(max(int(capacity), 1), dtype=torch.int32, device=dev)
+        kv_last = torch.empty(batch, dtype=torch.int32, device=dev)
     if batch == 0:
-        kv_indptr.zero_()
-        return kv_indptr, kv_indices[:0], kv_last
+        kv_indptr[:1].zero_()
+        return kv_indptr[:1], kv_indices[:0], kv_last[:0]
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
         rc = dk_lib.load().dk_build_page_table(
@@ -64,7 +79,7 @@ def build_page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
             batch, PAGE_SIZE, kv_indptr.data_ptr(), kv_indices.data_ptr(), int(capacity),
             kv_last.data_ptr(), stream)
     dk_lib.check(rc, "build_page_table")
-    return kv_indptr, kv_indices[:int(capacity)], kv_last
+    return kv_indptr[:batch + 1], kv_indices[:int(capacity)], kv_last[:batch]
 
 
 def rope_inv_freq(head_dim: int, theta: float = 10000.0, device="cuda") -> torch.Tensor:

@@ -76,6 +76,8 @@ class SplitKVHipBackend(_import_sglang_base()):
         self.forward_metadata: Optional[DecodeMetadata] = None
         self._workspace: Optional[torch.Tensor] = None
         self._scales: dict = {}           # layer_id -> (k_scale, v_scale) of an fp8 pool
+        self._graph_tables = None         # persistent page tables for HIP graph replay
+        self._graph_max_bs = 0
 
     @classmethod
     def name(cls) -> str:
@@ -195,6 +197,51 @@ class SplitKVHipBackend(_import_sglang_base()):
         if forward_batch.forward_mode.is_decode():
             return self.forward_decode(q, k, v, layer, forward_batch, save_kv_cache)
         return self.forward_extend(q, k, v, layer, forward_batch, save_kv_cache)
+
+    # ---------------------------------------------------------------- HIP graphs
+    # SGLang captures decode steps in graphs (its "CUDA graph" runner; HIP graphs here).
+    # The page table then lives in persistent buffers the graph reads, refilled in place
+    # before each replay by one kernel; the captured decode call uses the balanced
+    # schedule (no plan hint), which is valid for any sequence lengths at replay.
+
+    def get_cuda_graph_seq_len_fill_value(self) -> int:
+        return 1
+
+    def init_cuda_graph_state(self, max_bs: int, max_num_tokens: Optional[int] = None,
+                              max_context_len: Optional[int] = None, device=None):
+        """Persistent page-table buffers for batches of up to max_bs requests."""
+        mr = self.model_runner
+        if max_context_len is None:
+            max_context_len = int(mr.model_config.context_len)
+        if device is None:
+            device = mr.device if mr is not None and hasattr(mr, "device") else "cuda"
+        pages = max_bs * ((int(max_context_len) + PAGE_SIZE - 1) // PAGE_SIZE + 1)
+        self._graph_tables = (torch.zeros(max_bs + 1, dtype=torch.int32, device=device),
+                              torch.zeros(pages, dtype=torch.int32, device=device),
+                              torch.ones(max_bs, dtype=torch.int32, device=device))
+        self._graph_max_bs = max_bs
+
+    def _fill_graph_tables(self, bs, req_pool_indices, seq_lens, req_to_token=None):
+        if getattr(self, "_graph_tables", None) is None:
+            raise RuntimeError("init_cuda_graph_state must run before graph capture")
+        if bs > self._graph_max_bs:
+            raise ValueError(f"batch {bs} exceeds the graph state's {self._graph_max_bs}")
+        if req_to_token is None:
+            req_to_token = self.model_runner.req_to_token_pool.req_to_token
+        indptr, indices, last = paging.build_page_table(
+            req_to_token, req_pool_indices[:bs], seq_lens[:bs], out=self._graph_tables)
+        self.forward_metadata = DecodeMetadata(indptr, indices, last, 0)
+
+    def init_forward_metadata_capture_cuda_graph(self, bs, num_tokens, req_pool_indices,
+                                                 seq_lens, encoder_lens=None, forward_mode=None,
+                                                 spec_info=None, req_to_token=None):
+        self._fill_graph_tables(bs, req_pool_indices, seq_lens, req_to_token)
+
+    def init_forward_metadata_replay_cuda_graph(self, bs, req_pool_indices, seq_lens,
+                                                seq_lens_sum=None, encoder_lens=None,
+                                                forward_mode=None, spec_info=None,
+                                                seq_lens_cpu=None, req_to_token=None):
+        self._fill_graph_tables(bs, req_pool_indices, seq_lens, req_to_token)
 
     # ---------------------------------------------------------------- reference shim API
     def forward(self, q, kv_data=None, kv_indptr=None, kv_indices=None, kv_last_page_len=None,
