@@ -230,6 +230,10 @@ def main():
     dk_lib.check(full_call(), "decode_attention")
     torch.cuda.synchronize()
     finite = bool(torch.isfinite(out).all())
+    # q.k path the library takes (its automatic rule: MFMA beyond 4 q heads per kv head
+    # and for fp8 at D = 256)
+    mfma_qk = args.qk_path == 1 or (args.qk_path == 0 and (hq // hkv > 4 or (kv8 and d >= 256)))
+    qk_name = "mfma" if mfma_qk else "valu"
 
     rec = {
         "metric": METRIC, "value": round(nbytes / (p50 * 1e-6) / 1e12, 4), "unit": "TB/s",
@@ -246,7 +250,7 @@ def main():
                    "schedule": {1: "one pass"}.get(eff, "balanced + merge" if eff == 0
                                                    else f"split {eff} + merge"),
                    "plan_hint_max_pages": hint,
-                   "qk_path": "mfma" if args.qk_path == 1 else "valu", "pv_path": "mfma"},
+                   "qk_path": qk_name, "pv_path": "mfma"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
         "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
         "bytes_per_call": nbytes, "wall_s_timed_loop": round(wall, 3),

@@ -238,8 +238,8 @@ def decode_attention(
                            uint8 scratch of dk_lib.workspace_bytes(...) bytes
         qk_path, waves_per_group, waves_per_cu, schedule : tuning knobs (0 =
                            defaults; qk_path 1 = MFMA q.k, 2 = VALU q.k, 0 = VALU up to
-                           8 q heads per kv head (4 at D=256 or over fp8) and MFMA with
-                           16 heads per wavefront beyond; schedule (for
+                           4 q heads per kv head and MFMA (up to 16 heads per wavefront)
+                           beyond and for fp8 at D=256; schedule (for
                            split_kv 0) 1 = always balanced, 2 = always one pass)
         max_pages_per_seq: plan hint for split_kv 0 (see plan_hint): the longest
                            sequence's page count, 0 = unknown. Affects speed only.

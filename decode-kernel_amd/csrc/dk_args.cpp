@@ -43,13 +43,12 @@ const char* last_error() { return g_error.c_str(); }
 int valu_head_cap(int head_dim) { return head_dim >= 256 ? 4 : 8; }
 
 bool qk_on_mfma(int qk_path, int group, int head_dim, bool kv8) {
-  // automatic: MFMA once the group exceeds what the VALU path serves best in one chunk --
-  // 8 heads, or 4 at D = 256 and over an fp8 cache -- and for fp8 at D = 256 (measured at
-  // B=32 ctx 8192: fp8 40/8 and 64/8 heads 156 us VALU vs 116 MFMA; fp8 D=256 16/4
-  // 131 vs 103; fp16 64/8 171 vs 185, at D=64 103 vs 115 and at D=256 16/4 188 vs 196,
-  // so 16-bit caches keep the VALU path up to 8 heads)
-  const int cap = kv8 ? 4 : valu_head_cap(head_dim);
-  return qk_path == 1 || (qk_path == 0 && (group > cap || (kv8 && head_dim >= 256)));
+  // automatic: MFMA beyond 4 q heads per kv head, and for fp8 at D = 256. Measured at B=32
+  // ctx 8192, best schedule, VALU vs MFMA q.k, us: fp16 D=128 32/32 633 vs 640, 16/8 163
+  // vs 165, 32/8 159 vs 164, 40/8 173 vs 169, 56/8 171 vs 169, 64/8 170 vs 170 (balanced
+  // 182 vs 174); D=64 32/8 93 vs 95, 40/8 108 vs 95; bf16 32/8 158 vs 165; fp8 64/8 156
+  // vs 93, D=256 16/4 131 vs 103.
+  return qk_path == 1 || (qk_path == 0 && (group > 4 || (kv8 && head_dim >= 256)));
 }
 
 HeadChunks head_chunks(int group, int head_dim, bool mfma) {

@@ -8,10 +8,11 @@
 //     its dims for its 4 tokens and the G heads of the GQA group, and a reduce-scatter
 //     over the row's 16 lanes leaves lane (r, c) with the scores of tokens 4r..4r+3 for
 //     q head c mod 4.
-//   * K rows, MFMA q.k path: lane l holds token l%16 with 8 dims per
-//     v_mfma_f32_16x16x32_{f16,bf16}, so S^T = K.Q^T lands in the same score layout.
-//     Its loads read 64 bytes per row per instruction; the VALU path's full-row loads
-//     measured faster on MI355X, so VALU is the default.
+//   * K rows, MFMA q.k path (groups above 4 heads): lane l holds token l%16 with 8 dims
+//     per v_mfma_f32_16x16x32_{f16,bf16}, so S^T = K.Q^T lands in the same score layout.
+//     K is loaded like V (whole rows per instruction) and moved into that layout through
+//     a per-wavefront LDS tile (Wave::STAGE); loading the operand layout directly reads
+//     64 bytes per row per instruction, which MI355X streams markedly slower.
 //   Every K/V element is read once and serves all G heads of its kv head.
 //   Online softmax is fp32 in the log2 domain (v_exp_f32); the reference max only moves
 //   when a score exceeds it by more than 2^8, so accumulators are rescaled a handful of
@@ -71,6 +72,12 @@ constexpr float kEmptyM = -1e9f;        // partial_m of an empty split (attentio
 constexpr float kMinit = -1e30f;        // running reference before the first score
 constexpr float kSlack = 8.0f;          // log2 headroom before the reference max moves
 constexpr float kNegInf = -__builtin_inff();
+
+// MFMA q.k with K staged through LDS (see Wave::STAGE); a build may turn it off with
+// DK_STAGE_K=0 for comparisons.
+#ifndef DK_STAGE_K
+#define DK_STAGE_K 1
+#endif
 
 // ---------------------------------------------------------------- launch arguments
 struct Pass1Args {
@@ -347,8 +354,22 @@ struct Wave {
   // MFMA q.k: 16-byte K loads per lane, token c, bytes 16*r16 + 64*i of the row; an fp8
   // load holds the dims of two MFMAs (D/64 loads), a 16-bit load those of one (D/32)
   static constexpr int NKL = KV8 ? D / 64 : NMF;
+  // STAGE (MFMA q.k): K is loaded like V -- lane (r16, c) takes bytes c*RB/16 .. of tokens
+  // 4*r16 .. 4*r16+3, so every load instruction reads whole rows -- then written to this
+  // wavefront's LDS tile and read back in the MFMA layout above (token c, 16-byte chunk
+  // 4*i + r16). Loading the MFMA layout directly reads 64-byte row segments per
+  // instruction, which HBM serves markedly slower. Chunk k of token t sits at chunk
+  // position k ^ (t & SWZ) of LDS row t, so neither the writes (one token per 16 lanes)
+  // nor the reads (16 tokens per 16 lanes) meet the same bank twice. Not for fp8 at
+  // D = 256, whose wavefronts already need all 256 registers and measured slower staged.
+  static constexpr bool STAGE = MFMA && (DK_STAGE_K != 0) && !(KV8 && D >= 256);
+  static constexpr int RB = D * EB;                       // bytes per K row
+  static constexpr int NCH = RB / 16;                     // 16-byte chunks per row
+  static constexpr int SWZ = (NCH < 16 ? NCH : 16) - 1;
+  static constexpr int STAGE_BYTES = STAGE ? kPage * RB : 0;
 
   int r16, c;
+  uint8_t* kst;           // STAGE: this wavefront's K tile in LDS (STAGE_BYTES)
   int hv;                 // valid q heads of this chunk (<= G); heads hv.. are masked
   u32 koff, voff, tok_s, extent;
   int64_t kv_v;
@@ -366,7 +387,7 @@ struct Wave {
     r16 = lane >> 4;
     c = lane & 15;
     tok_s = (u32)a.kv_s;
-    koff = MFMA ? (u32)(c * a.kv_s + 16 * r16) : (u32)(4 * r16 * a.kv_s + EB * DPL * c);
+    koff = MFMA && !STAGE ? (u32)(c * a.kv_s + 16 * r16) : (u32)(4 * r16 * a.kv_s + EB * DPL * c);
     voff = (u32)(4 * r16 * a.kv_s + EB * DPL * c);
     extent = a.page_extent;
     kv_v = a.kv_v;
@@ -430,7 +451,7 @@ struct Wave {
     const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, ext);
     const __amdgpu_buffer_rsrc_t rv = page_rsrc(pg + kv_v, ext);
     constexpr int TW = KB / 4;   // words per token per lane as loaded
-    if constexpr (MFMA) {
+    if constexpr (MFMA && !STAGE) {
 #pragma unroll
       for (int i = 0; i < NKL; ++i) ld_buf<4>(&kb[4 * i], rk, koff, 64 * i);
     } else {
@@ -441,10 +462,55 @@ struct Wave {
     for (int r = 0; r < 4; ++r) ld_buf<TW>(&vb[r * TW], rv, voff, r * tok_s);
   }
 
-  // One loaded page: fp8 buffers are widened to T pairs first (word u of a token's fp8
-  // dims 4u..4u+3 becomes words 2u, 2u+1), then compute_page.
+  // STAGE: the K words of a page as loaded (row layout) -> the MFMA layout, through LDS
+  __device__ __forceinline__ void stage_k(const u32 (&kb)[KB], u32 (&km)[KB]) const {
+    constexpr int TB = RB / 16;   // bytes per token per lane as loaded (4, 8, 16 or 32)
+    constexpr int TW = TB / 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * r16 + r;
+      uint8_t* row = kst + t * RB;
+      if constexpr (TB >= 16) {
+#pragma unroll
+        for (int h = 0; h < TB / 16; ++h) {
+          const int k = c * (TB / 16) + h;
+          *reinterpret_cast<u32x4*>(row + ((k ^ (t & SWZ)) << 4)) =
+              u32x4{kb[r * TW + 4 * h], kb[r * TW + 4 * h + 1], kb[r * TW + 4 * h + 2],
+                    kb[r * TW + 4 * h + 3]};
+        }
+      } else {
+        const int k = (c * TB) >> 4, o = (c * TB) & 15;
+        uint8_t* dst = row + ((k ^ (t & SWZ)) << 4) + o;
+        if constexpr (TB == 8)
+          *reinterpret_cast<u32x2*>(dst) = u32x2{kb[2 * r], kb[2 * r + 1]};
+        else
+          *reinterpret_cast<u32*>(dst) = kb[r];
+      }
+    }
+    const uint8_t* row = kst + c * RB;
+#pragma unroll
+    for (int i = 0; i < NCH / 4; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(row + (((4 * i + r16) ^ (c & SWZ)) << 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) km[4 * i + e] = v[e];
+    }
+  }
+
+  // One loaded page: K staged into the MFMA layout (STAGE); fp8 buffers are widened to T
+  // pairs (word u of a token's fp8 dims 4u..4u+3 becomes words 2u, 2u+1); then compute_page.
   template <bool CAP>
   __device__ __forceinline__ void consume(const u32 (&kb)[KB], u32 (&vb)[VB], int valid) {
+    if constexpr (STAGE) {
+      u32 km[KB];
+      stage_k(kb, km);
+      consume_loaded<CAP>(km, vb, valid);
+    } else {
+      consume_loaded<CAP>(kb, vb, valid);
+    }
+  }
+
+  template <bool CAP>
+  __device__ __forceinline__ void consume_loaded(const u32 (&kb)[KB], u32 (&vb)[VB], int valid) {
     if constexpr (KV8) {
       u32 kw[KW], vw[VW];
 #pragma unroll
@@ -976,9 +1042,11 @@ template <class T, int D, int G, int NW, bool MFMA, bool KV8>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_split(Pass1Args a) {
   using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
+  __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? NW * WV::STAGE_BYTES : 16];
   WV wv;
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
+  wv.kst = kst + w * WV::STAGE_BYTES;
 
   // workgroup -> (head chunk, kv head, split, sequence). The head chunks of one (sequence,
   // kv head, split) read the same pages: they are placed kXcds workgroup ids apart (the
@@ -1050,9 +1118,11 @@ template <class T, int D, int G, int NW, bool MFMA, bool KV8>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_balanced(Pass1Args a) {
   using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
+  __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? NW * WV::STAGE_BYTES : 16];
   WV wv;
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
+  wv.kst = kst + w * WV::STAGE_BYTES;
   const int HC = a.hkv * a.chunks;
   const int g = blockIdx.x;
   const int hc = g % HC;

@@ -70,10 +70,9 @@ typedef struct {
 /* Optional tuning knobs (NULL = defaults). No counterpart in the reference, which
  * hard-codes one kernel per extension module (src/cuda_/build.py:256-282). */
 typedef struct {
-  int32_t qk_path;         /* 0 = automatic: VALU dot2 q.k up to 8 q heads per kv head (4 at
-                              D = 256 or over an fp8 cache), MFMA q.k with 16 heads per
-                              wavefront beyond and for fp8 at D = 256; 1 = MFMA, 2 = VALU;
-                              P.V always on MFMA                                          */
+  int32_t qk_path;         /* 0 = automatic: VALU dot2 q.k up to 4 q heads per kv head,
+                              MFMA q.k (up to 16 heads per wavefront) beyond and for fp8
+                              at D = 256; 1 = MFMA, 2 = VALU; P.V always on MFMA         */
   int32_t waves_per_group; /* 0 = default: 2, or 4 with kv-head rows of <= 128 bytes (fp8,
                               or D = 64) or 8+ heads per wavefront; else 1, 2 or 4        */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
