@@ -14,6 +14,9 @@ host sync, so host launch overhead is hidden behind it and the events measure GP
 The W warm-up steps are such flush + call steps too, after an untimed settling phase of
 the same steps (0.3 s) that lets the GPU clocks reach their steady state.
 
+Other shapes (--num-q-heads, --num-kv-heads, --head-dim, --batch, --ctx, --kv-dtype) are
+for profiling; the JSON's config names the workload measured.
+
 Prints one JSON line. `value` is achieved algorithmic HBM bandwidth in TB/s
 (bytes of the reference's model, bench/microbench_cuda.py:114-121, plus page tables,
 divided by the p50 per-call time); `us_per_call` is the p50 time.
@@ -57,6 +60,9 @@ def parse_args():
                     help="balanced schedule: wavefronts per CU (0 = default)")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--num-q-heads", type=int, default=32)
+    ap.add_argument("--num-kv-heads", type=int, default=8)
+    ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128, 256])
     ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"])
     ap.add_argument("--kv-dtype", default="same", choices=["same", "fp8"],
                     help="cache element type: q's (the metric's fp16) or fp8 E4M3 (an "
@@ -136,7 +142,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
-    B, ctx, hq, hkv, d = args.batch, args.ctx, 32, 8, 128
+    B, ctx, hq, hkv, d = args.batch, args.ctx, args.num_q_heads, args.num_kv_heads, args.head_dim
+    # the recorded rocprofv3 traffic belongs to the metric's workload only
+    metric_workload = ((B, ctx, hq, hkv, d) == (32, 8192, 32, 8, 128)
+                       and args.page_table == "permuted")
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table=args.page_table, seed=1)
     kv_ref = kv                        # the cache's values for the CPU baseline
@@ -257,7 +266,7 @@ def main():
         "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": read_traffic(args.kv_dtype),
+                     "traffic": read_traffic(args.kv_dtype) if metric_workload else None,
                      "kernel": "dk_pass1_balanced" if eff == 0 else "dk_pass1_split"},
         "cpu_baseline": None,
     }

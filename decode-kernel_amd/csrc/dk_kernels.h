@@ -360,8 +360,9 @@ struct Wave {
   // 4*i + r16). Loading the MFMA layout directly reads 64-byte row segments per
   // instruction, which HBM serves markedly slower. Chunk k of token t sits at chunk
   // position k ^ (t & SWZ) of LDS row t, so neither the writes (one token per 16 lanes)
-  // nor the reads (16 tokens per 16 lanes) meet the same bank twice. Not for fp8 at
-  // D = 256, whose wavefronts already need all 256 registers and measured slower staged.
+  // nor the reads (16 tokens per 16 lanes) put two lanes of a 16-lane group on one bank.
+  // Not for fp8 at D = 256, whose wavefronts already need all 256 registers and measured
+  // slower staged.
   static constexpr bool STAGE = MFMA && (DK_STAGE_K != 0) && !(KV8 && D >= 256);
   static constexpr int RB = D * EB;                       // bytes per K row
   static constexpr int NCH = RB / 16;                     // 16-byte chunks per row
