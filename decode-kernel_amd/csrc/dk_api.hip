@@ -192,6 +192,7 @@ int run(Problem p, bool do_merge, void* stream) {
   // bytes from a kv head's K (or V) slice base that its rows reach (validated < 2^31)
   a.page_extent = (uint32_t)(((int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * kes);
   a.direct = direct ? 1 : 0;
+  a.ranges = waves_per_pair;
   const bool kv8 = pl.kv8;
   const float k_scale = kv8 && p.opt.k_scale != 0.f ? p.opt.k_scale : 1.f;
   const float score_scale =
@@ -213,6 +214,11 @@ int run(Problem p, bool do_merge, void* stream) {
   L.balanced = pl.balanced;
   L.kv8 = pl.kv8;
   L.grid = (int)pl.grid;
+  if (pl.balanced && pl.chunks > 1) {
+    // the chunks of a (range, kv head) unit sit kXcds workgroup ids apart: whole rounds
+    const int64_t units = (int64_t)p.hkv * waves_per_pair;
+    L.grid = (int)((units + kXcds - 1) / kXcds * kXcds * pl.chunks);
+  }
   L.stream = static_cast<hipStream_t>(stream);
   hipError_t e = p.dtype == DK_F16 ? launch_pass1<F16>(a, L) : launch_pass1<BF16>(a, L);
   if (e != hipSuccess) return hip_fail(e, "pass-1 launch");

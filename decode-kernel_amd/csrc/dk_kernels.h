@@ -103,6 +103,7 @@ struct Pass1Args {
   uint32_t page_extent;               // bytes one kv head's K (or V) rows of a page span (< 2^31)
   int32_t direct;                     // explicit split 1 / balanced: may write the
                                       // normalised output (0: partials only)
+  int32_t ranges;                     // balanced: workgroups (page ranges) per head chunk
   float kscale;                       // log2(e) * softmax scale (* K dequant scale)
   float cap_in, cap_out;              // logit soft-cap: x = cap_out * tanh(q.k * cap_in)
                                       // (cap_out == 0: off, x = q.k * kscale)
@@ -1105,10 +1106,10 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
 }
 
 // ---------------------------------------------------------------- pass 1, balanced
-// Head-major persistent schedule over workgroups. Workgroup g serves head chunk
-// hc = g % HC (HC = hkv * chunks pairs per sequence), so consecutive workgroups -- and the
-// XCDs they are dispatched to round-robin -- cover all kv heads of the same pages at the
-// same time. The Wg = gridDim / HC workgroups of a head chunk split its pages in sequence
+// Head-major persistent schedule over workgroups. Each of the HC = hkv * chunks head
+// chunks (hc = chunk * hkv + kv head) has Wg = a.ranges workgroups; consecutive
+// workgroups -- and the XCDs they are dispatched to round-robin -- cover all kv heads of
+// the same pages at the same time. The Wg workgroups of a head chunk split its pages in sequence
 // order ((b, page) is linear unit seq_begin(b) - seq_begin(0) + page) into Wg ranges of
 // L = ceil(P / Wg) pages; workgroup j takes range j and its NW wavefronts interleave the
 // pages of each segment (maximal run of the range inside one sequence). A sequence covered
@@ -1124,11 +1125,22 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
   wv.kst = kst + w * WV::STAGE_BYTES;
-  const int HC = a.hkv * a.chunks;
-  const int g = blockIdx.x;
-  const int hc = g % HC;
-  const int Wg = (int)(gridDim.x / HC);
-  const int j = g / HC;
+  // workgroup -> (head chunk hc, range j). Unit u = j * hkv + kv head: consecutive
+  // workgroups cover the kv heads of the same pages. With several head chunks, which all
+  // read the unit's pages, the chunks of a unit are placed kXcds workgroup ids apart (the
+  // grid is padded to whole rounds), so they run on one XCD and share its L2.
+  const int Wg = a.ranges;
+  int hc, j;
+  if (a.chunks > 1) {
+    const int x = (int)blockIdx.x % kXcds, y = (int)blockIdx.x / kXcds;
+    const int un = (y / a.chunks) * kXcds + x;
+    if (un >= a.hkv * Wg) return;                            // padding of the last round
+    j = un / a.hkv;
+    hc = (y % a.chunks) * a.hkv + un % a.hkv;
+  } else {
+    hc = (int)blockIdx.x % a.hkv;
+    j = (int)blockIdx.x / a.hkv;
+  }
   const int base = seq_begin(a, 0);
   const int P = max(seq_begin(a, a.batch) - base, 0);        // pages per head chunk
   const int L = (P + Wg - 1) / Wg;
