@@ -363,7 +363,7 @@ def test_balanced_head_layouts(d, hq, hkv):
 
 # GQA groups that are not a power of two, or exceed one chunk: the group is processed in
 # the fewest chunks of at most 8 q heads (4 at D=256) on the VALU q.k path or 16 on the
-# MFMA path (the default for groups beyond one VALU chunk), each by a wavefront sized to
+# MFMA path (the default beyond 4 q heads per kv head), each by a wavefront sized to
 # the next power of two with the surplus heads masked (no q read, no output or partial
 # write)
 PADDED_GROUPS = [(128, 3, 1), (128, 10, 2), (64, 12, 2), (128, 14, 2), (128, 20, 2),
