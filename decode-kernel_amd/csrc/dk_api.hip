@@ -140,6 +140,13 @@ int run(Problem p, bool do_merge, void* stream) {
       pl.balanced = false;
       pl.grid = split_grid(p.batch, p.hkv, 1, pl.chunks);
     } else {
+      const int64_t hint = p.opt.max_pages_per_seq;
+      if (hint > 0 && !p.opt.waves_per_group && !p.opt.waves_per_cu &&
+          pl.waves < kDefaultWavesPerGroupNarrow &&
+          (int64_t)p.batch * hint * pl.pairs_per_seq <= (int64_t)kSmallUnitsPerCU * cus) {
+        pl.waves = kDefaultWavesPerGroupNarrow;
+        p.opt.waves_per_cu = kDefaultWavesPerCUNarrow;
+      }
       pl.grid = balanced_groups(p, pl, cus);
       waves_per_pair = (int)(pl.grid / pl.pairs_per_seq);
     }

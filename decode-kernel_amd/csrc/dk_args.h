@@ -23,6 +23,12 @@ constexpr int kDefaultWavesPerGroup = 2;
 constexpr int kDefaultWavesPerCUNarrow = 4;
 constexpr int kDefaultWavesPerGroupNarrow = 4;
 constexpr int kNarrowRowBytes = 128;
+// Balanced schedule over a small problem (the plan hint bounds it at this many (page, head
+// chunk) units per compute unit or fewer): the narrow-row wave counts, so each wavefront
+// streams half the pages and the call ends one page round trip sooner (B=1 and B=4 at ctx
+// 4096, 32/8/128 fp16: 16.2 -> 15.1 and 23.3 -> 22.4 us; at 128 units per CU or 64 with
+// one sequence of 32768 tokens, two wavefronts stay faster)
+constexpr int kSmallUnitsPerCU = 32;
 
 // Everything a launch needs that is known on the host.
 struct Problem {
