@@ -66,17 +66,36 @@ int explicit_split(const Problem& p, int device) {
 // MI355X at every decode shape tried with rows of 256 bytes or more and up to 4 q heads
 // per wavefront (each wavefront keeps two pages of loads in flight); four with narrower
 // rows (fp8 cache, or D = 64) or 8 q heads per wavefront (twice the work per page).
-int waves_per_cu(const Problem& p, const Plan& pl) {
+int waves_per_cu(const Problem& p, const Plan& pl, int hp = 1) {
   if (p.opt.waves_per_cu) return p.opt.waves_per_cu;
+  if (hp > 1) return kGroupedWavesPerCU;
   return p.narrow_rows() || pl.heads >= 8 ? kDefaultWavesPerCUNarrow : kDefaultWavesPerCU;
 }
 
+// Kv heads per workgroup of the balanced schedule (1 = one). Rows of at most
+// kNarrowRowBytes per kv head and token: the workgroup serves kGroupedKvHeads neighbouring
+// kv heads of the same pages (2 if the kv-head count is not a multiple of it), two
+// wavefronts each, so their row segments of each token are fetched together. Not with
+// user-set wave counts, nor for problems the plan hint shows to be small (fewer than
+// kGroupedMinUnitsPerCU (page, head chunk) units per CU), where it measured slower.
+int grouped_kv_heads(const Problem& p, const Plan& pl, int cus) {
+  if (p.split != 0 || !p.narrow_rows() || p.opt.waves_per_group || p.opt.waves_per_cu) return 1;
+  const int64_t hint = p.opt.max_pages_per_seq;
+  if (hint > 0 &&
+      (int64_t)p.batch * hint * pl.pairs_per_seq < (int64_t)kGroupedMinUnitsPerCU * cus)
+    return 1;
+  if (p.hkv % kGroupedKvHeads == 0) return kGroupedKvHeads;
+  return p.hkv % 2 == 0 ? 2 : 1;
+}
+
 // Workgroups of the balanced grid: about waves_per_cu wavefronts per compute unit, a
-// whole number of workgroups per head chunk, at most kMaxWaves wavefronts.
-int64_t balanced_groups(const Problem& p, const Plan& pl, int cus) {
-  const int64_t hc = pl.pairs_per_seq;
-  const int64_t max_groups = std::max<int64_t>(hc, kMaxWaves / pl.waves / hc * hc);
-  const int64_t groups = std::max<int64_t>(1, (int64_t)cus * waves_per_cu(p, pl) / pl.waves);
+// whole number of workgroups per range (pairs_per_seq / hp of them), at most kMaxWaves
+// wavefronts.
+int64_t balanced_groups(const Problem& p, const Plan& pl, int cus, int hp = 1) {
+  const int64_t hc = pl.pairs_per_seq / hp;
+  const int64_t block = (int64_t)pl.waves * hp;
+  const int64_t max_groups = std::max<int64_t>(hc, kMaxWaves / block / hc * hc);
+  const int64_t groups = std::max<int64_t>(1, (int64_t)cus * waves_per_cu(p, pl, hp) / block);
   return std::min(max_groups, std::max(hc, (groups + hc / 2) / hc * hc));
 }
 
@@ -88,6 +107,10 @@ int64_t balanced_groups(const Problem& p, const Plan& pl, int cus) {
 bool auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return false;
   if (p.opt.schedule == 2) return true;
+  // rows of at most 64 bytes: the balanced schedule with grouped kv heads
+  if ((int64_t)p.head_dim * p.kv_esize() <= kGroupedAlwaysRowBytes &&
+      grouped_kv_heads(p, pl, cus) > 1)
+    return false;
   const int64_t hint = p.opt.max_pages_per_seq;
   if (hint <= 0) return false;
   const int64_t groups = balanced_groups(p, pl, cus);
@@ -106,6 +129,7 @@ int run(Problem p, bool do_merge, void* stream) {
   if (rc != DK_OK || p.batch == 0) return rc;
   Plan pl = make_plan(p);
   int waves_per_pair = 0;   // balanced: workgroups per head chunk
+  int hp = 1;               // balanced: kv heads per workgroup
   if (pl.balanced && p.opt.window > 0) {
     // a sliding window bounds every sequence's pages: explicit splits of the window's
     // pages, as many as fill the device and fit the workspace
@@ -140,15 +164,18 @@ int run(Problem p, bool do_merge, void* stream) {
       pl.balanced = false;
       pl.grid = split_grid(p.batch, p.hkv, 1, pl.chunks);
     } else {
+      hp = grouped_kv_heads(p, pl, cus);
       const int64_t hint = p.opt.max_pages_per_seq;
-      if (hint > 0 && !p.opt.waves_per_group && !p.opt.waves_per_cu &&
-          pl.waves < kDefaultWavesPerGroupNarrow &&
-          (int64_t)p.batch * hint * pl.pairs_per_seq <= (int64_t)kSmallUnitsPerCU * cus) {
+      if (hp > 1) {
+        pl.waves = kGroupedWavesPerKvHead;
+      } else if (hint > 0 && !p.opt.waves_per_group && !p.opt.waves_per_cu &&
+                 pl.waves < kDefaultWavesPerGroupNarrow &&
+                 (int64_t)p.batch * hint * pl.pairs_per_seq <= (int64_t)kSmallUnitsPerCU * cus) {
         pl.waves = kDefaultWavesPerGroupNarrow;
         p.opt.waves_per_cu = kDefaultWavesPerCUNarrow;
       }
-      pl.grid = balanced_groups(p, pl, cus);
-      waves_per_pair = (int)(pl.grid / pl.pairs_per_seq);
+      pl.grid = balanced_groups(p, pl, cus, hp);
+      waves_per_pair = (int)(pl.grid / (pl.pairs_per_seq / hp));
     }
   }
   const bool direct = p.need_out && (p.split == 1 || pl.balanced);
@@ -220,10 +247,12 @@ int run(Problem p, bool do_merge, void* stream) {
   L.mfma = pl.mfma;
   L.balanced = pl.balanced;
   L.kv8 = pl.kv8;
+  L.hp = hp;
   L.grid = (int)pl.grid;
   if (pl.balanced && pl.chunks > 1) {
-    // the chunks of a (range, kv head) unit sit kXcds workgroup ids apart: whole rounds
-    const int64_t units = (int64_t)p.hkv * waves_per_pair;
+    // the chunks of a (range, kv-head group) unit sit kXcds workgroup ids apart: whole
+    // rounds
+    const int64_t units = (int64_t)(p.hkv / hp) * waves_per_pair;
     L.grid = (int)((units + kXcds - 1) / kXcds * kXcds * pl.chunks);
   }
   L.stream = static_cast<hipStream_t>(stream);

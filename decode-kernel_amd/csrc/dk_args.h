@@ -29,6 +29,19 @@ constexpr int kNarrowRowBytes = 128;
 // 4096, 32/8/128 fp16: 16.2 -> 15.1 and 23.3 -> 22.4 us; at 128 units per CU or 64 with
 // one sequence of 32768 tokens, two wavefronts stay faster)
 constexpr int kSmallUnitsPerCU = 32;
+// Balanced schedule over narrow rows: 4 neighbouring kv heads per workgroup, 2 wavefronts
+// each, one such workgroup per CU (64- and 128-byte row segments 512 B or 1 KB apart
+// stream far better when the segments of neighbouring heads are fetched together). B=32
+// ctx 8192, balanced before -> after, us: fp8 D=64 96 -> 64, fp8 D=128 97 -> 94, fp16
+// D=64 96 -> 91; fp8 D=128 B=64 184 -> 172; but B=4 ctx 8192 fp8 25.4 -> 26.7 (hence
+// kGroupedMinUnitsPerCU). With rows of at most kGroupedAlwaysRowBytes the automatic
+// schedule takes it over one pass (fp8 D=64: 64 vs 94 us); wider narrow rows keep the
+// one-pass choice (fp8 D=128 95 vs 94, D=64 bf16 ctx 2048 29 vs 33 us).
+constexpr int kGroupedKvHeads = 4;
+constexpr int kGroupedWavesPerKvHead = 2;
+constexpr int kGroupedWavesPerCU = 8;
+constexpr int kGroupedMinUnitsPerCU = 128;
+constexpr int kGroupedAlwaysRowBytes = 64;
 
 // Everything a launch needs that is known on the host.
 struct Problem {

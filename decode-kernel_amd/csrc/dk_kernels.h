@@ -947,19 +947,23 @@ struct CombineSmem {
   float m[NW][G], mt[NW][G], l[NW][G];
 };
 
-// After every wavefront's reduce_rows: the workgroup's result for its G heads, written
-// normalised to out (head h at out + h * o_h) when `direct`, otherwise as a partial with
-// head h at row prow0 + h * phstride.
+// After every wavefront's reduce_rows: the result of the NW wavefronts that share one kv
+// head (w = this wavefront among them, tid = this thread among their NW * 64) for its G
+// heads, written normalised to out (head h at out + h * o_h) when `direct`, otherwise as a
+// partial with head h at row prow0 + h * phstride. Every wavefront of the workgroup calls
+// it the same number of times (it holds workgroup barriers).
 template <class T, int D, int G, int NW, class WV>
 __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 ? NW : 1)>& sm,
                                               const Pass1Args& a, bool direct, uint8_t* out,
-                                              int64_t o_h, int64_t prow0, int64_t phstride) {
+                                              int64_t o_h, int64_t prow0, int64_t phstride,
+                                              int w, int tid) {
   constexpr int DPL = WV::DPL, NS = WV::NS, GQ = WV::GQ;
   if constexpr (NW == 1) {
+    (void)w;
+    (void)tid;
     if (direct) wv.store_output(out, o_h);
     else wv.store_partial(a, prow0, phstride);
   } else {
-    const int w = uniform(threadIdx.x >> 6);
     if constexpr (WV::WIDE) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -990,7 +994,7 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
       }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < wv.hv * D; idx += NW * 64) {
+    for (int idx = tid; idx < wv.hv * D; idx += NW * 64) {
       const int h = idx / D, d = idx % D;
       float mt = kNegInf;
 #pragma unroll
@@ -1102,7 +1106,8 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   wv.reduce_rows();
   combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
-                             ((int64_t)b * a.hq + qh0) * a.split + s, a.split);
+                             ((int64_t)b * a.hq + qh0) * a.split + s, a.split, w,
+                             (int)threadIdx.x);
 }
 
 // ---------------------------------------------------------------- pass 1, balanced
@@ -1116,30 +1121,36 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
 // by a single segment is written out directly (when a.direct); otherwise the segment is
 // stored as a partial at slot hc * (Wg + batch) + j + b (unique, < HC * (Wg + batch)) for the
 // merge kernel.
-template <class T, int D, int G, int NW, bool MFMA, bool KV8>
-__global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_balanced(Pass1Args a) {
+template <class T, int D, int G, int NW, bool MFMA, bool KV8, int HP>
+__global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_balanced(Pass1Args a) {
   using WV = Wave<T, D, G, MFMA, KV8>;
-  __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
-  __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? NW * WV::STAGE_BYTES : 16];
+  __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> smh[HP];
+  __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? HP * NW * WV::STAGE_BYTES : 16];
   WV wv;
   wv.init(a);
-  const int w = uniform(threadIdx.x >> 6);
-  wv.kst = kst + w * WV::STAGE_BYTES;
-  // workgroup -> (head chunk hc, range j). Unit u = j * hkv + kv head: consecutive
-  // workgroups cover the kv heads of the same pages. With several head chunks, which all
-  // read the unit's pages, the chunks of a unit are placed kXcds workgroup ids apart (the
-  // grid is padded to whole rounds), so they run on one XCD and share its L2.
+  const int wa = uniform(threadIdx.x >> 6);   // wavefront of the workgroup
+  const int hl = wa / NW, w = wa % NW;        // its kv head among the HP, its rank there
+  wv.kst = kst + wa * WV::STAGE_BYTES;
+  auto& sm = smh[hl];
+  // workgroup -> (HP head chunks hc, range j): its NW * HP wavefronts serve HP consecutive
+  // kv heads (same head chunk) of the same pages, so the HP row segments of each token are
+  // read at the same time (narrow rows: HP * 64 or HP * 128 contiguous bytes). Unit
+  // u = j * (hkv / HP) + kv-head group: consecutive workgroups cover the kv heads of the
+  // same pages. With several head chunks, which all read the unit's pages, the chunks of
+  // a unit are placed kXcds workgroup ids apart (the grid is padded to whole rounds), so
+  // they run on one XCD and share its L2.
   const int Wg = a.ranges;
+  const int hkg = a.hkv / HP;                 // kv-head groups (HP divides hkv)
   int hc, j;
   if (a.chunks > 1) {
     const int x = (int)blockIdx.x % kXcds, y = (int)blockIdx.x / kXcds;
     const int un = (y / a.chunks) * kXcds + x;
-    if (un >= a.hkv * Wg) return;                            // padding of the last round
-    j = un / a.hkv;
-    hc = (y % a.chunks) * a.hkv + un % a.hkv;
+    if (un >= hkg * Wg) return;                              // padding of the last round
+    j = un / hkg;
+    hc = (y % a.chunks) * a.hkv + (un % hkg) * HP + hl;
   } else {
-    hc = (int)blockIdx.x % a.hkv;
-    j = (int)blockIdx.x / a.hkv;
+    hc = ((int)blockIdx.x % hkg) * HP + hl;
+    j = (int)blockIdx.x / hkg;
   }
   const int base = seq_begin(a, 0);
   const int P = max(seq_begin(a, a.batch) - base, 0);        // pages per head chunk
@@ -1190,7 +1201,8 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
     const int nslots = (start + np - 1) / L - start / L + 1;
     combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
                                a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
-                               ((int64_t)hc * (Wg + a.batch) + j + b) * G, 1);
+                               ((int64_t)hc * (Wg + a.batch) + j + b) * G, 1, w,
+                               (int)(threadIdx.x & 63) + 64 * w);
     if (u + n >= u_end) break;
     // next non-empty sequence
     u += n;

@@ -13,35 +13,38 @@ struct Pass1Launch {
   int d = 128, heads = 4, waves = 4;   // head_dim, q heads per workgroup, waves per workgroup
   bool mfma = false, balanced = false;
   bool kv8 = false;                    // fp8 (E4M3) cache
+  int hp = 1;                          // balanced: kv heads per workgroup (waves each)
   int grid = 0;
   hipStream_t stream = nullptr;
 };
 
-// Kernel symbol for (head_dim, heads, waves, mode) with q.k on the matrix cores (M) or
-// the VALU, over a 16-bit cache and over an fp8 cache; nullptr if not instantiated.
+// Kernel symbol for (head_dim, heads, waves, mode, kv heads per workgroup) with q.k on the
+// matrix cores (M) or the VALU, over a 16-bit cache and over an fp8 cache; nullptr if not
+// instantiated.
 template <class T, bool M>
-const void* pass1_symbol_16(int d, int heads, int waves, bool balanced);
+const void* pass1_symbol_16(int d, int heads, int waves, bool balanced, int hp);
 template <class T, bool M>
-const void* pass1_symbol_kv8(int d, int heads, int waves, bool balanced);
+const void* pass1_symbol_kv8(int d, int heads, int waves, bool balanced, int hp);
 template <class T>
 const void* merge_symbol(int d, bool balanced);
 
 template <class T>
-const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool kv8, bool balanced) {
+const void* pass1_symbol(int d, int heads, int waves, bool mfma, bool kv8, bool balanced,
+                         int hp = 1) {
   if (kv8)
-    return mfma ? pass1_symbol_kv8<T, true>(d, heads, waves, balanced)
-                : pass1_symbol_kv8<T, false>(d, heads, waves, balanced);
-  return mfma ? pass1_symbol_16<T, true>(d, heads, waves, balanced)
-              : pass1_symbol_16<T, false>(d, heads, waves, balanced);
+    return mfma ? pass1_symbol_kv8<T, true>(d, heads, waves, balanced, hp)
+                : pass1_symbol_kv8<T, false>(d, heads, waves, balanced, hp);
+  return mfma ? pass1_symbol_16<T, true>(d, heads, waves, balanced, hp)
+              : pass1_symbol_16<T, false>(d, heads, waves, balanced, hp);
 }
 
 template <class T>
 hipError_t launch_pass1(const Pass1Args& a, const Pass1Launch& L) {
-  const void* fn = pass1_symbol<T>(L.d, L.heads, L.waves, L.mfma, L.kv8, L.balanced);
+  const void* fn = pass1_symbol<T>(L.d, L.heads, L.waves, L.mfma, L.kv8, L.balanced, L.hp);
   if (!fn) return hipErrorInvalidDeviceFunction;
   Pass1Args arg = a;
   void* args[] = {&arg};
-  return hipLaunchKernel(fn, dim3(L.grid), dim3(L.waves * 64), args, 0, L.stream);
+  return hipLaunchKernel(fn, dim3(L.grid), dim3(L.waves * L.hp * 64), args, 0, L.stream);
 }
 
 template <class T>
@@ -56,57 +59,65 @@ hipError_t launch_merge(const MergeArgs& m, int d, bool balanced, hipStream_t st
 
 // ---- symbol tables (instantiated per element type and cache type)
 template <class T, int D, int G, int NW, bool M, bool KV8>
-const void* pass1_sym(bool balanced) {
-  return balanced ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8>)
-                  : reinterpret_cast<const void*>(&dk_pass1_split<T, D, G, NW, M, KV8>);
+const void* pass1_sym(bool balanced, int hp) {
+  if (!balanced)
+    return hp == 1 ? reinterpret_cast<const void*>(&dk_pass1_split<T, D, G, NW, M, KV8>)
+                   : nullptr;
+  if (hp == 1) return reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 1>);
+  // several kv heads per workgroup: rows of at most kNarrowRowBytes, two wavefronts each
+  if constexpr (D * (KV8 ? 1 : 2) <= kNarrowRowBytes && NW == 2) {
+    if (hp == 2) return reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 2>);
+    if (hp == 4) return reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 4>);
+  }
+  return nullptr;
 }
 
 template <class T, int D, int G, bool M, bool KV8>
-const void* pass1_sym_w(int waves, bool balanced) {
+const void* pass1_sym_w(int waves, bool balanced, int hp) {
   switch (waves) {
-    case 1: return pass1_sym<T, D, G, 1, M, KV8>(balanced);
-    case 2: return pass1_sym<T, D, G, 2, M, KV8>(balanced);
-    case 4: return pass1_sym<T, D, G, 4, M, KV8>(balanced);
+    case 1: return pass1_sym<T, D, G, 1, M, KV8>(balanced, hp);
+    case 2: return pass1_sym<T, D, G, 2, M, KV8>(balanced, hp);
+    case 4: return pass1_sym<T, D, G, 4, M, KV8>(balanced, hp);
     default: return nullptr;
   }
 }
 
 template <class T, int D, bool M, bool KV8>
-const void* pass1_sym_g(int heads, int waves, bool balanced) {
+const void* pass1_sym_g(int heads, int waves, bool balanced, int hp) {
   switch (heads) {
-    case 1: return pass1_sym_w<T, D, 1, M, KV8>(waves, balanced);
-    case 2: return pass1_sym_w<T, D, 2, M, KV8>(waves, balanced);
-    case 4: return pass1_sym_w<T, D, 4, M, KV8>(waves, balanced);
+    case 1: return pass1_sym_w<T, D, 1, M, KV8>(waves, balanced, hp);
+    case 2: return pass1_sym_w<T, D, 2, M, KV8>(waves, balanced, hp);
+    case 4: return pass1_sym_w<T, D, 4, M, KV8>(waves, balanced, hp);
     case 8:
       // 8 heads at D = 256 on the VALU path do not fit a wavefront's registers; the MFMA
       // path holds up to 16 heads in the same registers
-      if constexpr (D <= 128 || M) return pass1_sym_w<T, D, 8, M, KV8>(waves, balanced);
+      if constexpr (D <= 128 || M) return pass1_sym_w<T, D, 8, M, KV8>(waves, balanced, hp);
       return nullptr;
     case 16:
-      if constexpr (M) return pass1_sym_w<T, D, 16, M, KV8>(waves, balanced);
+      if constexpr (M) return pass1_sym_w<T, D, 16, M, KV8>(waves, balanced, hp);
       return nullptr;
     default: return nullptr;
   }
 }
 
 template <class T, bool M, bool KV8>
-const void* pass1_symbol_t(int d, int heads, int waves, bool balanced) {
+const void* pass1_symbol_t(int d, int heads, int waves, bool balanced, int hp) {
   switch (d) {
-    case 64: return pass1_sym_g<T, 64, M, KV8>(heads, waves, balanced);
-    case 128: return pass1_sym_g<T, 128, M, KV8>(heads, waves, balanced);
-    case 256: return pass1_sym_g<T, 256, M, KV8>(heads, waves, balanced);
+    case 64: return pass1_sym_g<T, 64, M, KV8>(heads, waves, balanced, hp);
+    case 128: return pass1_sym_g<T, 128, M, KV8>(heads, waves, balanced, hp);
+    case 256: return pass1_sym_g<T, 256, M, KV8>(heads, waves, balanced, hp);
     default: return nullptr;
   }
 }
 
 template <class T, bool M>
-const void* pass1_symbol_16(int d, int heads, int waves, bool balanced) {
-  return pass1_symbol_t<T, M, false>(d, heads, waves, balanced);
+const void* pass1_symbol_16(int d, int heads, int waves, bool balanced, int hp) {
+  return pass1_symbol_t<T, M, false>(d, heads, waves, balanced, hp);
 }
 
 template <class T, bool M>
-const void* pass1_symbol_kv8(int d, int heads, int waves, bool balanced) {
-  return pass1_symbol_t<T, M, true>(d, heads, waves, balanced);
+const void* pass1_symbol_kv8(int d, int heads, int waves, bool balanced, int hp) {
+  return pass1_symbol_t<T, M, true>(d, heads, waves, balanced, hp);
 }
 
 template <class T>
@@ -127,7 +138,7 @@ const void* merge_symbol(int d, bool balanced) {
 // (-DDK_HEAD_DIM=64 / 128 / 256), so the 24 units compile in parallel. Everything else
 // (the dispatch above, the merge kernels) is instantiated where it is used (dk_api.hip).
 #define DK_DECLARE_TABLE(T, D, M, KV8) \
-  extern template const void* pass1_sym_g<T, D, M, KV8>(int, int, bool);
+  extern template const void* pass1_sym_g<T, D, M, KV8>(int, int, bool, int);
 #define DK_DECLARE_TABLES_D(T, D)      \
   DK_DECLARE_TABLE(T, D, false, false) \
   DK_DECLARE_TABLE(T, D, true, false)  \

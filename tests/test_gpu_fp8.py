@@ -121,6 +121,8 @@ CASES = [
     (2, [700, 33], 16, 2, 256, torch.bfloat16, "permuted"),
     (2, 160, 64, 4, 128, torch.float16, "permuted"),
     (3, [1, 300, 40], 14, 2, 128, torch.bfloat16, "permuted"),     # 7 q heads per kv head
+    (2, [900, 77], 128, 4, 128, torch.float16, "permuted"),       # 2 head chunks of 16
+    (3, [513, 1, 64], 16, 4, 64, torch.bfloat16, "freelist"),     # 64-byte rows
 ]
 
 

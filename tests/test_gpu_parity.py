@@ -368,7 +368,10 @@ def test_balanced_head_layouts(d, hq, hkv):
 # write)
 PADDED_GROUPS = [(128, 3, 1), (128, 10, 2), (64, 12, 2), (128, 14, 2), (128, 20, 2),
                  (64, 24, 2), (128, 48, 2), (256, 5, 1), (256, 12, 2), (128, 32, 1),
-                 (64, 40, 1), (256, 17, 1)]
+                 (64, 40, 1), (256, 17, 1),
+                 # narrow rows with several head chunks: the balanced schedule's grouped kv
+                 # heads (2 and 4 per workgroup) with the chunks of a unit 8 ids apart
+                 (64, 64, 2), (64, 96, 4)]
 
 
 @pytest.mark.parametrize("d,hq,hkv", PADDED_GROUPS)
