@@ -554,7 +554,8 @@ struct Wave {
     }
   }
 
-  // One page: scores, online softmax, P.V. valid < 16 masks tokens >= valid.
+  // One page: scores, online softmax, P.V. valid = hi | lo << 8 masks the tokens outside
+  // [lo, hi) (a full page: valid == 16).
   // CAP: logit soft-capping on (a separate instantiation, so uncapped calls carry no
   // trace of it)
   template <bool CAP>
@@ -594,8 +595,8 @@ struct Wave {
     // `valid` = hi | lo << 8: tokens [lo, hi) of the page are attended. Others (the tail
     // of a sequence's last page, or before a sliding window's first token) are masked by
     // selection (never by multiplying), so stale or NaN bytes cannot reach the output
-    const int hi = valid & 0xff, lo = valid >> 8;
-    if (hi < kPage || lo > 0) {
+    if (valid != kPage) {
+      const int hi = valid & 0xff, lo = valid >> 8;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool dead = 4 * r16 + r >= hi || 4 * r16 + r < lo;
@@ -1095,9 +1096,14 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
     pid = pid < a.num_pages ? pid : 0u;
     return kvh_base + (int64_t)pid * a.kv_p;
   };
+  // page validity hi | lo << 8: a full page but for the sequence's last page and, with a
+  // window starting inside a page, that page
+  const int lo_page = first_tok > 0 ? first_page : -1;
+  const int enc_last = valid_last | (npages - 1 == lo_page ? first_tok << 8 : 0);
+  const int enc_lo = kPage | first_tok << 8;
   auto valid = [&](int i) -> int {
     const int pg = p0 + i;
-    return (pg == npages - 1 ? valid_last : kPage) | (pg == first_page ? first_tok << 8 : 0);
+    return pg == npages - 1 ? enc_last : (pg == lo_page ? enc_lo : kPage);
   };
   if (a.cap_out != 0.f)
     stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
