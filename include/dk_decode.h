@@ -74,9 +74,14 @@ typedef struct {
                               MFMA q.k (up to 16 heads per wavefront) beyond and for fp8
                               at D = 256; 1 = MFMA, 2 = VALU; P.V always on MFMA         */
   int32_t waves_per_group; /* 0 = default: 2, or 4 with kv-head rows of <= 128 bytes (fp8,
-                              or D = 64) or 8+ heads per wavefront; else 1, 2 or 4        */
+                              or D = 64) or 8+ heads per wavefront; the balanced schedule
+                              over such narrow rows serves 4 (or 2) neighbouring kv heads
+                              per workgroup with 2 wavefronts each, and over small
+                              problems (plan hint) uses 4; else 1, 2 or 4 (then one kv
+                              head per workgroup)                                         */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
-                              schedules aim for (0 = default: 2, or 4 as above)           */
+                              schedules aim for (0 = default: 2, or 4 as above, 8 with
+                              grouped kv heads)                                           */
   int32_t schedule;        /* split_kv == 0: 0 = automatic, 1 = balanced, 2 = one workgroup
                               per (sequence, kv head) (split_kv == 1)                       */
   int32_t max_pages_per_seq; /* plan hint for split_kv == 0: the most pages any sequence
@@ -153,7 +158,9 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *                  stream an equal share of all (sequence, kv head, page) units whatever
  *                  the lengths; sequences one workgroup covers are written directly, the
  *                  rest merged), or the split_kv == 1 pass when options.max_pages_per_seq
- *                  shows that one workgroup per pair fits that grid and is no longer.
+ *                  shows that one workgroup per pair fits that grid and is no longer
+ *                  (never for kv-head rows of <= 64 bytes, which stream faster with
+ *                  grouped kv heads in the balanced schedule).
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
  * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
  * functions behind src/attention.py:50-58. Differences: the caller allocates `out`
