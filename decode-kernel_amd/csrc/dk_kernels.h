@@ -1044,6 +1044,7 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
   }
 }
 
+
 // ---------------------------------------------------------------- pass 1, explicit split
 template <class T, int D, int G, int NW, bool MFMA, bool KV8>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_split(Pass1Args a) {
@@ -1178,47 +1179,55 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   int pg = u - (seq0 - base);
   if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
-  // head chunks are chunk-major (hc = chunk * hkv + kv head), so the chunks of one kv head
-  // are hkv workgroup ids apart: on one XCD when hkv is a multiple of kXcds
   const int kvh = hc % a.hkv, chunk = hc / a.hkv;
   const int qh0 = kvh * a.group + chunk * a.per;
   wv.hv = min(a.per, a.group - chunk * a.per);
   const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
+  auto page_at = [&](int idx) -> const uint8_t* {   // page of kv_indices[idx]
+    u32 pid = (u32)uniform(ld_const(a.indices, idx));
+    pid = pid < a.num_pages ? pid : 0u;
+    return kvh_base + (int64_t)pid * a.kv_p;
+  };
 
+  // Segment after segment; the next segment's q is loaded before the current segment's
+  // reduction and workgroup combine, so its memory latency overlaps that work. (Loading
+  // the next segment's first page there too measured slower: the page buffers then stay
+  // live across the combine and the kernel needs ~40 more registers.)
+  wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
   while (true) {
     const int n = min(np - pg, u_end - u);   // pages of this segment (>= 1)
-    wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
     wv.reset();
     const int valid_last = min(max(ld_const(a.last_len, b), 0), kPage);
-    const int first = pg, cur_seq0 = seq0, cur_np = np;
-    auto page = [&](int i) -> const uint8_t* {
-      u32 pid = (u32)uniform(ld_const(a.indices, cur_seq0 + first + i));
-      pid = pid < a.num_pages ? pid : 0u;
-      return kvh_base + (int64_t)pid * a.kv_p;
-    };
+    const int first = pg, cur_seq0 = seq0, cur_np = np, cur_b = b;
+    auto page = [&](int i) -> const uint8_t* { return page_at(cur_seq0 + first + i); };
     auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
     if (a.cap_out != 0.f)
       stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
     else
       stream_interleaved<D, KV8, false>(wv, NW, w, n, page, valid);
-    wv.reduce_rows();
 
-    const int start = seq0 - base;
-    const int nslots = (start + np - 1) / L - start / L + 1;
+    // the next non-empty sequence of the range, if any
+    bool more = false;
+    if (u + n < u_end) {
+      u += n;
+      do {
+        ++b;
+        seq0 = seq_begin(a, b);
+        np = max(seq_begin(a, b + 1), seq0) - seq0;
+      } while (np == 0 && b < a.batch - 1);
+      more = np > 0;   // np == 0 only for an invalid kv_indptr
+      pg = 0;
+    }
+    if (more) wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+
+    wv.reduce_rows();
+    const int start = cur_seq0 - base;
+    const int nslots = (start + cur_np - 1) / L - start / L + 1;
     combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
-                               a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
-                               ((int64_t)hc * (Wg + a.batch) + j + b) * G, 1, w,
+                               a.out + (int64_t)cur_b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
+                               ((int64_t)hc * (Wg + a.batch) + j + cur_b) * G, 1, w,
                                (int)(threadIdx.x & 63) + 64 * w);
-    if (u + n >= u_end) break;
-    // next non-empty sequence
-    u += n;
-    do {
-      ++b;
-      seq0 = seq_begin(a, b);
-      np = max(seq_begin(a, b + 1), seq0) - seq0;
-    } while (np == 0 && b < a.batch - 1);
-    if (np == 0) break;   // only for an invalid kv_indptr
-    pg = 0;
+    if (!more) break;
   }
 }
 
