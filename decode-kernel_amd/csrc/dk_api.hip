@@ -166,13 +166,20 @@ int run(Problem p, bool do_merge, void* stream) {
     } else {
       hp = grouped_kv_heads(p, pl, cus);
       const int64_t hint = p.opt.max_pages_per_seq;
+      const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
       if (hp > 1) {
         pl.waves = kGroupedWavesPerKvHead;
-      } else if (hint > 0 && !p.opt.waves_per_group && !p.opt.waves_per_cu &&
-                 pl.waves < kDefaultWavesPerGroupNarrow &&
+      } else if (hint > 0 && auto_waves && pl.waves < kDefaultWavesPerGroupNarrow &&
                  (int64_t)p.batch * hint * pl.pairs_per_seq <= (int64_t)kSmallUnitsPerCU * cus) {
         pl.waves = kDefaultWavesPerGroupNarrow;
         p.opt.waves_per_cu = kDefaultWavesPerCUNarrow;
+      } else if (hint > 0 && auto_waves && pl.waves > 1) {
+        // short sequences: when even the longest is at most 1/kShortSegments of a
+        // workgroup's page range, one wavefront per workgroup (same wavefronts per CU)
+        const int64_t groups = balanced_groups(p, pl, cus);
+        const int64_t per_chunk = std::max<int64_t>(groups / pl.pairs_per_seq, 1);
+        const int64_t range = (p.num_indices + per_chunk - 1) / per_chunk;
+        if (hint * kShortSegments <= range) pl.waves = 1;
       }
       pl.grid = balanced_groups(p, pl, cus, hp);
       waves_per_pair = (int)(pl.grid / (pl.pairs_per_seq / hp));

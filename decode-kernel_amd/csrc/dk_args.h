@@ -29,6 +29,13 @@ constexpr int kNarrowRowBytes = 128;
 // 4096, 32/8/128 fp16: 16.2 -> 15.1 and 23.3 -> 22.4 us; at 128 units per CU or 64 with
 // one sequence of 32768 tokens, two wavefronts stay faster)
 constexpr int kSmallUnitsPerCU = 32;
+// Balanced schedule over many short sequences (the plan hint: the longest is at most
+// 1/kShortSegments of a workgroup's page range, so a workgroup walks through several
+// sequences): one wavefront per workgroup, so a change of sequence needs no workgroup
+// combine (B=32*k, ctx 8192/k, 32/8/128 unless noted, balanced, NW=1 vs the default,
+// us: B=128 ctx 2048 166 vs 174, B=256 ctx 1024 176 vs 185, 64/8 B=256 ctx 1024 188 vs
+// 204, 16/4 93 vs 99; sequences of 1/2 to 1/4 of a range, or ragged, ~1 % either way)
+constexpr int kShortSegments = 4;
 // Balanced schedule over narrow rows: 4 neighbouring kv heads per workgroup, 2 wavefronts
 // each, one such workgroup per CU (64- and 128-byte row segments 512 B or 1 KB apart
 // stream far better when the segments of neighbouring heads are fetched together). B=32
