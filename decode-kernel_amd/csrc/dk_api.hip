@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "dk_args.h"
 #include "dk_decode.h"
@@ -25,13 +26,18 @@ int current_device(int device) {
 
 // Compute units of `device` (cached; the count never changes for a device).
 int cu_count(int device) {
-  static int cached[64] = {0};
+  // per-device cache; calls from several host threads may fill an entry concurrently
+  // (with the same value), hence atomics
+  static std::atomic<int> cached[64];
   if (device < 0) return -1;
-  if (device < 64 && cached[device] > 0) return cached[device];
+  if (device < 64) {
+    const int c = cached[device].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return -1;
-  if (device < 64) cached[device] = n;
+  if (device < 64) cached[device].store(n, std::memory_order_relaxed);
   return n;
 }
 
