@@ -21,14 +21,16 @@
 //   and B taken from the V registers as loaded. The next pages' loads are in flight while
 //   the current page is computed.
 //
-// Pass 1, explicit split (dk_pass1_split): one workgroup per (sequence, kv head, split)
-//   over ceil(N/S)-page ranges as in the reference partition kernel
+// Pass 1, explicit split (dk_pass1_split): one workgroup per (sequence, kv head chunk,
+//   split) over ceil(N/S)-page ranges as in the reference partition kernel
 //   (src/cuda_/attention_ext.cu:207-349); NW wavefronts take the split's pages round-robin
 //   and merge through LDS. With one split it writes the normalised output.
-// Pass 1, balanced (dk_pass1_balanced): a persistent grid of W wavefronts splits the
-//   linear (sequence, kv head, page) space into W equal ranges; a wavefront writes one
-//   partial per (sequence, kv head) segment it crosses, at slot wave + pair (unique,
-//   < W + pairs). Uniform or ragged, every wavefront streams the same number of pages.
+// Pass 1, balanced (dk_pass1_balanced): a persistent grid; the Wg workgroups of each head
+//   chunk split the linear (sequence, page) space into Wg equal ranges, so every
+//   workgroup streams the same number of pages, uniform or ragged. A workgroup writes the
+//   output of a sequence its range covers alone and one partial per other sequence it
+//   crosses (slot hc * (Wg + batch) + range + sequence: unique per head chunk). Over narrow
+//   rows a workgroup serves HP neighbouring kv heads of the same range.
 // Pass 2 (dk_merge_split / dk_merge_balanced): one wavefront per (sequence, q head)
 //   merges its partials with the log-sum-exp identity (reference decode_attn_reduce_kernel,
 //   src/cuda_/attention_ext.cu:363-406; contract src/layout.md:142-167).
