@@ -69,13 +69,15 @@ int explicit_split(const Problem& p, int device) {
 }
 
 // Wavefronts per compute unit the balanced schedule keeps resident. Two measured best on
-// MI355X at every decode shape tried with rows of 256 bytes or more and up to 4 q heads
-// per wavefront (each wavefront keeps two pages of loads in flight); four with narrower
-// rows (fp8 cache, or D = 64) or 8 q heads per wavefront (twice the work per page).
+// MI355X at every decode shape tried with rows of 256 bytes or more (each wavefront keeps
+// two pages of loads in flight), also with 8-16 heads on the MFMA q.k path; four with
+// narrower rows (fp8 cache, or D = 64) or 8 q heads on the VALU path (twice the work per
+// page).
 int waves_per_cu(const Problem& p, const Plan& pl, int hp = 1) {
   if (p.opt.waves_per_cu) return p.opt.waves_per_cu;
   if (hp > 1) return kGroupedWavesPerCU;
-  return p.narrow_rows() || pl.heads >= 8 ? kDefaultWavesPerCUNarrow : kDefaultWavesPerCU;
+  return p.narrow_rows() || (pl.heads >= 8 && !pl.mfma) ? kDefaultWavesPerCUNarrow
+                                                        : kDefaultWavesPerCU;
 }
 
 // Kv heads per workgroup of the balanced schedule (1 = one). Rows of at most

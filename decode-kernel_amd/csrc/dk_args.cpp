@@ -127,7 +127,7 @@ Plan make_plan(const Problem& p) {
   pl.pairs_per_seq = p.hkv * pl.chunks;
   const bool kv8 = p.opt.kv_dtype == DK_KV_FP8_E4M3;
   pl.waves = p.opt.waves_per_group ? p.opt.waves_per_group
-                                   : (p.narrow_rows() || pl.heads >= 8
+                                   : (p.narrow_rows() || (pl.heads >= 8 && !pl.mfma)
                                           ? kDefaultWavesPerGroupNarrow
                                           : kDefaultWavesPerGroup);
   pl.kv8 = kv8;

@@ -17,9 +17,12 @@ constexpr int kDefaultWavesPerCU = 2;
 constexpr int kDefaultWavesPerGroup = 2;
 // Rows of at most 128 bytes per kv head (fp8 at D <= 128, fp16/bf16 at D = 64) carry half
 // the bytes of a page for about the same per-token arithmetic, and 8 q heads per
-// wavefront double the arithmetic per byte: then one wavefront per SIMD is needed to keep
-// HBM busy (measured at B=32 ctx=8192 with 4 wavefronts per group vs 2: fp8 D=128 93 vs
-// 162 us; fp16 D=64 92 vs 122; 64 q / 8 kv heads at D=128 172 vs 254)
+// wavefront on the VALU q.k path double the arithmetic per byte: then one wavefront per
+// SIMD is needed to keep HBM busy (measured at B=32 ctx=8192 with 4 wavefronts per group
+// vs 2: fp8 D=128 93 vs 162 us; fp16 D=64 92 vs 122; 64 q / 8 kv heads at D=128, VALU,
+// 172 vs 254). On the MFMA q.k path (K staged through LDS) 8-16 heads keep the 2/2
+// defaults: 64/8 one pass 165.5 vs 169.9, balanced 168 vs 174; 28/4 balanced 92.6 vs
+// 97.5)
 constexpr int kDefaultWavesPerCUNarrow = 4;
 constexpr int kDefaultWavesPerGroupNarrow = 4;
 constexpr int kNarrowRowBytes = 128;

@@ -74,11 +74,12 @@ typedef struct {
                               MFMA q.k (up to 16 heads per wavefront) beyond and for fp8
                               at D = 256; 1 = MFMA, 2 = VALU; P.V always on MFMA         */
   int32_t waves_per_group; /* 0 = default: 2, or 4 with kv-head rows of <= 128 bytes (fp8,
-                              or D = 64) or 8+ heads per wavefront; the balanced schedule
-                              over such narrow rows serves 4 (or 2) neighbouring kv heads
-                              per workgroup with 2 wavefronts each, over small problems
-                              (plan hint) uses 4, and over many short sequences (plan
-                              hint) 1; else 1, 2 or 4 (then one kv head per workgroup)    */
+                              or D = 64) or 8 heads per wavefront on the VALU q.k path;
+                              the balanced schedule over such narrow rows serves 4 (or
+                              2) neighbouring kv heads per workgroup with 2 wavefronts
+                              each, over small problems (plan hint) uses 4, and over many
+                              short sequences (plan hint) 1; else 1, 2 or 4 (then one kv
+                              head per workgroup)                                         */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
                               schedules aim for (0 = default: 2, or 4 as above, 8 with
                               grouped kv heads)                                           */
