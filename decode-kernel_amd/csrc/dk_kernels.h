@@ -80,6 +80,11 @@ constexpr float kNegInf = -__builtin_inff();
 #ifndef DK_STAGE_K
 #define DK_STAGE_K 1
 #endif
+// 16-bit caches at D = 256 on the VALU q.k path: pages loaded straight into LDS
+// (stream_lds); a build may turn it off with DK_LDS_PAGES=0 for comparisons.
+#ifndef DK_LDS_PAGES
+#define DK_LDS_PAGES 1
+#endif
 
 // ---------------------------------------------------------------- launch arguments
 struct Pass1Args {
@@ -371,6 +376,10 @@ struct Wave {
   static constexpr int NCH = RB / 16;                     // 16-byte chunks per row
   static constexpr int SWZ = (NCH < 16 ? NCH : 16) - 1;
   static constexpr int STAGE_BYTES = STAGE ? kPage * RB : 0;
+  // LDS pages (stream_lds): a page slot holds the K rows then the V rows of one kv head,
+  // row-major, as the 1 KB buffer-load-to-LDS instructions write them
+  static constexpr int LDS_PAGE = 2 * kPage * RB;
+  static constexpr int LDS_LOADS = kPage * RB / 1024;   // instructions per K (or V) slice
 
   int r16, c;
   uint8_t* kst;           // STAGE: this wavefront's K tile in LDS (STAGE_BYTES)
@@ -464,6 +473,75 @@ struct Wave {
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) ld_buf<TW>(&vb[r * TW], rv, voff, r * tok_s);
+  }
+
+  // K and V rows of a page straight into the LDS slot: instruction i writes bytes
+  // i*1024.. of the slot's K (V) part, lane L bytes 16L..16L+15, i.e. token
+  // i*TPI + L/(64/TPI), 16-byte chunk L%(64/TPI) of its row (RB >= 256 bytes per row).
+  // live == false: a zero-extent descriptor (no memory access; the slot gets zeros).
+  __device__ __forceinline__ void lds_load_page(uint8_t* slot, const uint8_t* pg,
+                                                bool live = true) const {
+    static_assert(RB >= 256 && 1024 % RB == 0, "rows of 256, 512 or 1024 bytes");
+    constexpr int TPI = 1024 / RB, LPR = 64 / TPI;   // tokens per instruction, lanes per row
+    const u32 ext = live ? extent : 0u;
+    const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, ext);
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(pg + kv_v, ext);
+    const int lane = threadIdx.x & 63;
+    const u32 voff = (u32)(lane / LPR) * tok_s + (u32)(lane % LPR) * 16u;
+#pragma unroll
+    for (int i = 0; i < LDS_LOADS; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(slot + i * 1024), 16, (int)voff,
+          (int)(i * TPI * tok_s), 0, kBufNT);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void*)(slot + LDS_PAGE / 2 + i * 1024), 16,
+          (int)voff, (int)(i * TPI * tok_s), 0, kBufNT);
+    }
+  }
+
+  // A page of the LDS slot into the VALU layout's registers (tokens 4*r16 .. 4*r16+3,
+  // bytes c*RB/16 .. of each row): 16 ds_read_b128 and their lgkmcnt wait in one asm
+  // block (outputs early-clobber, so none shares a register with the address). Written in
+  // asm because a compiler-visible LDS read after the LDS-bound buffer loads makes hipcc
+  // wait for all of them (vmcnt(0)), which would serialise the ring; the waits for those
+  // loads are stream_lds's.
+  __device__ __forceinline__ void lds_read_page(const uint8_t* slot, u32 (&kb)[KB],
+                                                u32 (&vb)[VB]) const {
+    static_assert(KB == 32 && VB == 32 && RB == 512 && LDS_PAGE == 16384,
+                  "LDS pages: 16-bit caches at D = 256 (the offsets below)");
+    const u32 base = (u32)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(
+        slot + 4 * r16 * RB + c * (RB / 16));
+    u32x4 k[8], v[8];
+    asm volatile(
+        "ds_read_b128 %0, %16 offset:0\n\t"
+        "ds_read_b128 %1, %16 offset:16\n\t"
+        "ds_read_b128 %2, %16 offset:512\n\t"
+        "ds_read_b128 %3, %16 offset:528\n\t"
+        "ds_read_b128 %4, %16 offset:1024\n\t"
+        "ds_read_b128 %5, %16 offset:1040\n\t"
+        "ds_read_b128 %6, %16 offset:1536\n\t"
+        "ds_read_b128 %7, %16 offset:1552\n\t"
+        "ds_read_b128 %8, %16 offset:8192\n\t"
+        "ds_read_b128 %9, %16 offset:8208\n\t"
+        "ds_read_b128 %10, %16 offset:8704\n\t"
+        "ds_read_b128 %11, %16 offset:8720\n\t"
+        "ds_read_b128 %12, %16 offset:9216\n\t"
+        "ds_read_b128 %13, %16 offset:9232\n\t"
+        "ds_read_b128 %14, %16 offset:9728\n\t"
+        "ds_read_b128 %15, %16 offset:9744\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]),
+          "=&v"(k[6]), "=&v"(k[7]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]),
+          "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+        : "v"(base)
+        : "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kb[4 * i + e] = k[i][e];
+        vb[4 * i + e] = v[i][e];
+      }
   }
 
   // STAGE: the K words of a page as loaded (row layout) -> the MFMA layout, through LDS
@@ -942,6 +1020,46 @@ __device__ __forceinline__ void stream_ring(W& wv, int n, PageFn page, ValidFn v
   }
 }
 
+// Pages straight into LDS: a ring of DEPTH + 1 page slots per wavefront (`ring`,
+// DEPTH + 1 slots of W::LDS_PAGE bytes); while page k is read and computed, the loads of
+// the next DEPTH pages are in flight without holding registers. hipcc does not order the
+// loads' LDS writes before later LDS reads, so each step waits explicitly: the wavefront's
+// only vector-memory operations here are these loads, 2 * LDS_LOADS per page, so when
+// at most DEPTH pages' worth are outstanding, page k has landed. Steps past the last page
+// load with a zero-extent descriptor (no memory access) into a slot already consumed, so
+// every step waits for the same count; all are drained before returning.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int DEPTH, bool CAP, class W, class PageFn, class ValidFn>
+__device__ __forceinline__ void stream_lds(W& wv, uint8_t* ring, int n, PageFn page,
+                                           ValidFn valid) {
+  constexpr int NB = DEPTH + 1;
+  constexpr int PER = 2 * W::LDS_LOADS;
+#pragma unroll
+  for (int j = 0; j < DEPTH; ++j) wv.lds_load_page(ring + j * W::LDS_PAGE, page(min(j, n - 1)), j < n);
+  for (int k = 0; k < n; ++k) {
+    const int ld = k + DEPTH;
+    wv.lds_load_page(ring + (ld % NB) * W::LDS_PAGE, page(min(ld, n - 1)), ld < n);
+    wait_vmem<PER * DEPTH>();
+    u32 kb[W::KB], vb[W::VB];
+    wv.lds_read_page(ring + (k % NB) * W::LDS_PAGE, kb, vb);
+    wv.template consume<CAP>(kb, vb, valid(k));
+  }
+  wait_vmem<0>();
+}
+
+// Whether a kernel streams its pages through LDS (stream_lds): 16-bit caches at D = 256
+// on the VALU q.k path, with at most 2 wavefronts per workgroup (LDS: 64 KB each).
+constexpr int kLdsDepth = 3;
+template <int D, bool KV8, bool MFMA, int NW>
+constexpr bool lds_pages() {
+  return DK_LDS_PAGES && D == 256 && !KV8 && !MFMA && NW <= 2;
+}
+
 // ---------------------------------------------------------------- workgroup combine
 // LDS scratch for merging the NW wavefronts of a workgroup.
 template <int G, int D, int NW>
@@ -1027,16 +1145,19 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
   }
 }
 
-// Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages.
-template <int D, bool KV8, bool CAP, class WV, class PageFn, class ValidFn>
+// Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages
+// (through its LDS ring when LDS is set).
+template <int D, bool KV8, bool CAP, bool LDS = false, class WV, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n, PageFn page,
-                                                   ValidFn valid) {
+                                                   ValidFn valid, uint8_t* ring = nullptr) {
   const int nk = n > w ? (n - w + NW - 1) / NW : 0;
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
     constexpr int depth = prefetch_depth<D, KV8>();
-    if constexpr (depth <= 2) {
+    if constexpr (LDS) {
+      stream_lds<kLdsDepth, CAP>(wv, ring, nk, pk, vk);
+    } else if constexpr (depth <= 2) {
       u32 ka[WV::KB], va[WV::VB];
       wv.load_page(ka, va, pk(0));
       stream_pages<depth, CAP>(wv, ka, va, nk, pk, vk);
@@ -1044,6 +1165,7 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
       stream_ring<depth, CAP>(wv, nk, pk, vk);
     }
   }
+  (void)ring;
 }
 
 
@@ -1053,10 +1175,14 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
   __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? NW * WV::STAGE_BYTES : 16];
+  constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW>();
+  constexpr int RING = (kLdsDepth + 1) * WV::LDS_PAGE;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? NW * RING : 16];
   WV wv;
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
   wv.kst = kst + w * WV::STAGE_BYTES;
+  uint8_t* const wring = ring + (LDSP ? w * RING : 0);
 
   // workgroup -> (head chunk, kv head, split, sequence). The head chunks of one (sequence,
   // kv head, split) read the same pages: they are placed kXcds workgroup ids apart (the
@@ -1109,9 +1235,9 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
     return pg == npages - 1 ? enc_last : (pg == lo_page ? enc_lo : kPage);
   };
   if (a.cap_out != 0.f)
-    stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
+    stream_interleaved<D, KV8, true, LDSP>(wv, NW, w, n, page, valid, wring);
   else
-    stream_interleaved<D, KV8, false>(wv, NW, w, n, page, valid);
+    stream_interleaved<D, KV8, false, LDSP>(wv, NW, w, n, page, valid, wring);
   wv.reduce_rows();
   combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
@@ -1135,11 +1261,15 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> smh[HP];
   __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? HP * NW * WV::STAGE_BYTES : 16];
+  constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW * HP>();
+  constexpr int RING = (kLdsDepth + 1) * WV::LDS_PAGE;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? HP * NW * RING : 16];
   WV wv;
   wv.init(a);
   const int wa = uniform(threadIdx.x >> 6);   // wavefront of the workgroup
   const int hl = wa / NW, w = wa % NW;        // its kv head among the HP, its rank there
   wv.kst = kst + wa * WV::STAGE_BYTES;
+  uint8_t* const wring = ring + (LDSP ? wa * RING : 0);
   auto& sm = smh[hl];
   // workgroup -> (HP head chunks hc, range j): its NW * HP wavefronts serve HP consecutive
   // kv heads (same head chunk) of the same pages, so the HP row segments of each token are
@@ -1204,9 +1334,9 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     auto page = [&](int i) -> const uint8_t* { return page_at(cur_seq0 + first + i); };
     auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
     if (a.cap_out != 0.f)
-      stream_interleaved<D, KV8, true>(wv, NW, w, n, page, valid);
+      stream_interleaved<D, KV8, true, LDSP>(wv, NW, w, n, page, valid, wring);
     else
-      stream_interleaved<D, KV8, false>(wv, NW, w, n, page, valid);
+      stream_interleaved<D, KV8, false, LDSP>(wv, NW, w, n, page, valid, wring);
 
     // the next non-empty sequence of the range, if any
     bool more = false;
