@@ -1054,7 +1054,11 @@ __device__ __forceinline__ void stream_lds(W& wv, uint8_t* ring, int n, PageFn p
 
 // Whether a kernel streams its pages through LDS (stream_lds): 16-bit caches at D = 256
 // on the VALU q.k path, with at most 2 wavefronts per workgroup (LDS: 64 KB each).
-constexpr int kLdsDepth = 3;
+// (a build may set another depth with DK_LDS_DEPTH; 2 measured the same as 3 at D=256)
+#ifndef DK_LDS_DEPTH
+#define DK_LDS_DEPTH 3
+#endif
+constexpr int kLdsDepth = DK_LDS_DEPTH;
 template <int D, bool KV8, bool MFMA, int NW>
 constexpr bool lds_pages() {
   return DK_LDS_PAGES && D == 256 && !KV8 && !MFMA && NW <= 2;
