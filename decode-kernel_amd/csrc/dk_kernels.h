@@ -19,7 +19,8 @@
 //   times per split instead of every page. P.V runs on v_mfma_f32_16x16x16_{f16,bf16}
 //   with p split into hi + lo parts of the element type (weights exact to 2^-22 / 2^-16)
 //   and B taken from the V registers as loaded. The next pages' loads are in flight while
-//   the current page is computed.
+//   the current page is computed: in registers, or, for 16-bit caches at D = 256 on the
+//   VALU q.k path, straight into a per-wavefront LDS ring (stream_lds).
 //
 // Pass 1, explicit split (dk_pass1_split): one workgroup per (sequence, kv head chunk,
 //   split) over ceil(N/S)-page ranges as in the reference partition kernel
