@@ -123,6 +123,8 @@ CASES = [
     (3, [1, 300, 40], 14, 2, 128, torch.bfloat16, "permuted"),     # 7 q heads per kv head
     (2, [900, 77], 128, 4, 128, torch.float16, "permuted"),       # 2 head chunks of 16
     (3, [513, 1, 64], 16, 4, 64, torch.bfloat16, "freelist"),     # 64-byte rows
+    (3, [400, 9, 130], 24, 6, 128, torch.float16, "freelist"),    # 3 groups of 2 kv heads
+    (2, [333, 65], 48, 12, 128, torch.bfloat16, "permuted"),      # 3 groups of 4 kv heads
 ]
 
 

@@ -371,7 +371,10 @@ PADDED_GROUPS = [(128, 3, 1), (128, 10, 2), (64, 12, 2), (128, 14, 2), (128, 20,
                  (64, 40, 1), (256, 17, 1),
                  # narrow rows with several head chunks: the balanced schedule's grouped kv
                  # heads (2 and 4 per workgroup) with the chunks of a unit 8 ids apart
-                 (64, 64, 2), (64, 96, 4)]
+                 (64, 64, 2), (64, 96, 4),
+                 # kv-head counts that are not a power of two: 3 groups of 2 (6 kv heads)
+                 # and 3 groups of 4 (12 kv heads) per sequence
+                 (64, 24, 6), (64, 36, 12)]
 
 
 @pytest.mark.parametrize("d,hq,hkv", PADDED_GROUPS)
