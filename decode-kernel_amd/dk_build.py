@@ -50,10 +50,12 @@ RESOURCE_FLAG = "-Rpass-analysis=kernel-resource-usage"
 
 def _filter(out: str) -> str:
     # hipcc's host pass reports the device-only feature flag as unknown; the resource
-    # remarks are parsed separately. Drop both from what is echoed.
+    # remarks are parsed separately. Drop both, and the source lines the compiler echoes
+    # under each remark (" 1179 | ..."), from what is echoed.
     return "\n".join(l for l in out.splitlines()
                      if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l
-                     and not l.startswith(("  ", "In file included from")))
+                     and not l.startswith(("  ", "In file included from"))
+                     and not re.match(r"\s*\d*\s*\|", l))
 
 
 def kernel_resources(out: str) -> dict:
