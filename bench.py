@@ -55,7 +55,7 @@ def parse_args():
     ap.add_argument("--schedule", type=int, default=0,
                     help="split_kv 0: 0 automatic, 1 balanced, 2 one pass")
     ap.add_argument("--qk-path", type=int, default=0, help="0 default, 1 MFMA, 2 VALU")
-    ap.add_argument("--waves", type=int, default=0, help="wavefronts per workgroup (0 = 1)")
+    ap.add_argument("--waves", type=int, default=0, help="wavefronts per workgroup (0 = the library's default)")
     ap.add_argument("--waves-per-cu", type=int, default=0,
                     help="balanced schedule: wavefronts per CU (0 = default)")
     ap.add_argument("--batch", type=int, default=32)
