@@ -14,8 +14,9 @@ host sync, so host launch overhead is hidden behind it and the events measure GP
 The W warm-up steps are such flush + call steps too, after an untimed settling phase of
 the same steps (0.3 s) that lets the GPU clocks reach their steady state.
 
-Other shapes (--num-q-heads, --num-kv-heads, --head-dim, --batch, --ctx, --kv-dtype) are
-for profiling; the JSON's config names the workload measured.
+Other shapes (--num-q-heads, --num-kv-heads, --head-dim, --batch, --ctx, --kv-dtype, and
+--ragged-min for config 4's ragged mix) are for profiling; the JSON's config names the
+workload measured.
 
 Prints one JSON line. `value` is achieved algorithmic HBM bandwidth in TB/s
 (bytes of the reference's model, bench/microbench_cuda.py:114-121, plus page tables,
@@ -71,6 +72,11 @@ def parse_args():
                     help="cache flush before each step: fill (write) or sum (read) 1 GiB")
     ap.add_argument("--page-table", default="permuted", choices=["permuted", "contiguous"],
                     help="page-table shape of the synthetic pool (the metric uses permuted)")
+    ap.add_argument("--ragged-min", type=int, default=0, metavar="TOKENS",
+                    help="ragged mix (config 4 with --batch 128 --ragged-min 128): "
+                         "per-sequence lengths uniform in [TOKENS, ctx] (seeded), pages "
+                         "drawn from a shuffled free list of 65536 pages, q scaled by "
+                         "1/sqrt(head_dim)")
     ap.add_argument("--no-plan-hint", action="store_true",
                     help="do not pass the host-side max_pages_per_seq plan hint")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -121,7 +127,9 @@ def cpu_baseline(q, kv, indptr, ids, last, out, sample):
             times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     err = float(np.abs(out[subset].float().cpu().numpy() - want[subset]).max())
-    per_call_us = t / len(subset) * q.shape[0] * 1e6
+    # scaled to the whole batch by pages (the sample's share of the work, also when ragged)
+    pages = lambda bs: sum(max(int(ipn[b + 1]) - int(ipn[b]), 0) for b in bs)  # noqa: E731
+    per_call_us = t * pages(range(q.shape[0])) / max(pages(subset), 1) * 1e6
     return per_call_us, blas, len(subset), err
 
 
@@ -145,9 +153,19 @@ def main():
     B, ctx, hq, hkv, d = args.batch, args.ctx, args.num_q_heads, args.num_kv_heads, args.head_dim
     # the recorded rocprofv3 traffic belongs to the metric's workload only
     metric_workload = ((B, ctx, hq, hkv, d) == (32, 8192, 32, 8, 128)
-                       and args.page_table == "permuted")
-    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-        B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table=args.page_table, seed=1)
+                       and args.page_table == "permuted" and not args.ragged_min)
+    if args.ragged_min:
+        if not 1 <= args.ragged_min <= ctx:
+            sys.exit("bench.py: --ragged-min must be in [1, ctx]")
+        lens = layout.ragged_lengths(B, args.ragged_min, ctx, seed=4)
+        pool = max(65536, sum((n + 15) // 16 for n in lens))
+        q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+            B, lens, hq, hkv, d, dtype=dtype, device=dev, page_table="freelist",
+            pool_pages=pool, seed=1, q_scale=d ** -0.5)
+    else:
+        lens = ctx
+        q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+            B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table=args.page_table, seed=1)
     kv_ref = kv                        # the cache's values for the CPU baseline
     kv8 = args.kv_dtype == "fp8"
     if kv8:
@@ -167,7 +185,7 @@ def main():
         kv_ref = table[codes.long()]
         kv = codes.view(attention.KV_FP8)
     split = attention.resolve_split(args.split)
-    nbytes = layout.attention_bytes(B, ctx, hq, hkv, d, kv_elem_bytes=1 if kv8 else 0)
+    nbytes = layout.attention_bytes(B, lens, hq, hkv, d, kv_elem_bytes=1 if kv8 else 0)
     out = torch.empty_like(q)
     ws_bytes = dk_lib.workspace_bytes(B, hq, hkv, d, split)
     p_total = dk_lib.partials_layout(B, hq, d, split)[3] if split else ws_bytes
@@ -244,16 +262,20 @@ def main():
     mfma_qk = args.qk_path == 1 or (args.qk_path == 0 and (hq // hkv > 4 or (kv8 and d >= 256)))
     qk_name = "mfma" if mfma_qk else "valu"
 
+    ctx_label = f"U[{args.ragged_min},{ctx}]" if args.ragged_min else ctx
+    table_label = "free-list" if args.ragged_min else args.page_table
     rec = {
         "metric": METRIC, "value": round(nbytes / (p50 * 1e-6) / 1e12, 4), "unit": "TB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
-        "config": {"workload": f"paged decode attention B={B} ctx={ctx} Hq={hq} Hkv={hkv} "
-                               f"D={d} {args.dtype}{' (fp8 E4M3 cache)' if kv8 else ''} "
-                               f"page_size=16 {args.page_table} pages",
+        "config": {"workload": f"paged decode attention B={B} ctx={ctx_label} Hq={hq} "
+                               f"Hkv={hkv} D={d} {args.dtype}"
+                               f"{' (fp8 E4M3 cache)' if kv8 else ''} "
+                               f"page_size=16 {table_label} pages",
                    "kv_dtype": "fp8_e4m3" if kv8 else args.dtype,
-                   "batch": B, "context_length": ctx, "num_q_heads": hq, "num_kv_heads": hkv,
+                   "batch": B, "context_length": ctx_label, "num_q_heads": hq,
+                   "num_kv_heads": hkv,
                    "head_dim": d, "page_size": 16,
                    "split_kv": split,
                    "schedule": {1: "one pass"}.get(eff, "balanced + merge" if eff == 0
@@ -276,7 +298,8 @@ def main():
             "value": round(us, 1), "unit": "us/call", "cores": cores, "kind": "port",
             "tb_s": round(nbytes / (us * 1e-6) / 1e12, 5),
             "sample": f"numpy fp32 restatement of reference_attention_paged on {n} of {B} "
-                      f"sequences (full ctx), median of 3, scaled to the whole batch"}
+                      f"whole sequences, median of 3, scaled to the whole batch by "
+                      f"pages"}
         rec["max_abs_err_vs_fp32"] = err
     print(json.dumps(rec), flush=True)
     if args.calibration_copy > 0:
