@@ -11,6 +11,8 @@ one wavefront per balanced workgroup. Bar: max-abs 1e-2 and mean-abs 1e-3 agains
 fp32 oracle on the values the kernel reads (the dequantised cache for fp8).
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -58,7 +60,8 @@ def _case(i: int):
     return c
 
 
-CASES = [_case(i) for i in range(96)]
+# 96 cases by default; DK_RANDOM_CASES=N runs the first N seeds of the same generator
+CASES = [_case(i) for i in range(int(os.environ.get("DK_RANDOM_CASES", "96")))]
 
 
 @pytest.mark.parametrize("i", range(len(CASES)))
