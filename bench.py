@@ -85,7 +85,10 @@ def parse_args():
                          "known traffic that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-sample", type=int, default=16,
                     help="sequences of the workload the CPU baseline computes")
-    return ap.parse_args()
+    a = ap.parse_args()
+    if a.ragged_min and not 1 <= a.ragged_min <= a.ctx:
+        ap.error(f"--ragged-min must be in [1, ctx={a.ctx}], got {a.ragged_min}")
+    return a
 
 
 def read_traffic(kv_dtype="same"):
@@ -155,8 +158,6 @@ def main():
     metric_workload = ((B, ctx, hq, hkv, d) == (32, 8192, 32, 8, 128)
                        and args.page_table == "permuted" and not args.ragged_min)
     if args.ragged_min:
-        if not 1 <= args.ragged_min <= ctx:
-            sys.exit("bench.py: --ragged-min must be in [1, ctx]")
         lens = layout.ragged_lengths(B, args.ragged_min, ctx, seed=4)
         pool = max(65536, sum((n + 15) // 16 for n in lens))
         q, kv, indptr, ids, last, _ = layout.synthesize_paged(

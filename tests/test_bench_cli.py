@@ -1,4 +1,5 @@
-"""bench.py's contract on the CPU: the one-GPU limit and the recorded HBM traffic it reports."""
+"""bench.py's contract on the CPU: the one-GPU limit, argument checks, and the recorded
+HBM traffic it reports."""
 import subprocess
 import sys
 from pathlib import Path
@@ -16,6 +17,14 @@ def test_more_than_one_gpu_is_refused_with_a_message():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+    assert r.stdout == ""
+
+
+def test_ragged_lengths_beyond_the_context_are_refused_before_any_gpu_work():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--ragged-min", "9000"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "--ragged-min must be in [1, ctx=8192]" in r.stderr
     assert r.stdout == ""
 
 
