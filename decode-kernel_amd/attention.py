@@ -257,8 +257,8 @@ def decode_attention(
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
     """
     kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
-    if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale == 0.0):
-        _fail(f"sm_scale must be finite and non-zero, got {sm_scale}")
+    if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale <= 0.0):
+        _fail(f"sm_scale must be finite and > 0, got {sm_scale}")
     kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
     cap = _logit_cap(logit_cap)
     win = _window(window)

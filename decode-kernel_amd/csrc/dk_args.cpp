@@ -78,12 +78,16 @@ int64_t split_rows(int32_t batch, int32_t hq, int32_t split) {
 }
 
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) {
-  // enough rows for either q.k path (the path is an option of the call)
+  // Enough rows for either q.k path (the path is an option of the call). Pass 1 writes
+  // slot rows (hc * (Wg + batch) + j + b) * heads for head chunk hc < HC = hkv * chunks and
+  // range j < Wg, so it needs HC * (Wg + batch) * heads rows. The grid holds at most
+  // kMaxWaves wavefronts, i.e. HC * Wg <= kMaxWaves, except when HC alone exceeds that
+  // and the grid falls back to one range per head chunk (Wg = 1): hence max(kMaxWaves, HC).
   int64_t rows = 0;
   for (bool mfma : {false, true}) {
     const HeadChunks h = head_chunks(hq / hkv, head_dim, mfma);
-    const int64_t pairs = (int64_t)batch * hkv * h.chunks;
-    rows = std::max<int64_t>(rows, (kMaxWaves + pairs) * h.heads);
+    const int64_t hc = (int64_t)hkv * h.chunks;
+    rows = std::max<int64_t>(rows, (std::max<int64_t>(kMaxWaves, hc) + batch * hc) * h.heads);
   }
   return rows;
 }
@@ -173,8 +177,11 @@ int validate(const Problem& p) {
   if (o.max_pages_per_seq < 0)
     return set_error(DK_EINVAL, "options.max_pages_per_seq must be >= 0; got %d",
                      o.max_pages_per_seq);
-  if (!std::isfinite(o.sm_scale))
-    return set_error(DK_EINVAL, "options.sm_scale must be finite (0 = 1/sqrt(head_dim))");
+  // a negative scale would turn the kernels' -inf masking of dead tokens into +inf
+  if (!std::isfinite(o.sm_scale) || o.sm_scale < 0.f)
+    return set_error(DK_EINVAL,
+                     "options.sm_scale must be finite and >= 0 (0 = 1/sqrt(head_dim)); got %g",
+                     (double)o.sm_scale);
   if (o.kv_dtype != DK_KV_SAME && o.kv_dtype != DK_KV_FP8_E4M3)
     return set_error(DK_EINVAL, "options.kv_dtype must be DK_KV_SAME or DK_KV_FP8_E4M3; got %d",
                      o.kv_dtype);

@@ -126,7 +126,7 @@ Plan make_plan(const Problem& p);
 void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,
                           size_t* off_l, size_t* total);
 // Rows of partials each mode writes: explicit split S -> batch*hq*S; balanced ->
-// (kMaxWaves + batch*pairs_per_seq) * heads.
+// (max(kMaxWaves, pairs_per_seq) + batch*pairs_per_seq) * heads.
 int64_t split_rows(int32_t batch, int32_t hq, int32_t split);
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim);
 // Workspace of dk_decode_attention: split 1 -> 0, split > 1 -> explicit partials,

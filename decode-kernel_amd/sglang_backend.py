@@ -18,12 +18,17 @@ Two entry styles are provided:
 An fp8_e4m3 KV cache (SGLang stores it as uint8 and hands out float8_e4m3fn views) is
 read with the layer's k_scale / v_scale, which the pool also divides by when it writes.
 
-Registration mirrors the reference (:112-137): `register_backend()` or the environment
-variable SGLANG_ATTENTION_BACKEND=split_kv_hip. SGLang is imported lazily; without it the
-class derives from a stub so that the module imports (and is tested) anywhere.
+Registration (the reference's entry points, integration/sglang_backend.py:112-137):
+`register_backend()` adds the class under BACKEND_NAME to SGLang's attention-backend table,
+through `register_attention_backend` where SGLang exports it and into the module's
+`_BACKEND_REGISTRY` dict on versions that only have the dict; importing this module with
+SGLANG_ATTENTION_BACKEND=split_kv_hip does it once. SGLang is looked up lazily; without it
+the backend class has a plain base, so the module imports (and is tested) anywhere.
 """
 from __future__ import annotations
 
+import importlib
+import logging
 import math
 import os
 from dataclasses import dataclass
@@ -42,20 +47,31 @@ PAGE_SIZE = 16
 DEFAULT_SPLIT_KV = int(os.environ.get("SPLIT_KV", "0"))
 
 
-def _import_sglang_base():
+_log = logging.getLogger(__name__)
+
+# Where SGLang keeps its attention-backend base class and its backend table, newest
+# layout first (the class moved into base_attn_backend in later releases).
+_SGLANG_BASE_MODULES = ("sglang.srt.layers.attention.base_attn_backend",
+                        "sglang.srt.layers.attention")
+_SGLANG_REGISTRY_MODULE = "sglang.srt.layers.attention"
+
+
+def _optional_module(path: str):
+    """The module at `path`, or None when it (or SGLang itself) cannot be imported."""
     try:
-        from sglang.srt.layers.attention.base_attn_backend import AttentionBackend
-        return AttentionBackend
+        return importlib.import_module(path)
     except ImportError:
-        pass
-    try:
-        from sglang.srt.layers.attention import AttentionBackend
-        return AttentionBackend
-    except ImportError:
-        class AttentionBackend:  # stand-in when SGLang is not installed
-            def forward(self, *a, **kw):
-                raise NotImplementedError
-        return AttentionBackend
+        return None
+
+
+def _backend_base() -> type:
+    """SGLang's AttentionBackend when SGLang is importable, else `object`: the adapter
+    defines every method it is called through, so it needs nothing from the base."""
+    for path in _SGLANG_BASE_MODULES:
+        base = getattr(_optional_module(path), "AttentionBackend", None)
+        if isinstance(base, type):
+            return base
+    return object
 
 
 @dataclass
@@ -67,7 +83,7 @@ class DecodeMetadata:
     max_pages_per_seq: int          # plan hint (0 = unknown)
 
 
-class SplitKVHipBackend(_import_sglang_base()):
+class SplitKVHipBackend(_backend_base()):
     """Decode attention on the HIP split-KV kernel; prefill on PyTorch SDPA."""
 
     def __init__(self, model_runner=None, split_kv: Optional[int] = None):
@@ -78,6 +94,14 @@ class SplitKVHipBackend(_import_sglang_base()):
         self._scales: dict = {}           # layer_id -> (k_scale, v_scale) of an fp8 pool
         self._graph_tables = None         # persistent page tables for HIP graph replay
         self._graph_max_bs = 0
+        self._graph_workspace: Optional[torch.Tensor] = None   # captured calls' scratch
+        self._retired_graph_workspaces: list = []   # outgrown, still read by old graphs
+        self.page_size = _server_page_size(model_runner)
+        if self.page_size not in (None, PAGE_SIZE):
+            raise ValueError(
+                f"{BACKEND_NAME} reads the token pool as 16-token pages (page id = slot // "
+                f"16), so SGLang must run with page_size 16; this server has page_size "
+                f"{self.page_size} (start it with --page-size 16)")
 
     @classmethod
     def name(cls) -> str:
@@ -273,14 +297,40 @@ class SplitKVHipBackend(_import_sglang_base()):
         return kb[:pages * PAGE_SIZE].view(shape), vb[:pages * PAGE_SIZE].view(shape)
 
     def _workspace_for(self, q, hkv):
-        need = attention.dk_lib.workspace_bytes(q.shape[0], q.shape[1], hkv, q.shape[2],
-                                                attention.resolve_split(self.split_kv))
+        """Scratch for one decode call. Eager calls share one buffer that grows with the
+        batch. A call under graph capture gets the graph workspace instead: its address is
+        baked into the graph and every replay writes there, so it is sized once for the
+        graph state's largest batch, never handed to eager calls, and never freed while
+        the backend lives (one outgrown by a later capture is kept too)."""
+        split = attention.resolve_split(self.split_kv)
+        need = attention.dk_lib.workspace_bytes(q.shape[0], q.shape[1], hkv, q.shape[2], split)
         if need == 0:
             return None
+        if torch.cuda.is_current_stream_capturing():
+            ws = self._graph_workspace
+            if ws is None or ws.numel() < need or ws.device != q.device:
+                if ws is not None:
+                    self._retired_graph_workspaces.append(ws)
+                most = attention.dk_lib.workspace_bytes(
+                    max(q.shape[0], self._graph_max_bs), q.shape[1], hkv, q.shape[2], split)
+                ws = self._graph_workspace = torch.empty(max(need, most), dtype=torch.uint8,
+                                                         device=q.device)
+            return ws
         ws = self._workspace
         if ws is None or ws.numel() < need or ws.device != q.device:
             ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
         return ws
+
+
+def _server_page_size(model_runner) -> Optional[int]:
+    """Token-pool page size of the SGLang server (ModelRunner.page_size, else its
+    server_args.page_size); None when the runner does not say."""
+    if model_runner is None:
+        return None
+    ps = getattr(model_runner, "page_size", None)
+    if ps is None:
+        ps = getattr(getattr(model_runner, "server_args", None), "page_size", None)
+    return None if ps is None else int(ps)
 
 
 def _window(layer) -> Optional[int]:
@@ -303,26 +353,45 @@ def _scale(layer, d) -> Optional[float]:
     return float(s)
 
 
-def register_backend() -> bool:
-    """Register with SGLang's backend registry (reference :112-137). Returns success."""
-    try:
-        from sglang.srt.layers.attention import register_attention_backend
-        register_attention_backend(BACKEND_NAME, SplitKVHipBackend)
-        print(f"[{BACKEND_NAME}] Backend registered with SGLang.")
-        return True
-    except ImportError:
-        print(f"[{BACKEND_NAME}] WARNING: sglang not installed; backend registration skipped.")
+def register_backend(registry=None) -> bool:
+    """Make SplitKVHipBackend selectable under BACKEND_NAME (the reference's
+    register_backend, integration/sglang_backend.py:112-137). `registry` is the module
+    holding SGLang's backend table (default: sglang.srt.layers.attention). Uses its
+    `register_attention_backend(name, cls)` when present, else sets the entry of its
+    `_BACKEND_REGISTRY` dict. Returns whether the backend is now registered; never raises
+    for a missing or unfamiliar SGLang (the outcome is logged)."""
+    if registry is None:
+        registry = _optional_module(_SGLANG_REGISTRY_MODULE)
+    if registry is None:
+        _log.warning("%s: SGLang is not importable, so there is no backend table to add "
+                     "the decode backend to", BACKEND_NAME)
         return False
-    except AttributeError:
-        try:
-            import sglang.srt.layers.attention as attn_mod
-            attn_mod._BACKEND_REGISTRY[BACKEND_NAME] = SplitKVHipBackend
-            print(f"[{BACKEND_NAME}] Backend injected into registry (legacy path).")
-            return True
-        except Exception as e:  # noqa: BLE001 - report and carry on, as the reference does
-            print(f"[{BACKEND_NAME}] Registration failed: {e}")
+    name = getattr(registry, "__name__", type(registry).__name__)
+    hook = getattr(registry, "register_attention_backend", None)
+    table = getattr(registry, "_BACKEND_REGISTRY", None)
+    try:
+        if callable(hook):
+            hook(BACKEND_NAME, SplitKVHipBackend)
+            how = "register_attention_backend"
+        elif isinstance(table, dict):
+            table[BACKEND_NAME] = SplitKVHipBackend
+            how = "_BACKEND_REGISTRY"
+        else:
+            _log.warning("%s: %s has neither register_attention_backend nor a "
+                         "_BACKEND_REGISTRY dict; not registered", BACKEND_NAME, name)
             return False
+    except Exception as exc:  # noqa: BLE001 - SGLang's own checks: log them, do not fail import
+        _log.warning("%s: %s refused the backend: %s", BACKEND_NAME, name, exc)
+        return False
+    _log.info("%s: added to %s through %s", BACKEND_NAME, name, how)
+    return True
 
 
-if os.environ.get("SGLANG_ATTENTION_BACKEND") == BACKEND_NAME:
-    register_backend()
+def _register_if_selected() -> None:
+    """SGLANG_ATTENTION_BACKEND=split_kv_hip at import selects this backend (the
+    reference's environment switch)."""
+    if os.environ.get("SGLANG_ATTENTION_BACKEND", "").strip() == BACKEND_NAME:
+        register_backend()
+
+
+_register_if_selected()

@@ -54,6 +54,18 @@ def test_workspace_and_partials_layout():
         dk_lib.partials_layout(1, 1, 64, 0)
 
 
+
+@pytest.mark.parametrize("batch,hkv", [(1, 4096), (3, 2049), (2, 8192), (5, 2048)])
+def test_balanced_workspace_covers_every_slot_with_many_head_chunks(batch, hkv):
+    # Pass 1 of the balanced schedule writes slot rows (hc*(Wg + batch) + j + b)*heads for
+    # head chunk hc < HC and range j < Wg. With more head chunks than kMaxWaves = 2048 the
+    # grid falls back to one range per head chunk (Wg = 1), so the last slot row is
+    # HC*(1 + batch)*heads - 1: the workspace must hold at least that many rows.
+    d, heads = 64, 1                      # MHA: one q head per kv head
+    rows = hkv * (1 + batch) * heads
+    o, m, l, total = dk_lib.partials_layout(1, rows, d, 1)   # `rows` rows of D + m + l
+    assert dk_lib.workspace_bytes(batch, hkv, hkv, d, 0) >= total
+
 def _call(lib, **kw):
     """dk_decode_attention_ex with a valid metric-shaped problem, overridden by kw.
     Pointers are fake non-NULL 256-aligned values: validation rejects before any use."""
@@ -101,6 +113,9 @@ def _call(lib, **kw):
     (dict(opts=dk_lib.options(schedule=3)), dk_lib.DK_EINVAL, "schedule"),
     (dict(opts=dk_lib.options(kv_dtype=1)), dk_lib.DK_EINVAL, "kv_dtype"),
     (dict(opts=dk_lib.options(logit_cap=-1.0)), dk_lib.DK_EINVAL, "logit_cap"),
+    # a negative scale would flip the kernels' -inf masking of dead tokens to +inf
+    (dict(opts=dk_lib.options(sm_scale=-0.1)), dk_lib.DK_EINVAL, "sm_scale"),
+    (dict(opts=dk_lib.options(sm_scale=float("inf"))), dk_lib.DK_EINVAL, "sm_scale"),
     (dict(opts=dk_lib.options(logit_cap=float("nan"))), dk_lib.DK_EINVAL, "logit_cap"),
     (dict(opts=dk_lib.options(k_scale=2.0)), dk_lib.DK_EINVAL, "fp8 cache only"),
     (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3, v_scale=-1.0)),

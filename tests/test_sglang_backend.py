@@ -32,9 +32,50 @@ def test_backend_imports_and_names_without_sglang():
     assert sglang_backend.SplitKVHipBackend().split_kv == sglang_backend.DEFAULT_SPLIT_KV
 
 
-def test_register_backend_reports_missing_sglang(capsys):
-    assert sglang_backend.register_backend() is False
-    assert "sglang not installed" in capsys.readouterr().out
+def test_register_backend_reports_missing_sglang(caplog):
+    with caplog.at_level("WARNING"):
+        assert sglang_backend.register_backend() is False
+    assert "SGLang is not importable" in caplog.text
+
+
+def test_register_backend_uses_the_registration_hook():
+    from types import SimpleNamespace
+    seen = {}
+    mod = SimpleNamespace(__name__="fake_attention",
+                          register_attention_backend=lambda n, c: seen.update({n: c}),
+                          _BACKEND_REGISTRY={})
+    assert sglang_backend.register_backend(mod) is True
+    assert seen == {"split_kv_hip": sglang_backend.SplitKVHipBackend}
+    assert mod._BACKEND_REGISTRY == {}          # the hook wins over the dict
+
+
+def test_register_backend_falls_back_to_the_registry_dict():
+    from types import SimpleNamespace
+    mod = SimpleNamespace(__name__="fake_attention", _BACKEND_REGISTRY={"fa3": object})
+    assert sglang_backend.register_backend(mod) is True
+    assert mod._BACKEND_REGISTRY["split_kv_hip"] is sglang_backend.SplitKVHipBackend
+    assert sglang_backend.register_backend(SimpleNamespace(__name__="bare")) is False
+
+    def refuse(name, cls):
+        raise KeyError(name)
+    assert sglang_backend.register_backend(
+        SimpleNamespace(__name__="strict", register_attention_backend=refuse)) is False
+
+
+@pytest.mark.parametrize("runner,ok", [
+    (dict(page_size=16), True), (dict(page_size=1), False), (dict(page_size=32), False),
+    (dict(server_args=dict(page_size=16)), True), (dict(server_args=dict(page_size=1)), False),
+    (dict(), True)])
+def test_backend_requires_sixteen_token_pages(runner, ok):
+    from types import SimpleNamespace
+    if "server_args" in runner:
+        runner = dict(server_args=SimpleNamespace(**runner["server_args"]))
+    mr = SimpleNamespace(**runner)
+    if ok:
+        assert sglang_backend.SplitKVHipBackend(mr).split_kv == sglang_backend.DEFAULT_SPLIT_KV
+    else:
+        with pytest.raises(ValueError, match="page_size 16"):
+            sglang_backend.SplitKVHipBackend(mr)
 
 
 def test_page_capacity_bounds_the_page_count():
@@ -330,4 +371,23 @@ def test_hip_graph_capture_and_replay():
         eager = backend.forward_decode(q, None, None, layers[0], fb)
         torch.cuda.synchronize()
         assert float((eager.float() - outs[0].float()).abs().max()) <= 2e-3
+        # ... and an eager batch larger than any captured one, whose workspace is larger:
+        # the graph's workspace must stay the graph's (the next replay writes there while
+        # these tensors are alive), and this batch's result must survive that replay
+        big_fb, big_layers, big_pool, big_r2t = make_batch([700 + 13 * i for i in range(24)],
+                                                           seed=20 + step)
+        backend.init_forward_metadata(big_fb)
+        qb = torch.randn(24, 32 * 128, generator=torch.Generator(device=DEV).manual_seed(step),
+                         device=DEV).half()
+        big = backend.forward_decode(qb, None, None, big_layers[0], big_fb)
+        torch.cuda.synchronize()
+        big_keep = big.clone()
+        want_big = _want(qb.view(-1, 32, 128), big_pool, 0, big_r2t.numpy(),
+                         big_fb.req_pool_indices.tolist(), [700 + 13 * i for i in range(24)])
+        mx, mean = err_stats(big.view(-1, 32, 128), want_big)
+        assert mx <= 1e-2 and mean <= 1e-3, ("large eager batch", mx, mean)
         backend.init_forward_metadata_replay_cuda_graph(bs, rows, seq_lens)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(big, big_keep), "a graph replay wrote into an eager tensor"
+        del big_fb, big_layers, big_pool, big, big_keep
