@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "dk_args.h"
 #include "dk_decode.h"
@@ -303,6 +304,42 @@ int run(Problem p, bool do_merge, void* stream) {
 
 }  // namespace dk
 
+// ---------------------------------------------------------------- static scratch
+// Device memory of dk_decode_attention_noalloc: every GPU the library runs on holds one
+// copy of this array until the process ends. In host code `scratch` is only a handle for
+// the runtime; its device address on the current GPU comes from hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[DK_STATIC_SCRATCH_BYTES];
+
+namespace dk {
+namespace {
+
+// Device address of `scratch` on `device` (the current device), looked up once per device
+// with hipGetSymbolAddress; nullptr (and *err set) if the lookup fails.
+void* scratch_ptr(int device, hipError_t* err) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  *err = hipSuccess;
+  if (device < 0 || device >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    ptrs[device] = p;
+  }
+  return ptrs[device];
+}
+
+}  // namespace
+}  // namespace dk
+
 // ---------------------------------------------------------------- C ABI
 using dk::Problem;
 
@@ -418,6 +455,39 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
                            workspace_bytes, batch, num_q_heads, num_kv_heads, head_dim,
                            page_size, num_pages, num_indices, dtype, strides, split_kv, opts,
                            true);
+  return dk::run(p, true, hip_stream);
+}
+
+int dk_decode_attention_noalloc(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                                const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                void* out, int32_t batch, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                int64_t num_pages, int64_t num_indices, int32_t dtype,
+                                const dk_strides* strides, int32_t split_kv,
+                                const dk_options* opts, void* hip_stream) {
+  dk::clear_error();
+  if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
+  // the scratch this call needs, checked before any device call
+  const size_t need =
+      dk::workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, split_kv);
+  if (need > (size_t)DK_STATIC_SCRATCH_BYTES)
+    return dk::set_error(DK_EWORKSPACE,
+                         "dk_decode_attention_noalloc: this call needs %zu bytes of scratch, "
+                         "more than the %u of the library's static scratch; use "
+                         "dk_decode_attention_ex with a workspace",
+                         need, (unsigned)DK_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0 && batch > 0) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return dk::hip_fail(e, "dk_decode_attention_noalloc: current device");
+    ws = dk::scratch_ptr(dev, &e);
+    if (!ws) return dk::hip_fail(e, "dk_decode_attention_noalloc: static scratch address");
+  }
+  Problem p = make_problem(q, kv_data, nullptr, kv_indptr, kv_indices, kv_last_page_len, out,
+                           ws, ws ? (size_t)DK_STATIC_SCRATCH_BYTES : 0, batch, num_q_heads,
+                           num_kv_heads, head_dim, page_size, num_pages, num_indices, dtype,
+                           strides, split_kv, opts, true);
   return dk::run(p, true, hip_stream);
 }
 

@@ -20,6 +20,7 @@ DK_BF16 = 1
 DK_KV_SAME = 0
 DK_KV_FP8_E4M3 = 2
 ABI_VERSION = 2
+STATIC_SCRATCH_BYTES = 32 << 20     # DK_STATIC_SCRATCH_BYTES: dk_decode_attention_noalloc
 
 DK_OK = 0
 DK_EINVAL = -1
@@ -78,6 +79,10 @@ SIGNATURES = {
                                               _I32, _I32, _I32, _I64, _I64, _I32,
                                               ctypes.POINTER(DkStrides), _I32,
                                               ctypes.POINTER(DkOptions), _P]),
+    "dk_decode_attention_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                                   _I32, _I32, _I64, _I64, _I32,
+                                                   ctypes.POINTER(DkStrides), _I32,
+                                                   ctypes.POINTER(DkOptions), _P]),
     "dk_decode_attention_kv": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I32, _I32,
                                               _I32, _I32, _I32, _I64, _I64, _I32,
                                               ctypes.POINTER(DkStrides), _I32,

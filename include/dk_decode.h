@@ -184,6 +184,29 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
                            int64_t num_indices, int32_t dtype, const dk_strides* strides,
                            int32_t split_kv, const dk_options* opts, void* hip_stream);
 
+/* Bytes of the library's static scratch (see dk_decode_attention_noalloc). */
+#define DK_STATIC_SCRATCH_BYTES (32u << 20)
+
+/* dk_decode_attention_ex without a workspace argument: the fp32 partials go to a static
+ * device array of DK_STATIC_SCRATCH_BYTES (32 MiB) that the library holds on every GPU it
+ * runs on until the process ends, and the call allocates nothing (no hipMalloc / hipFree,
+ * no allocating library routine). No counterpart in the reference: this is for callers
+ * that cannot allocate device memory, e.g. code under HIP graph capture or serving loops
+ * that forbid allocation. The caller still passes inputs and `out`. Calls on one GPU share
+ * that GPU's scratch: calls that overlap in time on one GPU (different streams, or
+ * graphs replayed concurrently) race and give wrong results. Nothing in the scratch needs
+ * to start at zero. A call whose dk_workspace_bytes(batch, num_q_heads, num_kv_heads,
+ * head_dim, split_kv) exceeds DK_STATIC_SCRATCH_BYTES returns DK_EWORKSPACE before any
+ * device call (e.g. the balanced schedule, split_kv 0, at D = 128 and 4 q heads per kv
+ * head fits about 1,500 sequences x 8 kv heads). */
+int dk_decode_attention_noalloc(const void* q, const void* kv_data, const int32_t* kv_indptr,
+                                const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                                void* out, int32_t batch, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                int64_t num_pages, int64_t num_indices, int32_t dtype,
+                                const dk_strides* strides, int32_t split_kv,
+                                const dk_options* opts, void* hip_stream);
+
 /* dk_decode_attention_ex over separate K and V caches, each
  * (num_pages, page_size, num_kv_heads, head_dim) with the same strides (kv_p, kv_s, kv_h;
  * kv_r is ignored): the `(k_cache, v_cache)` form of FlashInfer's paged KV cache that
