@@ -1,26 +1,42 @@
 """Benchmark of the split-KV paged decode-attention path on one MI355X.
 
-Workload (BASELINE.json metric config): batch 32, context 8192 per sequence, 32 q heads,
-8 kv heads, head_dim 128, fp16, page_size 16, page table a seeded random permutation of
-the 16384-page pool; synthetic N(0,1) data already resident in HBM.
+Default workload (BASELINE.json's metric config): batch 32, context 8192 per sequence,
+32 q heads, 8 kv heads, head_dim 128, fp16, page_size 16, page table a seeded random
+permutation of the 16384-page pool; synthetic N(0,1) data already resident in HBM.
 
-A step is one decode_attention call (pass 1 + pass 2) through the C ABI, with split_kv 0
-(automatic schedule) and the plan hint max_pages_per_seq taken once from the host copy of
-kv_indptr before the timed region (as a serving framework plans a batch). Before every
-step a 1 GiB device fill evicts the 4 MB L2s and the 256 MB Infinity Cache, as the
-reference flushes L2 before each timed call (bench/microbench_cuda.py:75-90,140-157);
-HIP events on the launch stream bracket the call itself. The flush is enqueued without a
-host sync, so host launch overhead is hidden behind it and the events measure GPU time.
-The W warm-up steps are such flush + call steps too, after an untimed settling phase of
-the same steps (0.3 s) that lets the GPU clocks reach their steady state.
+A step is one decode_attention call (pass 1 + pass 2 when the schedule has one) through
+the C ABI, with split_kv 0 (automatic schedule) and the plan hint max_pages_per_seq taken
+once from the host copy of kv_indptr before the timed region (as a serving framework
+plans a batch). Before every step a 1 GiB device fill evicts the 4 MB L2s and the 256 MB
+Infinity Cache, as the reference flushes L2 before each timed call
+(bench/microbench_cuda.py:75-90,140-157); HIP events on the launch stream bracket the call
+itself. The flush is enqueued without a host sync, so host launch overhead is hidden
+behind it and the events measure GPU time. The W warm-up steps are such flush + call
+steps too, after an untimed settling phase of the same steps (0.3 s) that lets the GPU
+clocks reach their steady state.
 
-Other shapes (--num-q-heads, --num-kv-heads, --head-dim, --batch, --ctx, --kv-dtype, and
---ragged-min for config 4's ragged mix) are for profiling; the JSON's config names the
-workload measured.
+Modes:
+  (default)        one JSON line for the metric workload (or the shape given by --batch,
+                   --ctx, --num-q-heads, --num-kv-heads, --head-dim, --dtype, --kv-dtype,
+                   --ragged-min, --split ...), with `roofline` and `cpu_baseline`
+  --config N       BASELINE.json config N (1-5) on its own workloads: one JSON line per
+                   (shape, split_kv) of the config's sweep, each with p50/p95 us, TB/s,
+                   the fraction of 8 TB/s and the max-abs error against the CPU oracle on
+                   sampled sequences
+  --single-call    one flush and one call, no settling or warm-up (for rocprofv3 --pmc
+                   counter runs, which then see exactly the call's dispatches)
 
-Prints one JSON line. `value` is achieved algorithmic HBM bandwidth in TB/s
-(bytes of the reference's model, bench/microbench_cuda.py:114-121, plus page tables,
-divided by the p50 per-call time); `us_per_call` is the p50 time.
+`value` is achieved algorithmic HBM bandwidth in TB/s (bytes of the reference's model,
+bench/microbench_cuda.py:114-121, plus page tables, divided by the p50 per-call time);
+`us_per_call` is the p50 time.
+
+CPU baseline (default mode): the reference's CPU path (src/reference.py: the whole pool
+to fp32, a per-page gather into zero-padded dense K/V, GQA by repeat_interleave, fp32
+softmax attention) restated in torch (oracle/reference_torch.py), timed on the box's host
+cores over the whole batch, gather and attention separately, median of 3. For a ragged
+mix, where that padded form is wrong, the numpy per-sequence oracle (oracle/reference.py)
+is timed on a sample of sequences instead. In every mode the baseline's outputs are also
+the checker of the GPU output (max_abs_err_vs_fp32).
 """
 from __future__ import annotations
 
@@ -40,18 +56,39 @@ for _p in (ROOT / "decode-kernel_amd", ROOT):
         sys.path.insert(0, str(_p))
 
 METRIC = ("µs/call + achieved HBM TB/s (% peak), decode B=32 ctx=8k Hq32/Hkv8 d128")
+CONFIG_METRIC = "µs/call + achieved HBM TB/s (% peak), BASELINE config {n}"
 PEAK_GBPS = 8000.0          # MI355X HBM3E
 FLUSH_BYTES = 1 << 30
 SETTLE_S = 0.3              # untimed flush + call steps before the warm-up
+# Host threads of the CPU baseline: the GPU box gives each GPU a 16-thread CPU share
+# (whatever os.cpu_count() reports there), so at most that many.
+CPU_THREADS_CAP = 16
 TRAFFIC_FILES = {"same": ROOT / "profiles" / "pass1_metric_hbm_traffic.md",
                  "fp8": ROOT / "profiles" / "pass1_metric_fp8_hbm_traffic.md"}
 
+# BASELINE.json configs as concrete workloads: (label, shape) with the split_kv values of
+# the config's sweep (0 = the library's automatic schedule with the plan hint).
+CONFIGS = {
+    1: [dict(batch=2, ctx=512, dtype="fp16", table="contiguous", splits=(4, 0))],
+    2: [dict(batch=b, ctx=4096, dtype="fp16", table="permuted", splits=(1, 2, 4, 8, 16, 0))
+        for b in (1, 4, 16, 32, 64)],
+    3: [dict(batch=b, ctx=c, dtype="bf16", table="permuted", splits=(16, 32, 64, 128, 0))
+        for b in (1, 4) for c in (32768, 131072)],
+    4: [dict(batch=128, ctx=8192, ragged_min=128, dtype="fp16", table="freelist",
+             q_scale=128 ** -0.5, splits=(0, 1, 4, 16))],
+    5: [dict(batch=32, ctx=2048, d=64, dtype="bf16", table="permuted", splits=(0,))],
+}
 
-def parse_args():
+
+def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
+                    help="run BASELINE.json config N's sweep (one JSON line per point)")
+    ap.add_argument("--single-call", action="store_true",
+                    help="one flush + one call, no settling / warm-up (counter runs)")
     ap.add_argument("--split", type=int, default=0, help="split_kv (0 = automatic)")
     ap.add_argument("--schedule", type=int, default=0,
                     help="split_kv 0: 0 automatic, 1 balanced, 2 one pass")
@@ -83,11 +120,14 @@ def parse_args():
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="after the run, copy a MIB-MiB device buffer twice (a kernel of "
                          "known traffic that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--cpu-sample", type=int, default=16,
-                    help="sequences of the workload the CPU baseline computes")
-    a = ap.parse_args()
+    ap.add_argument("--cpu-sample", type=int, default=0,
+                    help="sequences the CPU baseline computes (0 = the whole batch for "
+                         "uniform lengths, 8 for a ragged mix)")
+    a = ap.parse_args(argv)
     if a.ragged_min and not 1 <= a.ragged_min <= a.ctx:
         ap.error(f"--ragged-min must be in [1, ctx={a.ctx}], got {a.ragged_min}")
+    if a.single_call and a.config:
+        ap.error("--single-call times the default workload; it does not combine with --config")
     return a
 
 
@@ -105,39 +145,410 @@ def read_traffic(kv_dtype="same"):
     return None
 
 
-def cpu_baseline(q, kv, indptr, ids, last, out, sample):
-    """The oracle (a numpy restatement of the reference's CPU path, src/reference.py) timed
-    on `sample` sequences of the same workload; also returns its max-abs difference from
-    the GPU output on those sequences."""
-    import numpy as np
-    from threadpoolctl import threadpool_info, threadpool_limits
+def host_cpu():
+    """(os.cpu_count(), threads the baseline uses, CPU model name)."""
+    n = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return n, min(n, CPU_THREADS_CAP), model
 
-    import torch
+
+def percentile(sorted_us, pct):
+    return sorted_us[min(len(sorted_us) - 1, int(math.ceil(pct / 100 * len(sorted_us))) - 1)]
+
+
+# ---------------------------------------------------------------- workloads
+
+class Workload:
+    """Synthetic decode inputs of one shape on the GPU, with the tables on the host."""
+
+    def __init__(self, torch, layout, dev, batch, ctx, hq=32, hkv=8, d=128, dtype="fp16",
+                 table="permuted", ragged_min=0, q_scale=1.0, kv_dtype="same", seed=1):
+        self.torch = torch
+        self.dtype_name = dtype
+        self.dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
+        self.batch, self.ctx, self.hq, self.hkv, self.d = batch, ctx, hq, hkv, d
+        self.ragged_min = ragged_min
+        if ragged_min:
+            self.lens = layout.ragged_lengths(batch, ragged_min, ctx, seed=4)
+            pool = max(65536, sum((n + 15) // 16 for n in self.lens))
+            q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+                batch, self.lens, hq, hkv, d, dtype=self.dtype, device=dev,
+                page_table="freelist", pool_pages=pool, seed=seed, q_scale=q_scale)
+            self.table = "free-list"
+        else:
+            self.lens = [ctx] * batch
+            q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+                batch, ctx, hq, hkv, d, dtype=self.dtype, device=dev, page_table=table,
+                seed=seed, q_scale=q_scale)
+            self.table = table
+        self.kv_ref = kv                      # the cache's values as q's dtype (CPU checks)
+        self.kv8 = kv_dtype == "fp8"
+        if self.kv8:
+            kv = self._to_fp8(dev, kv)
+        self.q, self.kv, self.indptr, self.ids, self.last = q, kv, indptr, ids, last
+        self.indptr_host = indptr.cpu()
+        self.bytes = layout.attention_bytes(batch, self.lens, hq, hkv, d,
+                                            kv_elem_bytes=1 if self.kv8 else 0)
+
+    def _to_fp8(self, dev, kv):
+        # random finite E4M3 codes of moderate magnitude (|value| <= 3.75), unit scales;
+        # the CPU checks attend over the same values stored as q's dtype (exact)
+        import numpy as np
+        torch = self.torch
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        codes = torch.randint(0, 0x48, kv.shape, generator=g, device=dev, dtype=torch.int32)
+        codes |= torch.randint(0, 2, kv.shape, generator=g, device=dev,
+                               dtype=torch.int32) * 0x80
+        codes = codes.to(torch.uint8)
+        from oracle import fp8 as fp8_oracle        # the CPU checks' input only
+        table = torch.from_numpy(fp8_oracle.decode(np.arange(256)).astype(np.float32))
+        table = torch.nan_to_num(table).to(dev).to(self.dtype)
+        self.kv_ref = table[codes.long()]
+        return codes.view(torch.float8_e4m3fn)
+
+    def label(self):
+        ctx = f"U[{self.ragged_min},{self.ctx}]" if self.ragged_min else self.ctx
+        return (f"paged decode attention B={self.batch} ctx={ctx} Hq={self.hq} Hkv={self.hkv} "
+                f"D={self.d} {self.dtype_name}{' (fp8 E4M3 cache)' if self.kv8 else ''} "
+                f"page_size=16 {self.table} pages")
+
+
+class Caller:
+    """One (workload, split_kv, options) through the C ABI, with its own output and
+    workspace, and the timing protocol."""
+
+    def __init__(self, lib, dk_lib, attention, wl, split, opts, stream):
+        torch = wl.torch
+        self.lib, self.dk_lib, self.wl, self.split, self.opts, self.stream = \
+            lib, dk_lib, wl, split, opts, stream
+        self.out = torch.empty_like(wl.q)
+        ws_bytes = dk_lib.workspace_bytes(wl.batch, wl.hq, wl.hkv, wl.d, split)
+        p_total = dk_lib.partials_layout(wl.batch, wl.hq, wl.d, split)[3] if split else ws_bytes
+        self.ws = torch.empty(max(ws_bytes, p_total, 1), dtype=torch.uint8, device=wl.q.device)
+        self.strides = attention._strides(wl.q, wl.kv, self.out)
+        self.code = attention._DTYPE_CODE[wl.dtype]
+        self.common = (wl.q.data_ptr(), wl.kv.data_ptr(), wl.indptr.data_ptr(),
+                       wl.ids.data_ptr(), wl.last.data_ptr())
+        self.shape = (wl.batch, wl.hq, wl.hkv, wl.d, 16, wl.kv.shape[0], wl.ids.shape[0],
+                      self.code, ctypes.byref(self.strides))
+        # the schedule the full call runs (split_kv 0 resolves on the device's CU count)
+        self.schedule = dk_lib.plan_schedule(wl.batch, wl.hq, wl.hkv, wl.d, wl.ids.shape[0],
+                                             self.code, split, opts)
+
+    def full(self):
+        return self.lib.dk_decode_attention_ex(*self.common, self.out.data_ptr(),
+                                               self.ws.data_ptr(), self.ws.numel(), *self.shape,
+                                               self.split, ctypes.byref(self.opts),
+                                               self.stream.cuda_stream)
+
+    def pass1(self):
+        return self.lib.dk_decode_partials(*self.common, self.ws.data_ptr(), self.ws.numel(),
+                                           *self.shape, self.split, ctypes.byref(self.opts),
+                                           self.stream.cuda_stream)
+
+    def dominant(self):
+        """The dominant kernel alone: the whole call in one pass, else pass 1."""
+        return self.full if self.schedule == 1 else self.pass1
+
+    def schedule_name(self):
+        return {1: "one pass"}.get(self.schedule, "balanced + merge" if self.schedule == 0
+                                    else f"split {self.schedule} + merge")
+
+
+class Timer:
+    """Flush + events around each call, on the launch stream."""
+
+    def __init__(self, torch, dev, stream, mode="write"):
+        self.torch, self.stream, self.mode = torch, stream, mode
+        self.buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+
+    def flush(self):
+        # evict the caches: write (fill) or read (sum) a 1 GiB buffer
+        if self.mode == "write":
+            self.buf.zero_()
+        else:
+            self.buf.sum()
+
+    def run(self, fn, steps):
+        torch = self.torch
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        for e0, e1 in evs:
+            self.flush()
+            e0.record(self.stream)
+            fn()
+            e1.record(self.stream)
+        torch.cuda.synchronize()
+        return [e0.elapsed_time(e1) * 1e3 for e0, e1 in evs]     # microseconds
+
+    def settle(self, fn):
+        # untimed flush + call steps until the GPU clocks reach their steady state; without
+        # it the first timed steps run slow
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < SETTLE_S:
+            self.run(fn, 20)
+
+
+# ---------------------------------------------------------------- CPU baseline leg
+
+def _host_subproblem(wl, seqs):
+    """q, kv pages and rebased page tables of sequences `seqs` on the host (the pages of
+    those sequences only, so the CPU side never holds the whole pool)."""
+    torch = wl.torch
+    ip = wl.indptr_host.tolist()
+    ids = wl.ids.cpu()
+    pages = [ids[ip[b]:ip[b + 1]] for b in seqs]
+    flat = torch.cat(pages) if pages else torch.zeros(0, dtype=torch.int32)
+    kv = wl.kv_ref[flat.to(wl.kv_ref.device).long()].cpu()
+    indptr = torch.zeros(len(seqs) + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor([len(p) for p in pages], dtype=torch.int64), 0).to(torch.int32)
+    return (wl.q[list(seqs)].cpu(), kv, indptr, torch.arange(len(flat), dtype=torch.int32),
+            wl.last.cpu()[list(seqs)])
+
+
+def cpu_baseline_literal(wl, seqs, threads, reps=3):
+    """The reference's CPU path (oracle/reference_torch.py) on sequences `seqs`: median
+    gather / attention / total seconds of `reps` runs, and the output (len(seqs), Hq, D)."""
+    torch = wl.torch
+    from oracle import reference_torch as rt
+    q, kv, indptr, ids, last = _host_subproblem(wl, seqs)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g, a, out = [], [], None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            K, V = rt.gather_dense(kv, indptr, ids, last)
+            t1 = time.perf_counter()
+            out = rt.attend_dense(q, K, V)
+            t2 = time.perf_counter()
+            del K, V
+            g.append(t1 - t0)
+            a.append(t2 - t1)
+    finally:
+        torch.set_num_threads(prev)
+    tot = [x + y for x, y in zip(g, a)]
+    return statistics.median(g), statistics.median(a), statistics.median(tot), out
+
+
+def cpu_baseline_masked(wl, seqs, threads, reps=3):
+    """The numpy per-sequence oracle (oracle/reference.py; masked, right for ragged mixes)
+    on sequences `seqs`: median seconds of `reps` runs (gather and attention are not
+    separable there: each sequence gathers its own pages), and the output."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
 
     from oracle.reference import reference_attention_paged
-
-    cores = min(os.cpu_count() or 1, 16)
-    as_np = lambda t: (t.float() if t.dtype == torch.bfloat16 else t).cpu().numpy()  # noqa: E731
+    torch = wl.torch
+    q, kv, indptr, ids, last = _host_subproblem(wl, seqs)
+    as_np = lambda t: (t.float() if t.dtype == torch.bfloat16 else t).numpy()  # noqa: E731
     qn, kvn = as_np(q), as_np(kv)
-    ipn, idn, ln = indptr.cpu().numpy(), ids.cpu().numpy(), last.cpu().numpy()
-    subset = list(range(min(sample, q.shape[0])))
-    with threadpool_limits(limits=cores):
-        blas = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-        times = []
-        for _ in range(3):
+    ipn, idn, ln = indptr.numpy(), ids.numpy(), last.numpy()
+    times, out = [], None
+    with threadpool_limits(limits=threads):
+        for _ in range(reps):
             t0 = time.perf_counter()
-            want = reference_attention_paged(qn, kvn, ipn, idn, ln, batch_subset=subset)
+            out = reference_attention_paged(qn, kvn, ipn, idn, ln)
             times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    err = float(np.abs(out[subset].float().cpu().numpy() - want[subset]).max())
-    # scaled to the whole batch by pages (the sample's share of the work, also when ragged)
-    pages = lambda bs: sum(max(int(ipn[b + 1]) - int(ipn[b]), 0) for b in bs)  # noqa: E731
-    per_call_us = t * pages(range(q.shape[0])) / max(pages(subset), 1) * 1e6
-    return per_call_us, blas, len(subset), err
+    return statistics.median(times), torch.from_numpy(np.asarray(out))
 
 
-def main():
-    args = parse_args()
+def max_abs_err(got, want_rows, seqs):
+    """max |got[seqs] - want| (want (len(seqs), Hq, D), fp32 on the host)."""
+    g = got[list(seqs)].float().cpu()
+    return float((g - want_rows.float()).abs().max()) if g.numel() else 0.0
+
+
+# ---------------------------------------------------------------- modes
+
+def make_opts(dk_lib, args, wl, split):
+    hint = 0 if args.no_plan_hint else _plan_hint(wl)
+    return dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule, hint,
+                          kv_dtype=dk_lib.DK_KV_FP8_E4M3 if wl.kv8 else dk_lib.DK_KV_SAME), hint
+
+
+def _plan_hint(wl):
+    import attention
+    return attention.plan_hint(wl.indptr_host)
+
+
+def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
+    wl = Workload(torch, layout, dev, args.batch, args.ctx, args.num_q_heads,
+                  args.num_kv_heads, args.head_dim, args.dtype,
+                  "freelist" if args.ragged_min else args.page_table, args.ragged_min,
+                  q_scale=args.head_dim ** -0.5 if args.ragged_min else 1.0,
+                  kv_dtype=args.kv_dtype)
+    split = attention.resolve_split(args.split)
+    opts, hint = make_opts(dk_lib, args, wl, split)
+    c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
+    timer = Timer(torch, dev, stream, args.flush)
+    dk_lib.check(c.full(), "decode_attention")
+    if args.single_call:
+        steps, warmup = 1, 0
+        torch.cuda.synchronize()
+        call_us = timer.run(c.full, 1)
+        pass1_us = call_us if c.schedule == 1 else None
+        wall = 0.0
+    else:
+        steps, warmup = args.steps, args.warmup
+        dk_lib.check(c.dominant()(), "decode_partials")
+        timer.settle(c.full)
+        timer.run(c.full, warmup)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        call_us = timer.run(c.full, steps)
+        wall = time.perf_counter() - wall0
+        pass1_us = timer.run(c.dominant(), steps)
+    call_us.sort()
+    p50 = statistics.median(call_us)
+    p95 = percentile(call_us, 95)
+    p1_avg = statistics.fmean(pass1_us) if pass1_us else p50
+    achieved = wl.bytes / (p1_avg * 1e-6) / 1e9           # GB/s, the dominant kernel alone
+    # final correctness of the timed output
+    dk_lib.check(c.full(), "decode_attention")
+    torch.cuda.synchronize()
+    finite = bool(torch.isfinite(c.out).all())
+    hq, hkv, d = wl.hq, wl.hkv, wl.d
+    mfma_qk = args.qk_path == 1 or (args.qk_path == 0 and (hq // hkv > 4 or (wl.kv8 and d >= 256)))
+    metric_workload = ((wl.batch, wl.ctx, hq, hkv, d) == (32, 8192, 32, 8, 128)
+                       and wl.table == "permuted" and not wl.ragged_min)
+    rec = {
+        "metric": METRIC, "value": round(wl.bytes / (p50 * 1e-6) / 1e12, 4), "unit": "TB/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
+        "config": {"workload": wl.label(),
+                   "kv_dtype": "fp8_e4m3" if wl.kv8 else args.dtype,
+                   "batch": wl.batch,
+                   "context_length": f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
+                   "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d, "page_size": 16,
+                   "split_kv": split, "schedule": c.schedule_name(),
+                   "plan_hint_max_pages": hint,
+                   "qk_path": "mfma" if mfma_qk else "valu", "pv_path": "mfma"},
+        "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
+        "pct_of_peak": round(100 * wl.bytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
+        "bytes_per_call": wl.bytes, "wall_s_timed_loop": round(wall, 3),
+        "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": read_traffic(args.kv_dtype) if metric_workload else None,
+                     "kernel": "dk_pass1_balanced" if c.schedule == 0 else "dk_pass1_split"},
+        "cpu_baseline": None,
+    }
+    if args.single_call:
+        rec["mode"] = "single call (no settling, no warm-up)"
+    if not args.no_cpu_baseline:
+        ncpu, threads, model = host_cpu()
+        if wl.ragged_min:
+            n = min(args.cpu_sample or 8, wl.batch)
+            seqs = list(range(n))
+            t, want = cpu_baseline_masked(wl, seqs, threads)
+            pages = lambda bs: sum(int(wl.indptr_host[b + 1] - wl.indptr_host[b]) for b in bs)  # noqa: E731
+            total_us = t * pages(range(wl.batch)) / max(pages(seqs), 1) * 1e6
+            base = {"value": round(total_us, 1), "unit": "us/call", "cores": threads,
+                    "kind": "port",
+                    "sample": f"numpy fp32 per-sequence oracle (oracle/reference.py; the "
+                              f"reference's zero-padded form is wrong for ragged batches) on "
+                              f"{n} of {wl.batch} sequences, median of 3, scaled to the "
+                              f"whole batch by pages"}
+        else:
+            n = min(args.cpu_sample or wl.batch, wl.batch)
+            seqs = list(range(n))
+            tg, ta, tt, want = cpu_baseline_literal(wl, seqs, threads)
+            scale = wl.batch / n
+            base = {"value": round(tt * scale * 1e6, 1), "unit": "us/call", "cores": threads,
+                    "kind": "port", "gather_us": round(tg * scale * 1e6, 1),
+                    "attention_us": round(ta * scale * 1e6, 1),
+                    "sample": f"the reference's CPU path (src/reference.py) restated in torch "
+                              f"(oracle/reference_torch.py: pool to fp32, per-page gather into "
+                              f"zero-padded dense K/V, repeat_interleave GQA, fp32 softmax "
+                              f"attention) on {n} of {wl.batch} sequences"
+                              f"{'' if n == wl.batch else ' (scaled to the batch)'}, "
+                              f"median of 3, gather and attention timed separately"}
+        base.update({"cpu_count": ncpu, "threads": threads, "cpu_model": model,
+                     "threads_note": f"threads = min(os.cpu_count(), {CPU_THREADS_CAP}): the "
+                                     f"GPU box's CPU share per GPU"})
+        base["tb_s"] = round(wl.bytes / (base["value"] * 1e-6) / 1e12, 6)
+        rec["cpu_baseline"] = base
+        rec["max_abs_err_vs_fp32"] = max_abs_err(c.out, want, seqs)
+    print(json.dumps(rec), flush=True)
+    if args.calibration_copy > 0:
+        src = torch.ones(args.calibration_copy << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+
+def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
+    """BASELINE config N: one JSON line per (shape, split_kv) point of its sweep."""
+    ncpu, threads, model = host_cpu()
+    timer = Timer(torch, dev, stream, args.flush)
+    settled = False
+    for shape in CONFIGS[args.config]:
+        shape = dict(shape)
+        splits = shape.pop("splits")
+        wl = Workload(torch, layout, dev, shape.pop("batch"), shape.pop("ctx"),
+                      d=shape.pop("d", 128), **shape)
+        # the CPU oracle on sampled sequences: the first and the last (one for very long
+        # contexts), the checker of every split of this shape and its CPU baseline
+        seqs = [0] if wl.batch == 1 or max(wl.lens) > 65536 else [0, wl.batch - 1]
+        cpu_s, want = None, None
+        if not args.no_cpu_baseline:
+            cpu_s, want = cpu_baseline_masked(wl, seqs, threads, reps=1)
+        for split in splits:
+            opts, hint = make_opts(dk_lib, args, wl, split)
+            c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
+            dk_lib.check(c.full(), "decode_attention")
+            if not settled:
+                timer.settle(c.full)
+                settled = True
+            timer.run(c.full, args.warmup)
+            us = sorted(timer.run(c.full, args.steps))
+            p1 = timer.run(c.dominant(), args.steps)
+            dk_lib.check(c.full(), "decode_attention")
+            torch.cuda.synchronize()
+            p50, p95 = statistics.median(us), percentile(us, 95)
+            tbs = wl.bytes / (p50 * 1e-6) / 1e12
+            rec = {
+                "metric": CONFIG_METRIC.format(n=args.config), "value": round(tbs, 4),
+                "unit": "TB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True,
+                "dtype": wl.dtype_name, "data": "synthetic",
+                "config": {"config_id": args.config, "workload": wl.label(),
+                           "batch": wl.batch, "context_length":
+                               f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
+                           "num_q_heads": wl.hq, "num_kv_heads": wl.hkv, "head_dim": wl.d,
+                           "split_kv": split, "schedule": c.schedule_name(),
+                           "plan_hint_max_pages": hint},
+                "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
+                "frac": round(tbs * 1e12 / (PEAK_GBPS * 1e9), 4),
+                "pct_of_peak": round(100 * tbs * 1e12 / (PEAK_GBPS * 1e9), 2),
+                "dominant_kernel_us_avg": round(statistics.fmean(p1), 2),
+                "bytes_per_call": wl.bytes, "output_finite": bool(torch.isfinite(c.out).all()),
+            }
+            if want is not None:
+                rec["max_abs_err_vs_fp32"] = max_abs_err(c.out, want, seqs)
+                rec["oracle_sequences"] = seqs
+                rec["cpu_baseline"] = {
+                    "value": round(cpu_s * 1e6, 1), "unit": "us for the sampled sequences",
+                    "cores": threads, "kind": "port", "cpu_count": ncpu, "cpu_model": model,
+                    "sample": f"numpy fp32 per-sequence oracle (oracle/reference.py) on "
+                              f"sequences {seqs}, one run"}
+            print(json.dumps(rec), flush=True)
+            del c
+
+
+def main(argv=None):
+    args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the decode path has no multi-GPU mode here)", file=sys.stderr)
@@ -152,163 +563,11 @@ def main():
     lib = dk_lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
-    B, ctx, hq, hkv, d = args.batch, args.ctx, args.num_q_heads, args.num_kv_heads, args.head_dim
-    # the recorded rocprofv3 traffic belongs to the metric's workload only
-    metric_workload = ((B, ctx, hq, hkv, d) == (32, 8192, 32, 8, 128)
-                       and args.page_table == "permuted" and not args.ragged_min)
-    if args.ragged_min:
-        lens = layout.ragged_lengths(B, args.ragged_min, ctx, seed=4)
-        pool = max(65536, sum((n + 15) // 16 for n in lens))
-        q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-            B, lens, hq, hkv, d, dtype=dtype, device=dev, page_table="freelist",
-            pool_pages=pool, seed=1, q_scale=d ** -0.5)
-    else:
-        lens = ctx
-        q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-            B, ctx, hq, hkv, d, dtype=dtype, device=dev, page_table=args.page_table, seed=1)
-    kv_ref = kv                        # the cache's values for the CPU baseline
-    kv8 = args.kv_dtype == "fp8"
-    if kv8:
-        # random finite E4M3 codes of moderate magnitude (|value| <= 3.75), unit scales;
-        # the CPU baseline attends over the same values stored as fp16 (exact)
-        import numpy as np
-        g = torch.Generator(device=dev)
-        g.manual_seed(1)
-        codes = torch.randint(0, 0x48, kv.shape, generator=g, device=dev, dtype=torch.int32)
-        codes |= torch.randint(0, 2, kv.shape, generator=g, device=dev,
-                               dtype=torch.int32) * 0x80
-        codes = codes.to(torch.uint8)
-        from oracle import fp8 as fp8_oracle        # the CPU baseline's input only
-        table = torch.from_numpy(fp8_oracle.decode(np.arange(256)).astype(np.float32))
-        table = torch.nan_to_num(table).to(dev).to(dtype)
-        del kv
-        kv_ref = table[codes.long()]
-        kv = codes.view(attention.KV_FP8)
-    split = attention.resolve_split(args.split)
-    nbytes = layout.attention_bytes(B, lens, hq, hkv, d, kv_elem_bytes=1 if kv8 else 0)
-    out = torch.empty_like(q)
-    ws_bytes = dk_lib.workspace_bytes(B, hq, hkv, d, split)
-    p_total = dk_lib.partials_layout(B, hq, d, split)[3] if split else ws_bytes
-    ws = torch.empty(max(ws_bytes, p_total), dtype=torch.uint8, device=dev)
-    flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
-
-    def flush():
-        # evict the caches: write (fill) or read (sum) a 1 GiB buffer
-        if args.flush == "write":
-            flush_buf.zero_()
-        else:
-            flush_buf.sum()
-    strides = attention._strides(q, kv, out)
-    # plan step, outside the timed region: the longest sequence's page count from the host
-    # side of the page table (what a serving framework keeps on the host)
-    hint = 0 if args.no_plan_hint else attention.plan_hint(indptr.cpu())
-    opts = dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule, hint,
-                          kv_dtype=dk_lib.DK_KV_FP8_E4M3 if kv8 else dk_lib.DK_KV_SAME)
-    code = attention._DTYPE_CODE[dtype]
-    # the schedule the full call runs (split_kv 0 resolves on the device's CU count)
-    eff = dk_lib.plan_schedule(B, hq, hkv, d, ids.shape[0], code, split, opts)
     stream = torch.cuda.current_stream(dev)
-    common = (q.data_ptr(), kv.data_ptr(), indptr.data_ptr(), ids.data_ptr(), last.data_ptr())
-    shape = (B, hq, hkv, d, 16, kv.shape[0], ids.shape[0], code, ctypes.byref(strides))
-
-    def full_call():
-        return lib.dk_decode_attention_ex(*common, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                          *shape, split, ctypes.byref(opts), stream.cuda_stream)
-
-    def pass1_only():
-        return lib.dk_decode_partials(*common, ws.data_ptr(), ws.numel(), *shape, split,
-                                      ctypes.byref(opts), stream.cuda_stream)
-
-    # The dominant kernel: with one pass it is the whole call; otherwise pass 1 alone.
-    pass1_call = full_call if eff == 1 else pass1_only
-
-    dk_lib.check(full_call(), "decode_attention")
-    dk_lib.check(pass1_call(), "decode_partials")
-
-    def timed(fn, steps):
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(steps)]
-        for e0, e1 in evs:
-            flush()
-            e0.record(stream)
-            fn()
-            e1.record(stream)
-        torch.cuda.synchronize()
-        return [e0.elapsed_time(e1) * 1e3 for e0, e1 in evs]     # microseconds
-
-    # Warm-up: W steps exactly like the timed ones (flush + call), after an untimed
-    # settling phase of the same steps (at least SETTLE_S seconds) that brings the GPU's
-    # clocks to their steady state; without it the first timed steps run slow.
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < SETTLE_S:
-        timed(full_call, 20)
-    timed(full_call, args.warmup)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    call_us = timed(full_call, args.steps)
-    wall = time.perf_counter() - wall0
-    pass1_us = timed(pass1_call, args.steps)
-    call_us.sort()
-    p50 = statistics.median(call_us)
-    p95 = call_us[min(len(call_us) - 1, int(math.ceil(0.95 * len(call_us))) - 1)]
-    p1_avg = statistics.fmean(pass1_us)
-    achieved = nbytes / (p1_avg * 1e-6) / 1e9           # GB/s, pass-1 kernel alone
-    # final correctness of the timed output
-    dk_lib.check(full_call(), "decode_attention")
-    torch.cuda.synchronize()
-    finite = bool(torch.isfinite(out).all())
-    # q.k path the library takes (its automatic rule: MFMA beyond 4 q heads per kv head
-    # and for fp8 at D = 256)
-    mfma_qk = args.qk_path == 1 or (args.qk_path == 0 and (hq // hkv > 4 or (kv8 and d >= 256)))
-    qk_name = "mfma" if mfma_qk else "valu"
-
-    ctx_label = f"U[{args.ragged_min},{ctx}]" if args.ragged_min else ctx
-    table_label = "free-list" if args.ragged_min else args.page_table
-    rec = {
-        "metric": METRIC, "value": round(nbytes / (p50 * 1e-6) / 1e12, 4), "unit": "TB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
-        "config": {"workload": f"paged decode attention B={B} ctx={ctx_label} Hq={hq} "
-                               f"Hkv={hkv} D={d} {args.dtype}"
-                               f"{' (fp8 E4M3 cache)' if kv8 else ''} "
-                               f"page_size=16 {table_label} pages",
-                   "kv_dtype": "fp8_e4m3" if kv8 else args.dtype,
-                   "batch": B, "context_length": ctx_label, "num_q_heads": hq,
-                   "num_kv_heads": hkv,
-                   "head_dim": d, "page_size": 16,
-                   "split_kv": split,
-                   "schedule": {1: "one pass"}.get(eff, "balanced + merge" if eff == 0
-                                                   else f"split {eff} + merge"),
-                   "plan_hint_max_pages": hint,
-                   "qk_path": qk_name, "pv_path": "mfma"},
-        "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
-        "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
-        "bytes_per_call": nbytes, "wall_s_timed_loop": round(wall, 3),
-        "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": read_traffic(args.kv_dtype) if metric_workload else None,
-                     "kernel": "dk_pass1_balanced" if eff == 0 else "dk_pass1_split"},
-        "cpu_baseline": None,
-    }
-    if not args.no_cpu_baseline:
-        us, cores, n, err = cpu_baseline(q, kv_ref, indptr, ids, last, out, args.cpu_sample)
-        rec["cpu_baseline"] = {
-            "value": round(us, 1), "unit": "us/call", "cores": cores, "kind": "port",
-            "tb_s": round(nbytes / (us * 1e-6) / 1e12, 5),
-            "sample": f"numpy fp32 restatement of reference_attention_paged on {n} of {B} "
-                      f"whole sequences, median of 3, scaled to the whole batch by "
-                      f"pages"}
-        rec["max_abs_err_vs_fp32"] = err
-    print(json.dumps(rec), flush=True)
-    if args.calibration_copy > 0:
-        src = torch.ones(args.calibration_copy << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(2):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+    if args.config:
+        config_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
+    else:
+        metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
     return 0
 
 

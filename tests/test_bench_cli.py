@@ -36,3 +36,57 @@ def test_recorded_traffic_is_read_and_close_to_the_algorithmic_bytes(kv_dtype, a
     t = bench.read_traffic(kv_dtype)
     assert t is not None
     assert abs(t / algorithmic - 1.0) < 0.01, t
+
+
+def test_config_sweeps_follow_baseline_json():
+    import json
+    base = json.loads((ROOT / "BASELINE.json").read_text())
+    assert len(base["configs"]) == len(bench.CONFIGS) == 5
+    c1, = bench.CONFIGS[1]
+    assert (c1["batch"], c1["ctx"], c1["table"], c1["splits"][0]) == (2, 512, "contiguous", 4)
+    assert [s["batch"] for s in bench.CONFIGS[2]] == [1, 4, 16, 32, 64]
+    assert all(s["ctx"] == 4096 and set(s["splits"]) >= {1, 2, 4, 8, 16}
+               for s in bench.CONFIGS[2])
+    assert {(s["batch"], s["ctx"]) for s in bench.CONFIGS[3]} == {
+        (1, 32768), (1, 131072), (4, 32768), (4, 131072)}
+    assert all(s["dtype"] == "bf16" and set(s["splits"]) >= {16, 32, 64, 128}
+               for s in bench.CONFIGS[3])
+    c4, = bench.CONFIGS[4]
+    assert (c4["batch"], c4["ragged_min"], c4["ctx"], c4["table"]) == (128, 128, 8192, "freelist")
+    c5, = bench.CONFIGS[5]
+    assert (c5["batch"], c5["ctx"], c5["d"], c5["dtype"]) == (32, 2048, 64, "bf16")
+
+
+def test_single_call_does_not_combine_with_a_config_sweep():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--single-call", "--config", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "--single-call" in r.stderr and r.stdout == ""
+
+
+def test_host_cpu_reports_count_threads_and_model():
+    n, threads, model = bench.host_cpu()
+    assert n >= 1 and 1 <= threads <= min(n, bench.CPU_THREADS_CAP) and model
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_cpu_baseline_legs_agree_with_the_oracle(ragged):
+    # the two CPU-baseline forms on a small CPU-resident workload: the literal torch path
+    # (uniform lengths) and the masked numpy oracle, on a subset of sequences
+    import numpy as np
+    import torch
+
+    import layout
+    from oracle.reference import reference_attention_paged
+    wl = bench.Workload(torch, layout, "cpu", 5, 200, hq=8, hkv=2, d=64,
+                        ragged_min=17 if ragged else 0, table="permuted")
+    seqs = [0, 3, 4]
+    want = reference_attention_paged(wl.q.numpy(), wl.kv.numpy(), wl.indptr.numpy(),
+                                     wl.ids.numpy(), wl.last.numpy())[seqs]
+    t, got = bench.cpu_baseline_masked(wl, seqs, threads=1, reps=1)
+    assert t > 0 and np.abs(got.numpy() - want).max() < 1e-6
+    if not ragged:
+        tg, ta, tt, got = bench.cpu_baseline_literal(wl, seqs, threads=1, reps=1)
+        assert tg > 0 and ta > 0 and abs(tt - tg - ta) < 1e-9
+        assert np.abs(got.numpy() - want).max() < 2e-6
+        assert bench.max_abs_err(torch.from_numpy(np.zeros((5, 8, 64), np.float16)), got, seqs) \
+            == float(got.abs().max())

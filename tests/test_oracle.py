@@ -207,6 +207,43 @@ def test_literal_padding_is_wrong_for_ragged_batches():
     np.testing.assert_allclose(masked[1], literal[1], atol=1e-6)   # the longest is unaffected
 
 
+
+# ---- the torch restatement of the literal path (bench.py's CPU baseline)
+
+@pytest.mark.parametrize("lens,Hq,Hkv,D", [([48, 48, 48], 8, 2, 64), ([16, 1024, 0, 33], 8, 2, 64),
+                                          ([300, 5], 32, 8, 128), ([17], 4, 4, 64)])
+def test_torch_literal_path_matches_numpy_literal_oracle(lens, Hq, Hkv, D):
+    from oracle import reference_torch as rt
+    q, kv, indptr, ids, last = _paged(lens, Hq, Hkv, D, 16, seed=len(lens) + D)
+    tq, tkv = torch.from_numpy(q), torch.from_numpy(kv)
+    tabs = [torch.from_numpy(a) for a in (indptr, ids, last)]
+    K, V = rt.gather_dense(tkv, *tabs)
+    K0, V0 = ref.gather_paged_to_dense(kv, indptr, ids, last)
+    np.testing.assert_array_equal(K.numpy(), K0)            # a copy: bit-exact
+    np.testing.assert_array_equal(V.numpy(), V0)
+    got = rt.reference_attention_paged_literal(tq, tkv, *tabs).numpy()
+    want = ref.reference_attention_paged(q, kv, indptr, ids, last, literal=True)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+    if len(set(lens)) == 1:      # uniform lengths: also the masked (and SDPA-pinned) form
+        np.testing.assert_allclose(got, ref.reference_attention_paged(q, kv, indptr, ids, last),
+                                   rtol=0, atol=2e-6)
+
+
+def test_torch_literal_path_catches_a_planted_gqa_mistake():
+    # repeat (tile) instead of repeat_interleave puts q head h on kv head h % Hkv
+    from oracle import reference_torch as rt
+    q, kv, indptr, ids, last = _paged([64, 64], 8, 2, 64, 16, seed=5)
+    tabs = [torch.from_numpy(a) for a in (indptr, ids, last)]
+    K, V = rt.gather_dense(torch.from_numpy(kv), *tabs)
+    g = 4
+    k = K.repeat(1, 1, g, 1).permute(0, 2, 3, 1)
+    v = V.repeat(1, 1, g, 1).permute(0, 2, 1, 3)
+    qf = torch.from_numpy(q).float()
+    bad = torch.matmul(torch.softmax(torch.matmul(qf.unsqueeze(2) * 64 ** -0.5, k), -1), v)
+    want = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    assert np.abs(bad.squeeze(2).numpy() - want).max() > 1e-1
+
+
 # ---------------------------------------------------------------- planted mistakes
 
 def _oracle_with_modulo_gqa(q, kv, indptr, ids, last):
