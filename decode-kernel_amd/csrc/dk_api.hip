@@ -1,8 +1,11 @@
 // dk_api.hip — the C ABI of libdk_decode (include/dk_decode.h): argument validation,
 // launch planning and the two passes.
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <atomic>
@@ -41,6 +44,53 @@ int cu_count(int device) {
   if (device < 64) cached[device].store(n, std::memory_order_relaxed);
   return n;
 }
+
+// Trace ranges around the launches, for rocprofv3 --marker-trace: with the environment
+// variable DK_TRACE set (to anything but "" or "0") each pass-1 and merge launch is
+// wrapped in a roctx range naming the pass, the schedule and the shape. The roctx library
+// is opened at the first call that finds DK_TRACE set, so the library does not link it.
+struct Roctx {
+  int (*push)(const char*) = nullptr;
+  int (*pop)() = nullptr;
+};
+
+const Roctx& roctx() {
+  static const Roctx r = [] {
+    Roctx t;
+    const char* e = getenv("DK_TRACE");
+    if (!e || !*e || (e[0] == '0' && !e[1])) return t;
+    for (const char* name : {"librocprofiler-sdk-roctx.so.1", "libroctx64.so.4"}) {
+      void* h = dlopen(name, RTLD_NOW | RTLD_LOCAL);
+      if (!h) continue;
+      t.push = reinterpret_cast<int (*)(const char*)>(dlsym(h, "roctxRangePushA"));
+      t.pop = reinterpret_cast<int (*)()>(dlsym(h, "roctxRangePop"));
+      if (t.push && t.pop) break;
+      t = Roctx{};
+    }
+    return t;
+  }();
+  return r;
+}
+
+// A roctx range for the lifetime of the object (nothing when tracing is off).
+class TraceRange {
+ public:
+  template <class... A>
+  explicit TraceRange(const char* fmt, A... args) : on_(roctx().push != nullptr) {
+    if (!on_) return;
+    char buf[160];
+    snprintf(buf, sizeof(buf), fmt, args...);
+    roctx().push(buf);
+  }
+  ~TraceRange() {
+    if (on_) roctx().pop();
+  }
+  TraceRange(const TraceRange&) = delete;
+  TraceRange& operator=(const TraceRange&) = delete;
+
+ private:
+  bool on_;
+};
 
 const void* pass1_fn(int dtype, const Plan& pl, int d) {
   return dtype == DK_F16 ? pass1_symbol<F16>(d, pl.heads, pl.waves, pl.mfma, pl.kv8, pl.balanced)
@@ -272,7 +322,13 @@ int run(Problem p, bool do_merge, void* stream) {
     L.grid = (int)((units + kXcds - 1) / kXcds * kXcds * pl.chunks);
   }
   L.stream = static_cast<hipStream_t>(stream);
-  hipError_t e = p.dtype == DK_F16 ? launch_pass1<F16>(a, L) : launch_pass1<BF16>(a, L);
+  hipError_t e;
+  {
+    TraceRange tr("dk_pass1 %s B=%d Hq=%d Hkv=%d D=%d split=%d grid=%d waves=%d",
+                  pl.balanced ? "balanced" : (p.split == 1 ? "one-pass" : "split"), p.batch,
+                  p.hq, p.hkv, p.head_dim, p.split, L.grid, L.waves * L.hp);
+    e = p.dtype == DK_F16 ? launch_pass1<F16>(a, L) : launch_pass1<BF16>(a, L);
+  }
   if (e != hipSuccess) return hip_fail(e, "pass-1 launch");
 
   if (do_merge && p.split != 1) {
@@ -295,6 +351,8 @@ int run(Problem p, bool do_merge, void* stream) {
     m.chunks = pl.chunks;
     m.hkv = p.hkv;
     m.waves_per_pair = waves_per_pair;
+    TraceRange tr("dk_merge %s B=%d Hq=%d D=%d", pl.balanced ? "balanced" : "split",
+                  p.batch, p.hq, p.head_dim);
     e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)
                           : launch_merge<BF16>(m, p.head_dim, pl.balanced, L.stream);
     if (e != hipSuccess) return hip_fail(e, "merge launch");
