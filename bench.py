@@ -25,6 +25,9 @@ Modes:
                    sampled sequences
   --single-call    one flush and one call, no settling or warm-up (for rocprofv3 --pmc
                    counter runs, which then see exactly the call's dispatches)
+  --host-overhead  host time per call of the Python entry point attention.decode_attention
+                   (back to back, no flush), against the bare C-ABI call and a call that
+                   validates its arguments afresh (no cached plan)
 
 `value` is achieved algorithmic HBM bandwidth in TB/s (bytes of the reference's model,
 bench/microbench_cuda.py:114-121, plus page tables, divided by the p50 per-call time);
@@ -89,6 +92,8 @@ def parse_args(argv=None):
                     help="run BASELINE.json config N's sweep (one JSON line per point)")
     ap.add_argument("--single-call", action="store_true",
                     help="one flush + one call, no settling / warm-up (counter runs)")
+    ap.add_argument("--host-overhead", action="store_true",
+                    help="host us per call of attention.decode_attention (see the modes)")
     ap.add_argument("--split", type=int, default=0, help="split_kv (0 = automatic)")
     ap.add_argument("--schedule", type=int, default=0,
                     help="split_kv 0: 0 automatic, 1 balanced, 2 one pass")
@@ -114,6 +119,10 @@ def parse_args(argv=None):
                          "per-sequence lengths uniform in [TOKENS, ctx] (seeded), pages "
                          "drawn from a shuffled free list of 65536 pages, q scaled by "
                          "1/sqrt(head_dim)")
+    ap.add_argument("--merge", default="kernel", choices=["fused", "kernel"],
+                    help="where the partials of a split or balanced call are merged: inside "
+                         "pass 1 (one launch, dk_decode_attention_fused) or by the separate "
+                         "merge kernel (dk_decode_attention_ex)")
     ap.add_argument("--no-plan-hint", action="store_true",
                     help="do not pass the host-side max_pages_per_seq plan hint")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -225,7 +234,7 @@ class Caller:
     """One (workload, split_kv, options) through the C ABI, with its own output and
     workspace, and the timing protocol."""
 
-    def __init__(self, lib, dk_lib, attention, wl, split, opts, stream):
+    def __init__(self, lib, dk_lib, attention, wl, split, opts, stream, fused=True):
         torch = wl.torch
         self.lib, self.dk_lib, self.wl, self.split, self.opts, self.stream = \
             lib, dk_lib, wl, split, opts, stream
@@ -233,6 +242,10 @@ class Caller:
         ws_bytes = dk_lib.workspace_bytes(wl.batch, wl.hq, wl.hkv, wl.d, split)
         p_total = dk_lib.partials_layout(wl.batch, wl.hq, wl.d, split)[3] if split else ws_bytes
         self.ws = torch.empty(max(ws_bytes, p_total, 1), dtype=torch.uint8, device=wl.q.device)
+        # fused merge (one launch): zeroed counters that every call leaves zero
+        self.fused = fused
+        n = dk_lib.merge_counters(wl.batch, wl.hq, wl.hkv, wl.d)
+        self.counters = torch.zeros(max(n, 1), dtype=torch.int32, device=wl.q.device)
         self.strides = attention._strides(wl.q, wl.kv, self.out)
         self.code = attention._DTYPE_CODE[wl.dtype]
         self.common = (wl.q.data_ptr(), wl.kv.data_ptr(), wl.indptr.data_ptr(),
@@ -244,6 +257,12 @@ class Caller:
                                              self.code, split, opts)
 
     def full(self):
+        if self.fused:
+            return self.lib.dk_decode_attention_fused(
+                self.common[0], self.common[1], None, *self.common[2:], self.out.data_ptr(),
+                self.ws.data_ptr(), self.ws.numel(), self.counters.data_ptr(),
+                self.counters.numel(), *self.shape, self.split, ctypes.byref(self.opts),
+                self.stream.cuda_stream)
         return self.lib.dk_decode_attention_ex(*self.common, self.out.data_ptr(),
                                                self.ws.data_ptr(), self.ws.numel(), *self.shape,
                                                self.split, ctypes.byref(self.opts),
@@ -255,12 +274,14 @@ class Caller:
                                            self.stream.cuda_stream)
 
     def dominant(self):
-        """The dominant kernel alone: the whole call in one pass, else pass 1."""
-        return self.full if self.schedule == 1 else self.pass1
+        """The dominant kernel alone: the whole call when it is one launch (one pass, or
+        the fused merge), else pass 1."""
+        return self.full if self.schedule == 1 or self.fused else self.pass1
 
     def schedule_name(self):
-        return {1: "one pass"}.get(self.schedule, "balanced + merge" if self.schedule == 0
-                                    else f"split {self.schedule} + merge")
+        merge = "fused merge" if self.fused else "merge kernel"
+        return {1: "one pass"}.get(self.schedule, f"balanced + {merge}" if self.schedule == 0
+                                    else f"split {self.schedule} + {merge}")
 
 
 class Timer:
@@ -388,7 +409,7 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                   kv_dtype=args.kv_dtype)
     split = attention.resolve_split(args.split)
     opts, hint = make_opts(dk_lib, args, wl, split)
-    c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
+    c = Caller(lib, dk_lib, attention, wl, split, opts, stream, fused=args.merge == "fused")
     timer = Timer(torch, dev, stream, args.flush)
     dk_lib.check(c.full(), "decode_attention")
     if args.single_call:
@@ -430,7 +451,7 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                    "batch": wl.batch,
                    "context_length": f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
                    "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d, "page_size": 16,
-                   "split_kv": split, "schedule": c.schedule_name(),
+                   "split_kv": split, "schedule": c.schedule_name(), "merge": args.merge,
                    "plan_hint_max_pages": hint,
                    "qk_path": "mfma" if mfma_qk else "valu", "pv_path": "mfma"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
@@ -506,7 +527,8 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
             cpu_s, want = cpu_baseline_masked(wl, seqs, threads, reps=1)
         for split in splits:
             opts, hint = make_opts(dk_lib, args, wl, split)
-            c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
+            c = Caller(lib, dk_lib, attention, wl, split, opts, stream,
+                       fused=args.merge == "fused")
             dk_lib.check(c.full(), "decode_attention")
             if not settled:
                 timer.settle(c.full)
@@ -528,7 +550,7 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                                f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
                            "num_q_heads": wl.hq, "num_kv_heads": wl.hkv, "head_dim": wl.d,
                            "split_kv": split, "schedule": c.schedule_name(),
-                           "plan_hint_max_pages": hint},
+                           "merge": args.merge, "plan_hint_max_pages": hint},
                 "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
                 "frac": round(tbs * 1e12 / (PEAK_GBPS * 1e9), 4),
                 "pct_of_peak": round(100 * tbs * 1e12 / (PEAK_GBPS * 1e9), 2),
@@ -545,6 +567,46 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                               f"sequences {seqs}, one run"}
             print(json.dumps(rec), flush=True)
             del c
+
+
+def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
+    """Host microseconds per call, issued back to back (no flush, no sync inside the
+    timed loop; the GPU runs behind): the bare C-ABI call with prebuilt arguments, the
+    Python entry point with its cached plan, and the Python entry point validating its
+    arguments afresh on every call (its cache cleared), as every call did before."""
+    wl = Workload(torch, layout, dev, args.batch, args.ctx, args.num_q_heads,
+                  args.num_kv_heads, args.head_dim, args.dtype, args.page_table)
+    split = attention.resolve_split(args.split)
+    opts, hint = make_opts(dk_lib, args, wl, split)
+    c = Caller(lib, dk_lib, attention, wl, split, opts, stream, fused=False)
+    q, kv, ip, ids, last = wl.q, wl.kv, wl.indptr, wl.ids, wl.last
+
+    def py():
+        return attention.decode_attention(q, kv, ip, ids, last, split_kv=split,
+                                          max_pages_per_seq=hint)
+
+    def py_fresh():
+        attention._PLANS.clear()
+        return py()
+
+    res = {}
+    for name, fn in (("c_abi", c.full), ("decode_attention", py),
+                     ("decode_attention_unplanned", py_fresh)):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        n = 200
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        t = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        res[name] = round(t / n * 1e6, 2)
+    print(json.dumps({"metric": "host us per decode call (issue only, back to back)",
+                      "unit": "us", "config": {"workload": wl.label(), "split_kv": split,
+                                               "plan_hint_max_pages": hint,
+                                               "schedule": c.schedule_name()},
+                      "host_us_per_call": res}), flush=True)
 
 
 def main(argv=None):
@@ -564,7 +626,9 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
-    if args.config:
+    if args.host_overhead:
+        host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
+    elif args.config:
         config_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
     else:
         metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream)

@@ -197,6 +197,106 @@ def choose_split(q: torch.Tensor, kv_data: torch.Tensor, kv_indices: torch.Tenso
                                _DTYPE_CODE[q.dtype], avg, q.device.index or 0)
 
 
+def _tensor_sig(t):
+    """What the host-side checks of one tensor argument depend on."""
+    return (t.shape, t.stride(), t.dtype, t.device)
+
+
+def _kv_sig(kv_data):
+    if isinstance(kv_data, torch.Tensor):
+        return _tensor_sig(kv_data)
+    if isinstance(kv_data, (tuple, list)) and len(kv_data) == 2 and \
+            all(isinstance(t, torch.Tensor) for t in kv_data):
+        return (_tensor_sig(kv_data[0]), _tensor_sig(kv_data[1]))
+    return None          # not cacheable: the slow path raises the type error
+
+
+class _CallPlan:
+    """Everything decode_attention derives from its arguments' shapes, dtypes, devices,
+    strides and options -- validated once, then reused by every call with the same
+    signature (a model's layers share one): the ctypes argument tuple (strides and options
+    structs included), the scratch sizes, the entry point."""
+
+    __slots__ = ("shape", "ws_need", "n_counters", "split_kv", "pair", "contig", "out_shape",
+                 "dtype", "device", "batch")
+
+    def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, out,
+                 workspace, counters, qk_path, waves_per_group, waves_per_cu, schedule,
+                 max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window):
+        kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+        if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale <= 0.0):
+            _fail(f"sm_scale must be finite and > 0, got {sm_scale}")
+        kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
+        cap = _logit_cap(logit_cap)
+        win = _window(window)
+        split = resolve_split(split_kv)
+        batch, hq, d = q.shape
+        if out is not None and (out.shape != q.shape or out.dtype != q.dtype or
+                                out.device != q.device or out.stride(2) != 1):
+            _fail("out must match q's shape, dtype and device with unit head_dim stride")
+        self.batch, self.out_shape, self.dtype, self.device = batch, (batch, hq, d), q.dtype, \
+            q.device
+        self.split_kv = split
+        self.pair = kv.v is not None
+        self.contig = (kv_indptr.is_contiguous(), kv_indices.is_contiguous(),
+                       kv_last_page_len.is_contiguous())
+        self.ws_need = dk_lib.workspace_bytes(batch, hq, kv.hkv, d, split) if batch else 0
+        if self.ws_need and workspace is not None and (
+                workspace.numel() * workspace.element_size() < self.ws_need or
+                workspace.device != q.device):
+            _fail(f"workspace must hold {self.ws_need} bytes on {q.device}")
+        self.n_counters = dk_lib.merge_counters(batch, hq, kv.hkv, d) if batch else 0
+        if counters is not None:
+            if workspace is None:
+                _fail("counters go with a caller workspace (without one the library uses "
+                      "its own workspace and counters)")
+            if counters.dtype != torch.int32 or counters.device != q.device or \
+                    counters.numel() < self.n_counters or not counters.is_contiguous():
+                _fail(f"counters must be a contiguous int32 tensor of at least "
+                      f"{self.n_counters} elements on {q.device}")
+        strides = dk_lib.DkStrides()
+        strides.q_b, strides.q_h = q.stride(0), q.stride(1)
+        strides.kv_p, strides.kv_r, strides.kv_s, strides.kv_h = kv.strides
+        # out's strides: those of the caller's out, else of a fresh contiguous tensor
+        strides.o_b, strides.o_h = (out.stride(0), out.stride(1)) if out is not None else \
+            (hq * d, d)
+        opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule,
+                              max_pages_per_seq, sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap, win)
+        self.shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
+                      _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts),
+                      strides, opts)      # the structs last, kept alive with the plan
+
+
+class _LibraryScratch:
+    """The workspace the library owns for calls made without a caller workspace, one per
+    (device, stream): a call allocates only when its problem outgrows it (calls on one
+    stream never overlap, and a replaced buffer is freed in stream order). Calls under
+    graph capture do not use it (a captured call keeps its own; see decode_attention)."""
+
+    def __init__(self):
+        self._by_stream = {}
+
+    def get(self, device, stream: int, ws_need: int):
+        key = (device, stream)
+        ws = self._by_stream.get(key)
+        if ws is None or ws.numel() < ws_need:
+            ws = self._by_stream[key] = torch.empty(ws_need, dtype=torch.uint8, device=device)
+        return ws
+
+
+_SCRATCH = _LibraryScratch()
+_PLANS: dict = {}
+_PLANS_MAX = 512
+
+
+def _raw_stream(device) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    try:
+        return torch._C._cuda_getCurrentRawStream(device.index)
+    except (AttributeError, TypeError):
+        return torch.cuda.current_stream(device).cuda_stream
+
+
 def decode_attention(
     q: torch.Tensor,
     kv_data: torch.Tensor,
@@ -207,6 +307,7 @@ def decode_attention(
     *,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
+    counters: Optional[torch.Tensor] = None,
     qk_path: int = 0,
     waves_per_group: int = 0,
     waves_per_cu: int = 0,
@@ -235,7 +336,16 @@ def decode_attention(
                            one-pass kernel when batch * kv heads fills the device, else the
                            balanced schedule (equal pages per workgroup) + merge.
         out, workspace   : optional preallocated output (batch, num_q_heads, head_dim) and
-                           uint8 scratch of dk_lib.workspace_bytes(...) bytes
+                           uint8 scratch of dk_lib.workspace_bytes(...) bytes. Without a
+                           workspace the library uses its own (one per device and stream,
+                           grown as needed); under graph capture it allocates one for the
+                           captured call.
+        counters         : with a caller workspace: int32 counters of at least
+                           dk_lib.merge_counters(...) elements, zero before the first use
+                           (every call leaves them zero): the merge then runs inside pass 1
+                           (dk_decode_attention_fused, one kernel launch). Without them the
+                           merge kernel runs after pass 1, which measured faster on MI355X
+                           for every explicit split and small batch.
         qk_path, waves_per_group, waves_per_cu, schedule : tuning knobs (0 =
                            defaults; qk_path 1 = MFMA q.k, 2 = VALU q.k, 0 = VALU up to
                            4 q heads per kv head and MFMA (up to 16 heads per wavefront)
@@ -253,52 +363,80 @@ def decode_attention(
                            sequence (the new one and window - 1 before it; Mistral,
                            Gemma); None or 0 = all tokens
 
+    The argument checks run once per call signature (shapes, strides, dtypes, devices and
+    options); later calls with the same signature reuse the validated plan, so a model's
+    layers pay only for the pointers and the library call.
+
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
     """
-    kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
-    if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale <= 0.0):
-        _fail(f"sm_scale must be finite and > 0, got {sm_scale}")
-    kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
-    cap = _logit_cap(logit_cap)
-    win = _window(window)
+    kvs = _kv_sig(kv_data) if isinstance(q, torch.Tensor) else None
+    key = None
+    if kvs is not None and all(isinstance(t, torch.Tensor) for t in
+                               (kv_indptr, kv_indices, kv_last_page_len)):
+        key = (_tensor_sig(q), kvs, _tensor_sig(kv_indptr), _tensor_sig(kv_indices),
+               _tensor_sig(kv_last_page_len),
+               None if out is None else _tensor_sig(out),
+               None if workspace is None else (workspace.numel() * workspace.element_size(),
+                                               workspace.device),
+               None if counters is None else _tensor_sig(counters),
+               split_kv, qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
+               sm_scale, k_scale, v_scale, logit_cap, window)
+    plan = _PLANS.get(key) if key is not None else None
+    if plan is None:
+        plan = _CallPlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, out,
+                         workspace, counters, qk_path, waves_per_group, waves_per_cu, schedule,
+                         max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window)
+        if key is not None:
+            if len(_PLANS) >= _PLANS_MAX:
+                _PLANS.clear()
+            _PLANS[key] = plan
     lib = dk_lib.load()
-    split = resolve_split(split_kv)
-    batch, hq, d = q.shape
     if out is None:
-        out = torch.empty((batch, hq, d), dtype=q.dtype, device=q.device)
-    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or \
-            out.stride(2) != 1:
-        _fail("out must match q's shape, dtype and device with unit head_dim stride")
-    if batch == 0:
+        out = torch.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
+    if plan.batch == 0:
         return out
-    kv_indptr = _contig1d(kv_indptr)
-    kv_indices = _contig1d(kv_indices)
-    kv_last_page_len = _contig1d(kv_last_page_len)
-    ws_need = dk_lib.workspace_bytes(batch, hq, kv.hkv, d, split)
-    if ws_need:
-        if workspace is None:
-            workspace = torch.empty(ws_need, dtype=torch.uint8, device=q.device)
-        elif workspace.numel() * workspace.element_size() < ws_need or \
-                workspace.device != q.device:
-            _fail(f"workspace must hold {ws_need} bytes on {q.device}")
-    ws_ptr = workspace.data_ptr() if ws_need else None
-    ws_bytes = workspace.numel() * workspace.element_size() if ws_need else 0
-    strides = _strides(q, kv_data, out)
-    opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
-                          sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap, win)
-    shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
-             _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts))
-    tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
-              out.data_ptr(), ws_ptr, ws_bytes)
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        if kv.v is None:
-            rc = lib.dk_decode_attention_ex(q.data_ptr(), kv.k.data_ptr(), *tables, *shape,
-                                            stream)
+    if not all(plan.contig):
+        kv_indptr, kv_indices, kv_last_page_len = (
+            _contig1d(kv_indptr), _contig1d(kv_indices), _contig1d(kv_last_page_len))
+    dev = plan.device
+    switch = dev.index != torch.cuda.current_device()
+    if switch:
+        prev = torch.cuda.current_device()
+        torch.cuda.set_device(dev)
+    try:
+        stream = _raw_stream(dev)
+        ctr = counters
+        if plan.ws_need and workspace is None:
+            if torch.cuda.is_current_stream_capturing():
+                # a captured call keeps this allocation (the graph's pool)
+                workspace = torch.empty(plan.ws_need, dtype=torch.uint8, device=dev)
+            else:
+                workspace = _SCRATCH.get(dev, stream, plan.ws_need)
+            # pass the bytes this call needs, not the buffer's size (grown by earlier,
+            # larger calls), so that what a workspace size can steer (the explicit splits
+            # of a sliding window) never depends on history
+            ws_ptr, ws_bytes = workspace.data_ptr(), plan.ws_need
+        elif plan.ws_need:
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
         else:
-            rc = lib.dk_decode_attention_kv(q.data_ptr(), kv.k.data_ptr(), kv.v.data_ptr(),
-                                            *tables, *shape, stream)
+            ws_ptr, ws_bytes, ctr = None, 0, None
+        k, v = (kv_data[0], kv_data[1]) if plan.pair else (kv_data, None)
+        tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
+                  out.data_ptr(), ws_ptr, ws_bytes)
+        if ctr is not None:
+            rc = lib.dk_decode_attention_fused(
+                q.data_ptr(), k.data_ptr(), None if v is None else v.data_ptr(), *tables,
+                ctr.data_ptr(), ctr.numel(), *plan.shape[:11], stream)
+        elif v is None:
+            rc = lib.dk_decode_attention_ex(q.data_ptr(), k.data_ptr(), *tables,
+                                            *plan.shape[:11], stream)
+        else:
+            rc = lib.dk_decode_attention_kv(q.data_ptr(), k.data_ptr(), v.data_ptr(), *tables,
+                                            *plan.shape[:11], stream)
+    finally:
+        if switch:
+            torch.cuda.set_device(prev)
     dk_lib.check(rc, "decode_attention")
     return out
 

@@ -297,13 +297,15 @@ class SplitKVHipBackend(_backend_base()):
         return kb[:pages * PAGE_SIZE].view(shape), vb[:pages * PAGE_SIZE].view(shape)
 
     def _workspace_for(self, q, hkv):
-        """Scratch for one decode call. Eager calls share one buffer that grows with the
-        batch. A call under graph capture gets the graph workspace instead: its address is
-        baked into the graph and every replay writes there, so it is sized once for the
-        graph state's largest batch, never handed to eager calls, and never freed while
-        the backend lives (one outgrown by a later capture is kept too)."""
+        """Scratch for one decode call (None when the call needs none). Eager calls share
+        one buffer that grows with the batch. A call under graph capture gets the graph
+        workspace instead: its address is baked into the graph and every replay writes
+        there, so it is sized once for the graph state's largest batch, never handed to
+        eager calls, and never freed while the backend lives (one outgrown by a later
+        capture is kept too)."""
         split = attention.resolve_split(self.split_kv)
-        need = attention.dk_lib.workspace_bytes(q.shape[0], q.shape[1], hkv, q.shape[2], split)
+        bs, hq, d = q.shape
+        need = attention.dk_lib.workspace_bytes(bs, hq, hkv, d, split)
         if need == 0:
             return None
         if torch.cuda.is_current_stream_capturing():
@@ -311,8 +313,8 @@ class SplitKVHipBackend(_backend_base()):
             if ws is None or ws.numel() < need or ws.device != q.device:
                 if ws is not None:
                     self._retired_graph_workspaces.append(ws)
-                most = attention.dk_lib.workspace_bytes(
-                    max(q.shape[0], self._graph_max_bs), q.shape[1], hkv, q.shape[2], split)
+                most = attention.dk_lib.workspace_bytes(max(bs, self._graph_max_bs), hq, hkv,
+                                                        d, split)
                 ws = self._graph_workspace = torch.empty(max(need, most), dtype=torch.uint8,
                                                          device=q.device)
             return ws
