@@ -119,10 +119,6 @@ def parse_args(argv=None):
                          "per-sequence lengths uniform in [TOKENS, ctx] (seeded), pages "
                          "drawn from a shuffled free list of 65536 pages, q scaled by "
                          "1/sqrt(head_dim)")
-    ap.add_argument("--merge", default="kernel", choices=["fused", "kernel"],
-                    help="where the partials of a split or balanced call are merged: inside "
-                         "pass 1 (one launch, dk_decode_attention_fused) or by the separate "
-                         "merge kernel (dk_decode_attention_ex)")
     ap.add_argument("--no-plan-hint", action="store_true",
                     help="do not pass the host-side max_pages_per_seq plan hint")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -234,7 +230,7 @@ class Caller:
     """One (workload, split_kv, options) through the C ABI, with its own output and
     workspace, and the timing protocol."""
 
-    def __init__(self, lib, dk_lib, attention, wl, split, opts, stream, fused=True):
+    def __init__(self, lib, dk_lib, attention, wl, split, opts, stream):
         torch = wl.torch
         self.lib, self.dk_lib, self.wl, self.split, self.opts, self.stream = \
             lib, dk_lib, wl, split, opts, stream
@@ -242,10 +238,6 @@ class Caller:
         ws_bytes = dk_lib.workspace_bytes(wl.batch, wl.hq, wl.hkv, wl.d, split)
         p_total = dk_lib.partials_layout(wl.batch, wl.hq, wl.d, split)[3] if split else ws_bytes
         self.ws = torch.empty(max(ws_bytes, p_total, 1), dtype=torch.uint8, device=wl.q.device)
-        # fused merge (one launch): zeroed counters that every call leaves zero
-        self.fused = fused
-        n = dk_lib.merge_counters(wl.batch, wl.hq, wl.hkv, wl.d)
-        self.counters = torch.zeros(max(n, 1), dtype=torch.int32, device=wl.q.device)
         self.strides = attention._strides(wl.q, wl.kv, self.out)
         self.code = attention._DTYPE_CODE[wl.dtype]
         self.common = (wl.q.data_ptr(), wl.kv.data_ptr(), wl.indptr.data_ptr(),
@@ -257,12 +249,6 @@ class Caller:
                                              self.code, split, opts)
 
     def full(self):
-        if self.fused:
-            return self.lib.dk_decode_attention_fused(
-                self.common[0], self.common[1], None, *self.common[2:], self.out.data_ptr(),
-                self.ws.data_ptr(), self.ws.numel(), self.counters.data_ptr(),
-                self.counters.numel(), *self.shape, self.split, ctypes.byref(self.opts),
-                self.stream.cuda_stream)
         return self.lib.dk_decode_attention_ex(*self.common, self.out.data_ptr(),
                                                self.ws.data_ptr(), self.ws.numel(), *self.shape,
                                                self.split, ctypes.byref(self.opts),
@@ -274,14 +260,12 @@ class Caller:
                                            self.stream.cuda_stream)
 
     def dominant(self):
-        """The dominant kernel alone: the whole call when it is one launch (one pass, or
-        the fused merge), else pass 1."""
-        return self.full if self.schedule == 1 or self.fused else self.pass1
+        """The dominant kernel alone: the whole call in one pass, else pass 1."""
+        return self.full if self.schedule == 1 else self.pass1
 
     def schedule_name(self):
-        merge = "fused merge" if self.fused else "merge kernel"
-        return {1: "one pass"}.get(self.schedule, f"balanced + {merge}" if self.schedule == 0
-                                    else f"split {self.schedule} + {merge}")
+        return {1: "one pass"}.get(self.schedule, "balanced + merge" if self.schedule == 0
+                                    else f"split {self.schedule} + merge")
 
 
 class Timer:
@@ -409,7 +393,7 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                   kv_dtype=args.kv_dtype)
     split = attention.resolve_split(args.split)
     opts, hint = make_opts(dk_lib, args, wl, split)
-    c = Caller(lib, dk_lib, attention, wl, split, opts, stream, fused=args.merge == "fused")
+    c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
     timer = Timer(torch, dev, stream, args.flush)
     dk_lib.check(c.full(), "decode_attention")
     if args.single_call:
@@ -451,7 +435,7 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                    "batch": wl.batch,
                    "context_length": f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
                    "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d, "page_size": 16,
-                   "split_kv": split, "schedule": c.schedule_name(), "merge": args.merge,
+                   "split_kv": split, "schedule": c.schedule_name(),
                    "plan_hint_max_pages": hint,
                    "qk_path": "mfma" if mfma_qk else "valu", "pv_path": "mfma"},
         "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
@@ -527,8 +511,7 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
             cpu_s, want = cpu_baseline_masked(wl, seqs, threads, reps=1)
         for split in splits:
             opts, hint = make_opts(dk_lib, args, wl, split)
-            c = Caller(lib, dk_lib, attention, wl, split, opts, stream,
-                       fused=args.merge == "fused")
+            c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
             dk_lib.check(c.full(), "decode_attention")
             if not settled:
                 timer.settle(c.full)
@@ -550,7 +533,7 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                                f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
                            "num_q_heads": wl.hq, "num_kv_heads": wl.hkv, "head_dim": wl.d,
                            "split_kv": split, "schedule": c.schedule_name(),
-                           "merge": args.merge, "plan_hint_max_pages": hint},
+                           "plan_hint_max_pages": hint},
                 "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
                 "frac": round(tbs * 1e12 / (PEAK_GBPS * 1e9), 4),
                 "pct_of_peak": round(100 * tbs * 1e12 / (PEAK_GBPS * 1e9), 2),
@@ -578,7 +561,7 @@ def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                   args.num_kv_heads, args.head_dim, args.dtype, args.page_table)
     split = attention.resolve_split(args.split)
     opts, hint = make_opts(dk_lib, args, wl, split)
-    c = Caller(lib, dk_lib, attention, wl, split, opts, stream, fused=False)
+    c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
     q, kv, ip, ids, last = wl.q, wl.kv, wl.indptr, wl.ids, wl.last
 
     def py():

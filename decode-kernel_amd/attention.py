@@ -217,11 +217,11 @@ class _CallPlan:
     signature (a model's layers share one): the ctypes argument tuple (strides and options
     structs included), the scratch sizes, the entry point."""
 
-    __slots__ = ("shape", "ws_need", "n_counters", "split_kv", "pair", "contig", "out_shape",
-                 "dtype", "device", "batch")
+    __slots__ = ("shape", "ws_need", "split_kv", "pair", "contig", "out_shape", "dtype",
+                 "device", "batch")
 
     def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, out,
-                 workspace, counters, qk_path, waves_per_group, waves_per_cu, schedule,
+                 workspace, qk_path, waves_per_group, waves_per_cu, schedule,
                  max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window):
         kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
         if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale <= 0.0):
@@ -245,15 +245,6 @@ class _CallPlan:
                 workspace.numel() * workspace.element_size() < self.ws_need or
                 workspace.device != q.device):
             _fail(f"workspace must hold {self.ws_need} bytes on {q.device}")
-        self.n_counters = dk_lib.merge_counters(batch, hq, kv.hkv, d) if batch else 0
-        if counters is not None:
-            if workspace is None:
-                _fail("counters go with a caller workspace (without one the library uses "
-                      "its own workspace and counters)")
-            if counters.dtype != torch.int32 or counters.device != q.device or \
-                    counters.numel() < self.n_counters or not counters.is_contiguous():
-                _fail(f"counters must be a contiguous int32 tensor of at least "
-                      f"{self.n_counters} elements on {q.device}")
         strides = dk_lib.DkStrides()
         strides.q_b, strides.q_h = q.stride(0), q.stride(1)
         strides.kv_p, strides.kv_r, strides.kv_s, strides.kv_h = kv.strides
@@ -307,7 +298,6 @@ def decode_attention(
     *,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
-    counters: Optional[torch.Tensor] = None,
     qk_path: int = 0,
     waves_per_group: int = 0,
     waves_per_cu: int = 0,
@@ -340,12 +330,6 @@ def decode_attention(
                            workspace the library uses its own (one per device and stream,
                            grown as needed); under graph capture it allocates one for the
                            captured call.
-        counters         : with a caller workspace: int32 counters of at least
-                           dk_lib.merge_counters(...) elements, zero before the first use
-                           (every call leaves them zero): the merge then runs inside pass 1
-                           (dk_decode_attention_fused, one kernel launch). Without them the
-                           merge kernel runs after pass 1, which measured faster on MI355X
-                           for every explicit split and small batch.
         qk_path, waves_per_group, waves_per_cu, schedule : tuning knobs (0 =
                            defaults; qk_path 1 = MFMA q.k, 2 = VALU q.k, 0 = VALU up to
                            4 q heads per kv head and MFMA (up to 16 heads per wavefront)
@@ -379,13 +363,12 @@ def decode_attention(
                None if out is None else _tensor_sig(out),
                None if workspace is None else (workspace.numel() * workspace.element_size(),
                                                workspace.device),
-               None if counters is None else _tensor_sig(counters),
                split_kv, qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
                sm_scale, k_scale, v_scale, logit_cap, window)
     plan = _PLANS.get(key) if key is not None else None
     if plan is None:
         plan = _CallPlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, out,
-                         workspace, counters, qk_path, waves_per_group, waves_per_cu, schedule,
+                         workspace, qk_path, waves_per_group, waves_per_cu, schedule,
                          max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window)
         if key is not None:
             if len(_PLANS) >= _PLANS_MAX:
@@ -406,7 +389,6 @@ def decode_attention(
         torch.cuda.set_device(dev)
     try:
         stream = _raw_stream(dev)
-        ctr = counters
         if plan.ws_need and workspace is None:
             if torch.cuda.is_current_stream_capturing():
                 # a captured call keeps this allocation (the graph's pool)
@@ -420,15 +402,11 @@ def decode_attention(
         elif plan.ws_need:
             ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
         else:
-            ws_ptr, ws_bytes, ctr = None, 0, None
+            ws_ptr, ws_bytes = None, 0
         k, v = (kv_data[0], kv_data[1]) if plan.pair else (kv_data, None)
         tables = (kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(),
                   out.data_ptr(), ws_ptr, ws_bytes)
-        if ctr is not None:
-            rc = lib.dk_decode_attention_fused(
-                q.data_ptr(), k.data_ptr(), None if v is None else v.data_ptr(), *tables,
-                ctr.data_ptr(), ctr.numel(), *plan.shape[:11], stream)
-        elif v is None:
+        if v is None:
             rc = lib.dk_decode_attention_ex(q.data_ptr(), k.data_ptr(), *tables,
                                             *plan.shape[:11], stream)
         else:

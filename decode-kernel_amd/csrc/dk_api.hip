@@ -302,9 +302,6 @@ int run(Problem p, bool do_merge, void* stream) {
   a.cap_in = p.opt.logit_cap > 0.f ? score_scale / p.opt.logit_cap : 0.f;
   a.cap_out = p.opt.logit_cap > 0.f ? kLog2e * p.opt.logit_cap : 0.f;
   a.vscale = kv8 && p.opt.v_scale != 0.f ? p.opt.v_scale : 1.f;
-  // fused merge: whenever a full call leaves partials to merge
-  const bool fused = p.counters && p.need_out && p.split != 1;
-  a.counters = fused ? p.counters : nullptr;
   // every launch that can store partials has them (or the library is inconsistent)
   if ((pl.balanced || !direct) && (!a.part_o || !a.part_m || !a.part_l))
     return set_error(DK_EWORKSPACE, "internal: partials not assigned for this schedule");
@@ -334,7 +331,7 @@ int run(Problem p, bool do_merge, void* stream) {
   }
   if (e != hipSuccess) return hip_fail(e, "pass-1 launch");
 
-  if (do_merge && p.split != 1 && !fused) {
+  if (do_merge && p.split != 1) {
     MergeArgs m{};
     m.po = a.part_o;
     m.pm = a.part_m;
@@ -516,31 +513,6 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
                            workspace_bytes, batch, num_q_heads, num_kv_heads, head_dim,
                            page_size, num_pages, num_indices, dtype, strides, split_kv, opts,
                            true);
-  return dk::run(p, true, hip_stream);
-}
-
-size_t dk_merge_counters(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                         int32_t head_dim) {
-  return dk::merge_counters(batch, num_q_heads, num_kv_heads, head_dim);
-}
-
-int dk_decode_attention_fused(const void* q, const void* k_cache, const void* v_cache,
-                              const int32_t* kv_indptr, const int32_t* kv_indices,
-                              const int32_t* kv_last_page_len, void* out, void* workspace,
-                              size_t workspace_bytes, uint32_t* counters, size_t num_counters,
-                              int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                              int32_t head_dim, int32_t page_size, int64_t num_pages,
-                              int64_t num_indices, int32_t dtype, const dk_strides* strides,
-                              int32_t split_kv, const dk_options* opts, void* hip_stream) {
-  dk::clear_error();
-  if (!strides) return dk::set_error(DK_ENULL, "strides must be non-NULL");
-  if (batch > 0 && !counters) return dk::set_error(DK_ENULL, "counters must be non-NULL");
-  Problem p = make_problem(q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, out,
-                           workspace, workspace_bytes, batch, num_q_heads, num_kv_heads,
-                           head_dim, page_size, num_pages, num_indices, dtype, strides, split_kv,
-                           opts, true);
-  p.counters = counters;
-  p.num_counters = num_counters;
   return dk::run(p, true, hip_stream);
 }
 

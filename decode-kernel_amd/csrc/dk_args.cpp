@@ -92,14 +92,6 @@ int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) 
   return rows;
 }
 
-size_t merge_counters(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) {
-  if (!valid_shape(batch, hq, hkv, head_dim)) return 0;
-  int64_t n = 0;
-  for (bool mfma : {false, true})
-    n = std::max<int64_t>(n, (int64_t)batch * hkv * head_chunks(hq / hkv, head_dim, mfma).chunks);
-  return (size_t)n;
-}
-
 size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split) {
   if (!valid_shape(batch, hq, hkv, head_dim) || split < 0 || batch == 0 || split == 1) return 0;
   const int64_t rows = split == 0 ? balanced_rows(batch, hq, hkv, head_dim)
@@ -255,14 +247,6 @@ int validate(const Problem& p) {
                        p.workspace_bytes);
     if (((uintptr_t)p.workspace % 256) != 0)
       return set_error(DK_EWORKSPACE, "workspace must be 256-byte aligned");
-  }
-  if (p.counters) {
-    const size_t need = merge_counters(p.batch, p.hq, p.hkv, p.head_dim);
-    if (p.num_counters < need)
-      return set_error(DK_EWORKSPACE, "%zu merge counters required, %zu given", need,
-                       p.num_counters);
-    if (((uintptr_t)p.counters % 4) != 0)
-      return set_error(DK_EWORKSPACE, "merge counters must be 4-byte aligned");
   }
   return DK_OK;
 }

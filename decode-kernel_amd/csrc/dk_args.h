@@ -73,8 +73,6 @@ struct Problem {
   int32_t split = 0;          // 0: balanced persistent mode; >= 1: explicit split
   bool need_out = true;       // false for the pass-1-only entry point
   dk_options opt{};
-  uint32_t* counters = nullptr;   // fused merge (dk_decode_attention_fused), or null
-  size_t num_counters = 0;
 };
 
 // Launch shape derived from a problem.
@@ -131,9 +129,6 @@ void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t*
 // (max(kMaxWaves, pairs_per_seq) + batch*pairs_per_seq) * heads.
 int64_t split_rows(int32_t batch, int32_t hq, int32_t split);
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim);
-// Counters of the fused merge: one per (sequence, kv head, head chunk) for either q.k
-// path (0 on invalid shapes).
-size_t merge_counters(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim);
 // Workspace of dk_decode_attention: split 1 -> 0, split > 1 -> explicit partials,
 // split 0 -> balanced partials. 0 on invalid shapes.
 size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split);

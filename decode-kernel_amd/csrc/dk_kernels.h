@@ -116,9 +116,6 @@ struct Pass1Args {
   float cap_in, cap_out;              // logit soft-cap: x = cap_out * tanh(q.k * cap_in)
                                       // (cap_out == 0: off, x = q.k * kscale)
   float vscale;                       // V dequant scale (1 unless the cache is fp8)
-  uint32_t* counters;                 // fused merge: one counter per (sequence, kv head,
-                                      // head chunk), zero between calls; null: the merge
-                                      // kernel runs after pass 1
 };
 
 struct MergeArgs {
@@ -318,22 +315,9 @@ __device__ __forceinline__ void ld_words_cached(u32* dst, const uint8_t* p) {
 #pragma unroll
   for (int k = 0; k < NWORDS; ++k) dst[k] = reinterpret_cast<const u32*>(p)[k];
 }
-// Partials (O, m, l) for the merge kernel are plain stores (it reads them after the launch
-// has ended). For the fused merge (dev) they are stored at device scope -- relaxed
-// agent-scope atomic stores, written through to where every XCD's device-scope loads see
-// them once the store has completed -- so that a workgroup of the same launch can merge
-// them without an L2 writeback. (Device scope always measured 0.5-0.7 us slower per call
-// at small sizes: the stores then complete only once written through.)
-__device__ __forceinline__ void st_part(float* p, float x, bool dev) {
-  if (dev) __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else *p = x;
-}
 template <int N>
-__device__ __forceinline__ void st_part_floats(float* p, const float* v, bool dev) {
-  if (dev) {
-#pragma unroll
-    for (int k = 0; k < N; ++k) __hip_atomic_store(p + k, v[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else if constexpr (N % 4 == 0) {
+__device__ __forceinline__ void st_floats(float* p, const float* v) {
+  if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int k = 0; k < N / 4; ++k)
       reinterpret_cast<f32x4*>(p)[k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
@@ -341,13 +325,6 @@ __device__ __forceinline__ void st_part_floats(float* p, const float* v, bool de
 #pragma unroll
     for (int k = 0; k < N; ++k) p[k] = v[k];
   }
-}
-// Loads of partials: plain (the separate merge kernel, after pass 1 has ended) or at
-// device scope (the fused merge, inside the pass-1 launch that stored them).
-template <bool DEV>
-__device__ __forceinline__ float ld_part(const float* p) {
-  if constexpr (DEV) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *p;
 }
 
 // Clamped CSR range of sequence b (so that no access leaves kv_indices).
@@ -871,7 +848,6 @@ struct Wave {
   // (reference semantics: m = max score in natural units or -1e9 if nothing was seen,
   // l = sum exp(s - m), O = sum exp(s - m) V).
   __device__ __forceinline__ void store_partial(const Pass1Args& a, int64_t row0, int64_t hstride) {
-    const bool dev = a.counters != nullptr;   // read by the fused merge of this launch
     float f[NS];
 #pragma unroll
     for (int ss = 0; ss < NS; ++ss)
@@ -885,14 +861,14 @@ struct Wave {
           float v[DPL];
 #pragma unroll
           for (int j = 0; j < DPL; ++j) v[j] = acc[i][j] * fh;
-          st_part_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v, dev);
+          st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
         }
       }
       if (r16 == 0 && c < hv) {
         const int64_t r = row0 + (int64_t)c * hstride;
         const bool seen = mtrue[0] > kNegInf;
-        st_part(a.part_m + r, seen ? mtrue[0] * kLn2 : kEmptyM, dev);
-        st_part(a.part_l + r, lsum[0] * f[0], dev);
+        a.part_m[r] = seen ? mtrue[0] * kLn2 : kEmptyM;
+        a.part_l[r] = lsum[0] * f[0];
       }
     } else {
       static_for<KR>([&](auto kc) {
@@ -903,7 +879,7 @@ struct Wave {
           float v[DPL];
 #pragma unroll
           for (int j = 0; j < DPL; ++j) v[j] = row_head<k>(j) * fh;
-          st_part_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v, dev);
+          st_floats<DPL>(a.part_o + (row0 + h * hstride) * D + c * DPL, v);
         }
       });
       if (r16 == 0 && c < GQ) {
@@ -912,8 +888,8 @@ struct Wave {
           if (ss * GQ + c >= hv) continue;
           const int64_t r = row0 + (int64_t)(ss * GQ + c) * hstride;
           const bool seen = mtrue[ss] > kNegInf;
-          st_part(a.part_m + r, seen ? mtrue[ss] * kLn2 : kEmptyM, dev);
-          st_part(a.part_l + r, lsum[ss] * f[ss], dev);
+          a.part_m[r] = seen ? mtrue[ss] * kLn2 : kEmptyM;
+          a.part_l[r] = lsum[ss] * f[ss];
         }
       }
     }
@@ -1144,7 +1120,6 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
       }
     }
     __syncthreads();
-    const bool dev = a.counters != nullptr;   // read by the fused merge of this launch
     for (int idx = tid; idx < wv.hv * D; idx += NW * 64) {
       const int h = idx / D, d = idx % D;
       float mt = kNegInf;
@@ -1164,10 +1139,10 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
         T::store(out + (int64_t)h * o_h + 2 * d, L > 0.f ? O / L : 0.f);
       } else {
         const int64_t row = prow0 + h * phstride;
-        st_part(a.part_o + row * D + d, empty ? 0.f : O, dev);
+        a.part_o[row * D + d] = empty ? 0.f : O;
         if (d == 0) {
-          st_part(a.part_m + row, empty ? kEmptyM : mt * kLn2, dev);
-          st_part(a.part_l + row, L, dev);
+          a.part_m[row] = empty ? kEmptyM : mt * kLn2;
+          a.part_l[row] = L;
         }
       }
     }
@@ -1199,126 +1174,6 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
 }
 
 
-// ---------------------------------------------------------------- log-sum-exp merge of a row
-// Partial k of a row: O at po + k * stride_rows * D, m and l at pm / pl + k * stride_rows.
-// One wavefront per row, lanes over the D dims (E = D/64 each). The O loads of the first
-// kU slots are issued before the m / l loads and the max, so a row with up to kU slots
-// costs one memory round trip; more slots are loaded kU at a time.
-// `orow`: the output row (D elements of T). DEV: the partials are read at device scope (the
-// fused merge, inside the launch whose workgroups stored them).
-template <class T, int D, bool DEV = false>
-__device__ __forceinline__ void merge_row(uint8_t* orow, const float* po, const float* pm,
-                                          const float* pl, int nslots, int64_t stride_rows) {
-  constexpr int E = D / 64;
-  constexpr int kU = E <= 2 ? 32 : 16;
-  typedef float vecE __attribute__((ext_vector_type(E)));
-  const int lane = threadIdx.x & 63;
-  const float* o = po + lane * E;
-  auto o_at = [&](int k) {
-    const float* src = o + (int64_t)k * stride_rows * D;
-    if constexpr (DEV) {
-      vecE v;
-#pragma unroll
-      for (int e = 0; e < E; ++e) v[e] = ld_part<true>(src + e);
-      return v;
-    } else {
-      return *reinterpret_cast<const vecE*>(src);
-    }
-  };
-  // first batch of O (uniform guards: no load past the row's last slot)
-  const int cnt0 = min(nslots, kU);
-  vecE v0[kU];
-#pragma unroll
-  for (int u = 0; u < kU; ++u) {
-    v0[u] = vecE{};
-    if (u < cnt0) v0[u] = o_at(u);
-  }
-  // the first 64 slots' m and l stay in registers (one slot per lane)
-  float pm0 = kNegInf, pl0 = 0.f;
-  if (lane < nslots) {
-    pm0 = ld_part<DEV>(pm + (int64_t)lane * stride_rows);
-    pl0 = ld_part<DEV>(pl + (int64_t)lane * stride_rows);
-  }
-  float M = pm0;
-  for (int k = lane + 64; k < nslots; k += 64)
-    M = fmaxf(M, ld_part<DEV>(pm + (int64_t)k * stride_rows));
-  M = wave_max(M);
-  vecE acc = {};
-  float L = 0.f;
-  for (int k0 = 0; k0 < nslots; k0 += 64) {
-    const int k = k0 + lane;
-    float wgt = 0.f;
-    if (k < nslots) {
-      const float mk = k0 == 0 ? pm0 : ld_part<DEV>(pm + (int64_t)k * stride_rows);
-      const float lk = k0 == 0 ? pl0 : ld_part<DEV>(pl + (int64_t)k * stride_rows);
-      wgt = __builtin_amdgcn_exp2f((mk - M) * kLog2e);
-      L += wgt * lk;
-    }
-    const int cnt = min(64, nslots - k0);
-    int j = 0;
-    if (k0 == 0) {
-#pragma unroll
-      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, u) * v0[u];   // zero past cnt0
-      j = cnt0;
-    }
-    for (; j + kU <= cnt; j += kU) {
-      vecE v[kU];
-#pragma unroll
-      for (int u = 0; u < kU; ++u) v[u] = o_at(k0 + j + u);
-#pragma unroll
-      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, j + u) * v[u];
-    }
-    for (; j < cnt; ++j) acc += readlane_f(wgt, j) * o_at(k0 + j);
-  }
-  L = wave_sum(L);
-  uint8_t* op = orow + 2 * lane * E;
-#pragma unroll
-  for (int e = 0; e < E; ++e) T::store(op + 2 * e, L > 0.f ? acc[e] / L : 0.f);
-}
-
-// Output row of (sequence b, q head qh) for the merge kernels.
-__device__ __forceinline__ uint8_t* merge_out_row(const MergeArgs& m, int row) {
-  const int b = row / m.hq, qh = row % m.hq;
-  return m.out + (int64_t)b * m.o_b + (int64_t)qh * m.o_h;
-}
-
-// ---------------------------------------------------------------- fused merge
-// With a.counters set, the merge runs inside the pass-1 launch. Every workgroup that
-// stores a partial of a merge group (one per split of a (sequence, kv head, head chunk),
-// or one per balanced range crossing a sequence) counts itself in once its partial stores
-// have completed; the last to arrive merges the group's rows and resets the counter to
-// zero for the next call. The partials are stored and loaded at device scope and the
-// count is a device-scope atomic issued only after every wavefront of the workgroup has
-// waited for its stores (s_waitcnt vmcnt(0), then a barrier), so no L2 writeback or
-// invalidation is needed (a release/acquire fence pair at agent scope writes back and
-// invalidates whole L2 caches, which measured 25-230 us per call).
-
-// All threads of the workgroup call this (it holds barriers); `leader` (one thread per
-// merge group) counts its group in and publishes whether it was last in *flag.
-__device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t target, bool leader,
-                                            uint32_t* flag) {
-  wait_vmem<0>();
-  __syncthreads();
-  if (leader) {
-    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old + 1u == target;
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = last ? 1u : 0u;
-  }
-  __syncthreads();
-  return *flag != 0u;
-}
-
-// Zeros for the hv q heads of an output row block (a sequence without pages), written by
-// `nthreads` threads of which this is `tid`.
-template <class T, int D>
-__device__ __forceinline__ void zero_rows(uint8_t* out, int64_t o_h, int hv, int tid,
-                                          int nthreads) {
-  for (int idx = tid; idx < hv * D; idx += nthreads)
-    T::store(out + (int64_t)(idx / D) * o_h + 2 * (idx % D), 0.f);
-}
-
 // ---------------------------------------------------------------- pass 1, explicit split
 template <class T, int D, int G, int NW, bool MFMA, bool KV8>
 __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_split(Pass1Args a) {
@@ -1328,7 +1183,6 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW>();
   constexpr int RING = (kLdsDepth + 1) * WV::LDS_PAGE;
   __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? NW * RING : 16];
-  __shared__ uint32_t last_flag;
   WV wv;
   wv.init(a);
   const int w = uniform(threadIdx.x >> 6);
@@ -1394,18 +1248,6 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
                              ((int64_t)b * a.hq + qh0) * a.split + s, a.split, w,
                              (int)threadIdx.x);
-  // fused merge: the last of the (sequence, kv head, head chunk)'s `split` workgroups
-  // merges its heads' partials (rows (b * hq + qh) * split + k, k < split)
-  if (a.counters && !a.direct) {
-    uint32_t* ctr = a.counters + ((int64_t)b * a.hkv + kvh) * a.chunks + hc;
-    if (arrive_last(ctr, (uint32_t)a.split, threadIdx.x == 0, &last_flag)) {
-      for (int h = w; h < wv.hv; h += NW) {
-        const int64_t r0 = ((int64_t)b * a.hq + qh0 + h) * a.split;
-        merge_row<T, D, true>(a.out + (int64_t)b * a.o_b + (int64_t)(qh0 + h) * a.o_h,
-                              a.part_o + r0 * D, a.part_m + r0, a.part_l + r0, a.split, 1);
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------- pass 1, balanced
@@ -1427,7 +1269,6 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW * HP>();
   constexpr int RING = (kLdsDepth + 1) * WV::LDS_PAGE;
   __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? HP * NW * RING : 16];
-  __shared__ uint32_t last_flag[HP];
   WV wv;
   wv.init(a);
   const int wa = uniform(threadIdx.x >> 6);   // wavefront of the workgroup
@@ -1455,28 +1296,10 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     hc = ((int)blockIdx.x % hkg) * HP + hl;
     j = (int)blockIdx.x / hkg;
   }
-  const int kvh = hc % a.hkv, chunk = hc / a.hkv;
-  const int qh0 = kvh * a.group + chunk * a.per;
-  wv.hv = min(a.per, a.group - chunk * a.per);
-  // Fused merge: besides merging, the workgroups write the zero outputs of sequences
-  // without pages (the merge kernel's job otherwise): those starting where a range
-  // starts or inside it belong to that range's workgroup, those after the last page to
-  // the workgroup of the last range, and all of them (no pages at all) to workgroup
-  // j of b = j mod Wg.
-  const bool fused = a.counters != nullptr && a.direct != 0;
-  const int stid = (int)(threadIdx.x & 63) + 64 * w;     // thread among this kv head's
-  auto zero_seq = [&](int bb) {
-    zero_rows<T, D>(a.out + (int64_t)bb * a.o_b + (int64_t)qh0 * a.o_h, a.o_h, wv.hv, stid,
-                    NW * 64);
-  };
   const int base = seq_begin(a, 0);
   const int P = max(seq_begin(a, a.batch) - base, 0);        // pages per head chunk
   const int L = (P + Wg - 1) / Wg;
-  if (L <= 0) {                                              // whole workgroup
-    if (fused)
-      for (int bb = j; bb < a.batch; bb += Wg) zero_seq(bb);
-    return;
-  }
+  if (L <= 0) return;                                        // whole workgroup
   int u = (int)min((int64_t)j * L, (int64_t)P);
   const int u_end = min(u + L, P);
   if (u >= u_end) return;
@@ -1492,9 +1315,10 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   int np = max(seq_begin(a, b + 1), seq0) - seq0;
   int pg = u - (seq0 - base);
   if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
-  if (fused && pg == 0)   // sequences without pages that start where this range starts
-    for (int bb = b - 1; bb >= 0 && seq_begin(a, bb) == seq0; --bb) zero_seq(bb);
 
+  const int kvh = hc % a.hkv, chunk = hc / a.hkv;
+  const int qh0 = kvh * a.group + chunk * a.per;
+  wv.hv = min(a.per, a.group - chunk * a.per);
   const uint8_t* kvh_base = a.kv + (int64_t)kvh * a.kv_h;
   auto page_at = [&](int idx) -> const uint8_t* {   // page of kv_indices[idx]
     u32 pid = (u32)uniform(ld_const(a.indices, idx));
@@ -1527,7 +1351,6 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
         ++b;
         seq0 = seq_begin(a, b);
         np = max(seq_begin(a, b + 1), seq0) - seq0;
-        if (fused && np == 0) zero_seq(b);
       } while (np == 0 && b < a.batch - 1);
       more = np > 0;   // np == 0 only for an invalid kv_indptr
       pg = 0;
@@ -1539,37 +1362,84 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     const int nslots = (start + cur_np - 1) / L - start / L + 1;
     combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
                                a.out + (int64_t)cur_b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
-                               ((int64_t)hc * (Wg + a.batch) + j + cur_b) * G, 1, w, stid);
-    // fused merge: the last of the nslots workgroups whose ranges cross this sequence
-    // merges its heads' partials (slot rows (hc * (Wg + batch) + j + b) * G + g for the
-    // ranges j = start / L ..); nslots is the same for the HP kv heads of the workgroup
-    if (fused && nslots > 1) {
-      uint32_t* ctr = a.counters + (int64_t)hc * a.batch + cur_b;
-      if (arrive_last(ctr, (uint32_t)nslots, stid == 0, &last_flag[hl])) {
-        const int j0 = start / L;
-        for (int g = w; g < wv.hv; g += NW) {
-          const int64_t r0 = ((int64_t)hc * (Wg + a.batch) + j0 + cur_b) * G + g;
-          merge_row<T, D, true>(a.out + (int64_t)cur_b * a.o_b + (int64_t)(qh0 + g) * a.o_h,
-                                a.part_o + r0 * D, a.part_m + r0, a.part_l + r0, nslots,
-                                (int64_t)G);
-        }
-      }
-    }
-    if (!more) {
-      if (fused && u_end == P)   // sequences without pages after the last page
-        for (int bb = cur_b + 1; bb < a.batch; ++bb) zero_seq(bb);
-      break;
-    }
+                               ((int64_t)hc * (Wg + a.batch) + j + cur_b) * G, 1, w,
+                               (int)(threadIdx.x & 63) + 64 * w);
+    if (!more) break;
   }
 }
 
-// ---------------------------------------------------------------- pass 2 kernels
+// ---------------------------------------------------------------- pass 2
+// Partial k of a row: O at po + k * stride_rows * D, m and l at pm / pl + k * stride_rows.
+// One wavefront per row, lanes over the D dims (E = D/64 each). The O loads of the first
+// kU slots are issued before the m / l loads and the max, so a row with up to kU slots
+// costs one memory round trip; more slots are loaded kU at a time.
+template <class T, int D>
+__device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const float* po,
+                                          const float* pm, const float* pl, int nslots,
+                                          int64_t stride_rows) {
+  constexpr int E = D / 64;
+  constexpr int kU = E <= 2 ? 32 : 16;
+  typedef float vecE __attribute__((ext_vector_type(E)));
+  const int lane = threadIdx.x & 63;
+  const float* o = po + lane * E;
+  auto o_at = [&](int k) { return *reinterpret_cast<const vecE*>(o + (int64_t)k * stride_rows * D); };
+  // first batch of O (uniform guards: no load past the row's last slot)
+  const int cnt0 = min(nslots, kU);
+  vecE v0[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    v0[u] = vecE{};
+    if (u < cnt0) v0[u] = o_at(u);
+  }
+  // the first 64 slots' m and l stay in registers (one slot per lane)
+  float pm0 = kNegInf, pl0 = 0.f;
+  if (lane < nslots) {
+    pm0 = pm[(int64_t)lane * stride_rows];
+    pl0 = pl[(int64_t)lane * stride_rows];
+  }
+  float M = pm0;
+  for (int k = lane + 64; k < nslots; k += 64) M = fmaxf(M, pm[(int64_t)k * stride_rows]);
+  M = wave_max(M);
+  vecE acc = {};
+  float L = 0.f;
+  for (int k0 = 0; k0 < nslots; k0 += 64) {
+    const int k = k0 + lane;
+    float wgt = 0.f;
+    if (k < nslots) {
+      const float mk = k0 == 0 ? pm0 : pm[(int64_t)k * stride_rows];
+      const float lk = k0 == 0 ? pl0 : pl[(int64_t)k * stride_rows];
+      wgt = __builtin_amdgcn_exp2f((mk - M) * kLog2e);
+      L += wgt * lk;
+    }
+    const int cnt = min(64, nslots - k0);
+    int j = 0;
+    if (k0 == 0) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, u) * v0[u];   // zero past cnt0
+      j = cnt0;
+    }
+    for (; j + kU <= cnt; j += kU) {
+      vecE v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = o_at(k0 + j + u);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, j + u) * v[u];
+    }
+    for (; j < cnt; ++j) acc += readlane_f(wgt, j) * o_at(k0 + j);
+  }
+  L = wave_sum(L);
+  const int b = row / m.hq, qh = row % m.hq;
+  uint8_t* op = m.out + (int64_t)b * m.o_b + (int64_t)qh * m.o_h + 2 * lane * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e) T::store(op + 2 * e, L > 0.f ? acc[e] / L : 0.f);
+}
+
 template <class T, int D>
 __global__ __launch_bounds__(256) void dk_merge_split(MergeArgs m) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= m.batch * m.hq) return;
   const int64_t r0 = (int64_t)row * m.split;
-  merge_row<T, D>(merge_out_row(m, row), m.po + r0 * D, m.pm + r0, m.pl + r0, m.split, 1);
+  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, m.split, 1);
 }
 
 template <class T, int D>
@@ -1596,8 +1466,7 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   }
   if (nslots == 1) return;   // pass 1 wrote this head's output
   // slot k of this pair is r0 + k * G (rows of G heads per slot); none -> zeros
-  merge_row<T, D>(merge_out_row(m, row), m.po + r0 * D, m.pm + r0, m.pl + r0, nslots,
-                  (int64_t)G);
+  merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, (int64_t)G);
 }
 
 }  // namespace dk

@@ -79,11 +79,6 @@ SIGNATURES = {
                                               _I32, _I32, _I32, _I64, _I64, _I32,
                                               ctypes.POINTER(DkStrides), _I32,
                                               ctypes.POINTER(DkOptions), _P]),
-    "dk_merge_counters": (_SZ, [_I32, _I32, _I32, _I32]),
-    "dk_decode_attention_fused": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P, _SZ,
-                                                 _I32, _I32, _I32, _I32, _I32, _I64, _I64,
-                                                 _I32, ctypes.POINTER(DkStrides), _I32,
-                                                 ctypes.POINTER(DkOptions), _P]),
     "dk_decode_attention_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                                    _I32, _I32, _I64, _I64, _I32,
                                                    ctypes.POINTER(DkStrides), _I32,
@@ -145,11 +140,6 @@ def workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: i
                     split_kv: int) -> int:
     """Scratch bytes for split_kv (0 = balanced mode, 1 = none, > 1 = explicit partials)."""
     return int(load().dk_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, split_kv))
-
-
-def merge_counters(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
-    """uint32 counters dk_decode_attention_fused needs (0 for an invalid shape)."""
-    return int(load().dk_merge_counters(batch, num_q_heads, num_kv_heads, head_dim))
 
 
 def partials_layout(batch: int, num_q_heads: int, head_dim: int, split_kv: int):

@@ -184,32 +184,6 @@ int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv
                            int64_t num_indices, int32_t dtype, const dk_strides* strides,
                            int32_t split_kv, const dk_options* opts, void* hip_stream);
 
-/* Counters dk_decode_attention_fused needs: one uint32 per (sequence, kv head, head
- * chunk). 0 for an invalid shape. No counterpart in the reference. */
-size_t dk_merge_counters(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                         int32_t head_dim);
-
-/* dk_decode_attention_ex (v_cache NULL: k_cache is the combined NHD cache) or
- * dk_decode_attention_kv (v_cache non-NULL) in ONE kernel launch: the log-sum-exp merge of
- * the partials runs inside pass 1, in the last workgroup to finish of each (sequence, kv
- * head, head chunk), instead of in a second kernel. Same results, bit for bit, as the
- * two-kernel calls. `counters` (device memory, at least dk_merge_counters(...) uint32,
- * 4-byte aligned) must be zero before the first call that uses them; every call leaves
- * them zero again, so a caller keeps one zeroed counter array per stream and passes it to
- * every call (calls that share counters, like calls that share a workspace, must not
- * overlap in time). A call with an invalid page table (a decreasing kv_indptr) may leave
- * them non-zero: zero them again before the next call. The workspace needs no
- * initialisation, as for dk_decode_attention_ex. No counterpart in the reference, which
- * always launches a separate reduce kernel (src/cuda_/attention_ext.cu:595-606). */
-int dk_decode_attention_fused(const void* q, const void* k_cache, const void* v_cache,
-                              const int32_t* kv_indptr, const int32_t* kv_indices,
-                              const int32_t* kv_last_page_len, void* out, void* workspace,
-                              size_t workspace_bytes, uint32_t* counters, size_t num_counters,
-                              int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                              int32_t head_dim, int32_t page_size, int64_t num_pages,
-                              int64_t num_indices, int32_t dtype, const dk_strides* strides,
-                              int32_t split_kv, const dk_options* opts, void* hip_stream);
-
 /* Bytes of the library's static scratch (see dk_decode_attention_noalloc). */
 #define DK_STATIC_SCRATCH_BYTES (32u << 20)
 
