@@ -1,31 +1,37 @@
-"""Decode-attention microbenchmark sweep on MI355X, CSV in the reference's schema.
+"""Decode-attention microbenchmark sweeps on MI355X, written as CSV in the reference's schema.
 
-Counterpart of the reference's bench/microbench_cuda.py: the same sweep (context lengths x
-batch sizes x split_kv), the same timing protocol (20 warm-up calls, then 100 timed calls
-each preceded by a cache-flushing device fill and bracketed by events; unlike the
-reference no host sync follows the fill, so host launch overhead overlaps it and the
-events time the GPU work), and the same CSV columns:
+Counterpart of the reference's bench/microbench_cuda.py. Sweeps:
 
-    implementation, context_length, batch_size, split_kv, latency_ms_p50, latency_ms_p95,
-    achieved_bw_gb_s, peak_bw_gb_s, bw_pct_of_peak, max_abs_err_vs_fp32
+  reference  its own grid: context 2K-64K x batch 1/4/16 x split_kv 1-16, fp16 (config_id 0)
+  config2    BASELINE config 2: batch 1/4/16/32/64 x context 4096 x split_kv 1-16, fp16
+  config3    BASELINE config 3: batch 1/4 x context 32768/131072 x split_kv 16-128, bf16
+  quick      a small validation grid
 
-Implementations: `hip_naive` (split_kv 1, one pass), `hip_split_kv` (the reference's
-ceil(N/S)-page partition + merge, for each split in the sweep) and `hip_auto` (split_kv 0
-with the host plan hint: the library's own schedule; reported with split_kv 0).
-FlashInfer has no ROCm build here; its rows are skipped as the reference skips them when
-flashinfer is missing. Bytes are the reference's model (q + K/V + out,
-microbench_cuda.py:114-121). The error column is against an fp32 PyTorch reference of
-the same attention computed on the device (gather, scaled scores, softmax, weighted V).
+Timing protocol (the reference's): 20 warm-up calls, then 100 timed calls, each after a
+cache-flushing 1 GiB device fill and bracketed by events. Unlike the reference no host
+sync follows the fill, so the call's host launch overlaps it and the events time GPU
+work. Rows: `hip_naive` (split_kv 1, one pass), `hip_split_kv` (the reference's
+ceil(N/S)-page partition + merge, per split of the sweep) and `hip_auto` (split_kv 0 with
+the host plan hint: the library's own schedule; reported as split_kv 0). FlashInfer has
+no ROCm build here; its rows are left out, as the reference leaves them out without
+flashinfer.
 
-    python decode-kernel_amd/microbench.py                  # full sweep
-    python decode-kernel_amd/microbench.py --quick
-    python decode-kernel_amd/microbench.py --out results/microbench_hip.csv
+Columns: the reference's ten (bench/microbench_cuda.py:270-283; bytes are its model, q +
+K/V + out, :114-121; the error is against an fp32 PyTorch attention computed on the
+device) and four more: dtype, config_id (0 for the reference grid, else the BASELINE
+config), fetch_bytes (bytes the call must read from HBM: K/V of the valid tokens, q and
+the page tables; rocprofv3's measured FETCH_SIZE for the metric shape is in profiles/)
+and cpu_cores (os.cpu_count() of the host).
+
+    python decode-kernel_amd/microbench.py                        # reference grid
+    python decode-kernel_amd/microbench.py --sweep config2 --out results/config2.csv
 """
 from __future__ import annotations
 
 import argparse
 import csv
 import math
+import os
 import sys
 from pathlib import Path
 
@@ -38,28 +44,27 @@ import attention  # noqa: E402
 import layout  # noqa: E402
 from dk_lib import workspace_bytes  # noqa: E402
 
-NUM_Q_HEADS = 32
-NUM_KV_HEADS = 8
-HEAD_DIM = 128
-PAGE_SIZE = 16
-DTYPE = torch.float16
+HQ, HKV, D, PAGE = 32, 8, 128, 16          # the reference's fixed head configuration
 DEVICE = "cuda"
-WARMUP_ITERS = 20
-TIMED_ITERS = 100
-FLUSH_BYTES = 1 << 30            # > the 256 MB Infinity Cache (the reference flushed 256 MB of L2)
+WARMUP_ITERS, TIMED_ITERS = 20, 100        # the reference's protocol
+FLUSH_BYTES = 1 << 30                      # > the 256 MB Infinity Cache
 
-COLUMNS = ["implementation", "context_length", "batch_size", "split_kv", "latency_ms_p50",
-           "latency_ms_p95", "achieved_bw_gb_s", "peak_bw_gb_s", "bw_pct_of_peak",
-           "max_abs_err_vs_fp32"]
+REFERENCE_COLUMNS = ["implementation", "context_length", "batch_size", "split_kv",
+                     "latency_ms_p50", "latency_ms_p95", "achieved_bw_gb_s", "peak_bw_gb_s",
+                     "bw_pct_of_peak", "max_abs_err_vs_fp32"]
+COLUMNS = REFERENCE_COLUMNS + ["dtype", "config_id", "fetch_bytes", "cpu_cores"]
 
-FULL_CONTEXT_LENGTHS = [2048, 4096, 8192, 16384, 32768, 65536]
-FULL_BATCH_SIZES = [1, 4, 16]
-FULL_SPLIT_KVS = [1, 2, 4, 8, 16]
-FULL_IMPLS = ["hip_naive", "hip_split_kv", "hip_auto"]
-QUICK_CONTEXT_LENGTHS = [2048, 8192]
-QUICK_BATCH_SIZES = [1]
-QUICK_SPLIT_KVS = [1, 4, 8]
-QUICK_IMPLS = ["hip_naive", "hip_split_kv", "hip_auto"]
+# name -> (config_id, dtype, context lengths, batch sizes, split_kv values, implementations)
+SWEEPS = {
+    "reference": (0, torch.float16, [2048, 4096, 8192, 16384, 32768, 65536], [1, 4, 16],
+                  [1, 2, 4, 8, 16], ["hip_naive", "hip_split_kv", "hip_auto"]),
+    "config2": (2, torch.float16, [4096], [1, 4, 16, 32, 64], [1, 2, 4, 8, 16],
+                ["hip_split_kv", "hip_auto"]),
+    "config3": (3, torch.bfloat16, [32768, 131072], [1, 4], [16, 32, 64, 128],
+                ["hip_split_kv", "hip_auto"]),
+    "quick": (0, torch.float16, [2048, 8192], [1], [1, 4, 8],
+              ["hip_naive", "hip_split_kv", "hip_auto"]),
+}
 
 
 def peak_bw_gb_s() -> float:
@@ -90,7 +95,7 @@ def torch_reference(q, kv, indptr_h, indices, last_h, rows):
     out = torch.full((b_, hq, d), float("nan"), device=q.device)
     for b in rows:
         s, e = int(indptr_h[b]), int(indptr_h[b + 1])
-        n = (e - s - 1) * PAGE_SIZE + int(last_h[b]) if e > s else 0
+        n = (e - s - 1) * PAGE + int(last_h[b]) if e > s else 0
         if n == 0:
             out[b] = 0
             continue
@@ -120,33 +125,35 @@ def time_kernel(fn, flush, n_warmup=WARMUP_ITERS, n_timed=TIMED_ITERS):
 
 
 def run_sweep(context_lengths, batch_sizes, split_kvs, implementations, out_path,
-              check_rows: int = 4, timed_iters: int = TIMED_ITERS):
+              check_rows: int = 4, timed_iters: int = TIMED_ITERS, dtype=torch.float16,
+              config_id: int = 0):
+    """Time every (context, batch, implementation, split) point; write and return the rows."""
     if not torch.cuda.is_available():
-        raise RuntimeError("a GPU is required for benchmarking")
+        raise RuntimeError("the sweep runs on a GPU")
     peak = peak_bw_gb_s()
-    print(f"Peak HBM bandwidth: {peak:.0f} GB/s")
-    print(f"GPU: {torch.cuda.get_device_name(0)}\n")
+    dname = {torch.float16: "fp16", torch.bfloat16: "bf16"}[dtype]
+    cores = os.cpu_count() or 1
+    print(f"# {torch.cuda.get_device_name(0)}: peak {peak:.0f} GB/s, {dname}, "
+          f"config_id {config_id}", flush=True)
     flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=DEVICE)
     rows = []
     for ctx in context_lengths:
         for batch in batch_sizes:
-            print(f"ctx={ctx:>6}  batch={batch:>3}", flush=True)
             q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-                batch, ctx, NUM_Q_HEADS, NUM_KV_HEADS, HEAD_DIM, dtype=DTYPE, device=DEVICE,
-                page_table="permuted", seed=ctx + batch)
+                batch, ctx, HQ, HKV, D, dtype=dtype, device=DEVICE, page_table="permuted",
+                seed=ctx + batch)
             indptr_h, last_h = indptr.cpu(), last.cpu()
             check = sorted({int(x) for x in np.linspace(0, batch - 1, min(check_rows, batch))})
             ref = torch_reference(q, kv, indptr_h, ids, last_h, check)
             hint = attention.plan_hint(indptr_h)
-            total = attention_bytes(batch, ctx, NUM_Q_HEADS, NUM_KV_HEADS, HEAD_DIM)
+            total = attention_bytes(batch, ctx, HQ, HKV, D)
+            reads = layout.attention_bytes(batch, ctx, HQ, HKV, D) - batch * HQ * D * 2
             for impl in implementations:
                 splits = split_kvs if impl == "hip_split_kv" else [1 if impl == "hip_naive" else 0]
                 for skv in splits:
                     out = torch.empty_like(q)
-                    ws = None
-                    need = workspace_bytes(batch, NUM_Q_HEADS, NUM_KV_HEADS, HEAD_DIM, skv)
-                    if need:
-                        ws = torch.empty(need, dtype=torch.uint8, device=DEVICE)
+                    need = workspace_bytes(batch, HQ, HKV, D, skv)
+                    ws = torch.empty(need, dtype=torch.uint8, device=DEVICE) if need else None
                     fn = (lambda s=skv: attention.decode_attention(
                         q, kv, indptr, ids, last, split_kv=s, out=out, workspace=ws,
                         max_pages_per_seq=hint))
@@ -156,16 +163,17 @@ def run_sweep(context_lengths, batch_sizes, split_kvs, implementations, out_path
                     lat = time_kernel(fn, flush, n_timed=timed_iters)
                     p50, p95 = float(np.percentile(lat, 50)), float(np.percentile(lat, 95))
                     bw = (total / 1e9) / (p50 / 1e3)
-                    print(f"  {impl:<14} split={skv:>2}  p50={p50:.4f}ms  bw={bw:.0f}GB/s  "
-                          f"max_err={err:.1e}", flush=True)
+                    print(f"ctx {ctx:6d} B {batch:3d} {impl:12s} split {skv:3d}: "
+                          f"{p50 * 1e3:8.1f} us  {bw:7.0f} GB/s ({100 * bw / peak:4.1f} %)  "
+                          f"err {err:.1e}", flush=True)
                     rows.append({
                         "implementation": impl, "context_length": ctx, "batch_size": batch,
                         "split_kv": skv, "latency_ms_p50": round(p50, 4),
                         "latency_ms_p95": round(p95, 4), "achieved_bw_gb_s": round(bw, 2),
                         "peak_bw_gb_s": round(peak, 2),
                         "bw_pct_of_peak": round(100.0 * bw / peak, 2),
-                        "max_abs_err_vs_fp32": round(err, 6)})
-            print()
+                        "max_abs_err_vs_fp32": round(err, 6), "dtype": dname,
+                        "config_id": config_id, "fetch_bytes": reads, "cpu_cores": cores})
             del q, kv
     out_file = Path(out_path)
     out_file.parent.mkdir(parents=True, exist_ok=True)
@@ -173,14 +181,15 @@ def run_sweep(context_lengths, batch_sizes, split_kvs, implementations, out_path
         w = csv.DictWriter(f, fieldnames=COLUMNS)
         w.writeheader()
         w.writerows(rows)
-    print(f"Results written to {out_file}")
+    print(f"# {len(rows)} rows -> {out_file}")
     return rows
 
 
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description="HIP decode attention microbenchmark")
+    ap.add_argument("--sweep", default="reference", choices=sorted(SWEEPS))
+    ap.add_argument("--quick", action="store_true", help="same as --sweep quick")
     ap.add_argument("--out", default="results/microbench_hip.csv", help="output CSV path")
-    ap.add_argument("--quick", action="store_true", help="small sweep for quick validation")
     ap.add_argument("--split-kv-only", action="store_true",
                     help="only the explicit split-KV rows")
     ap.add_argument("--timed-iters", type=int, default=TIMED_ITERS)
@@ -189,9 +198,8 @@ def parse_args(argv=None):
 
 if __name__ == "__main__":
     args = parse_args()
-    if args.quick:
-        sweep = (QUICK_CONTEXT_LENGTHS, QUICK_BATCH_SIZES, QUICK_SPLIT_KVS, QUICK_IMPLS)
-    else:
-        sweep = (FULL_CONTEXT_LENGTHS, FULL_BATCH_SIZES, FULL_SPLIT_KVS, FULL_IMPLS)
-    impls = ["hip_split_kv"] if args.split_kv_only else sweep[3]
-    run_sweep(sweep[0], sweep[1], sweep[2], impls, args.out, timed_iters=args.timed_iters)
+    cid, dt, ctxs, batches, splits, impls = SWEEPS["quick" if args.quick else args.sweep]
+    if args.split_kv_only:
+        impls = ["hip_split_kv"]
+    run_sweep(ctxs, batches, splits, impls, args.out, timed_iters=args.timed_iters, dtype=dt,
+              config_id=cid)
