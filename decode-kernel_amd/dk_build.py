@@ -118,7 +118,7 @@ def build(verbose: bool = False, defines: tuple = (), out: Path = LIB_PATH,
     hipcc = _hipcc()
     dflags = [f"-D{d}" for d in defines]
     objs = [build_dir / "dk_args.o"]
-    cmds = [["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}",
+    cmds = [["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", *dflags, f"-I{INCLUDE}",
              "-c", str(CSRC / "dk_args.cpp"), "-o", str(objs[0])]]
     for src in HIP_SOURCES:
         obj = build_dir / (Path(src).stem + ".o")
