@@ -25,9 +25,10 @@ Modes:
                    sampled sequences
   --single-call    one flush and one call, no settling or warm-up (for rocprofv3 --pmc
                    counter runs, which then see exactly the call's dispatches)
-  --host-overhead  host time per call of the Python entry point attention.decode_attention
-                   (back to back, no flush), against the bare C-ABI call and a call that
-                   validates its arguments afresh (no cached plan)
+  --host-overhead  host time per call of the Python entry points (back to back, no
+                   flush): attention.decode_attention, DecodePlan.run with a preallocated
+                   output, the bare C-ABI call, and a call that validates its arguments
+                   afresh (no cached plan)
 
 `value` is achieved algorithmic HBM bandwidth in TB/s (bytes of the reference's model,
 bench/microbench_cuda.py:114-121, plus page tables, divided by the p50 per-call time);
@@ -572,9 +573,15 @@ def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
         attention._PLANS.clear()
         return py()
 
+    plan = attention.DecodePlan(q, kv, ip, ids, last, split_kv=split, max_pages_per_seq=hint,
+                                out=c.out)
+
+    def py_plan():
+        return plan.run(q, kv, ip, ids, last, out=c.out)
+
     res = {}
-    for name, fn in (("c_abi", c.full), ("decode_attention", py),
-                     ("decode_attention_unplanned", py_fresh)):
+    for name, fn in (("c_abi", c.full), ("decode_plan_run_with_out", py_plan),
+                     ("decode_attention", py), ("decode_attention_unplanned", py_fresh)):
         for _ in range(20):
             fn()
         torch.cuda.synchronize()

@@ -374,6 +374,11 @@ def decode_attention(
             if len(_PLANS) >= _PLANS_MAX:
                 _PLANS.clear()
             _PLANS[key] = plan
+    return _launch(plan, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out, workspace)
+
+
+def _launch(plan, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out, workspace):
+    """One library call with a validated plan: pointers, `out`, the workspace, the stream."""
     lib = dk_lib.load()
     if out is None:
         out = torch.empty(plan.out_shape, dtype=plan.dtype, device=plan.device)
@@ -417,6 +422,55 @@ def decode_attention(
             torch.cuda.set_device(prev)
     dk_lib.check(rc, "decode_attention")
     return out
+
+
+class DecodePlan:
+    """decode_attention split into plan and run, as FlashInfer's decode wrappers are:
+    the plan validates the arguments once (shapes, strides, dtypes, devices, options) and
+    keeps the library call's argument tuple; run() then passes only the pointers, so a
+    model's layers, which share one shape, pay little more than the C ABI call.
+
+        plan = DecodePlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=0,
+                          max_pages_per_seq=hint)
+        for layer in layers:
+            out = plan.run(q_l, kv_l, kv_indptr, kv_indices, kv_last_page_len, out=out_l)
+
+    run() takes tensors with the planned shapes, strides, dtypes and devices: the shapes
+    and strides of q, the cache, the page tables and `out` are compared with the plan's
+    (the strides are what the kernels address memory with), dtypes and devices are not.
+    `out` may be None (a contiguous one is allocated; then the plan must have been made
+    without one) and `workspace` must hold at least the planned bytes (the library checks
+    its size on every call). Keyword options are those of decode_attention.
+    """
+
+    def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=1, *,
+                 out=None, workspace=None, qk_path=0, waves_per_group=0, waves_per_cu=0,
+                 schedule=0, max_pages_per_seq=0, sm_scale=None, k_scale=None, v_scale=None,
+                 logit_cap=None, window=None):
+        self._plan = _CallPlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
+                               out, workspace, qk_path, waves_per_group, waves_per_cu,
+                               schedule, max_pages_per_seq, sm_scale, k_scale, v_scale,
+                               logit_cap, window)
+        self._guard = self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+        self._out_strides = None if out is None else out.stride()
+        self.workspace_bytes = self._plan.ws_need
+
+    @staticmethod
+    def _layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
+        kv = (kv_data.shape, kv_data.stride()) if isinstance(kv_data, torch.Tensor) else \
+            tuple((t.shape, t.stride()) for t in kv_data)
+        return (q.shape, q.stride(), kv, kv_indptr.shape, kv_indptr.stride(), kv_indices.shape,
+                kv_indices.stride(), kv_last_page_len.shape, kv_last_page_len.stride())
+
+    def run(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out=None,
+            workspace=None):
+        if self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) != self._guard:
+            _fail("DecodePlan.run: the tensors differ in shape or strides from the planned call")
+        if (None if out is None else out.stride()) != self._out_strides or \
+                (out is not None and out.shape != q.shape):
+            _fail("DecodePlan.run: out differs from the planned call (none, or its strides)")
+        return _launch(self._plan, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out,
+                       workspace)
 
 
 def decode_partials(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv: int,

@@ -307,17 +307,19 @@ def test_config4_ragged_freelist():
         _check(out, want, rows=subset, label=f"ragged S={s}")
 
 
-def test_metric_config_sample():
-    # B=32, ctx=8192, 32/8/128 fp16, random page permutation; the oracle on 4 sequences
+def test_metric_config_every_sequence():
+    # B=32, ctx=8192, 32/8/128 fp16, random page permutation (bench.py's metric workload):
+    # the oracle on all 32 sequences, for the reference's split values, the automatic
+    # schedule without and with the plan hint (one pass, what bench.py times)
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
         32, 8192, 32, 8, 128, device=DEV, page_table="permuted", seed=1)
-    subset = [0, 11, 22, 31]
-    want = _oracle(q, kv, indptr, ids, last, batch_subset=subset)
-    for s in (1, 3, 8, 0):
-        _announce(f"metric S={s}")
-        out = decode_attention(q, kv, indptr, ids, last, split_kv=s)
+    want = _oracle(q, kv, indptr, ids, last)
+    hint = attention.plan_hint(indptr.cpu())
+    for s, h in ((1, 0), (3, 0), (8, 0), (0, 0), (0, hint)):
+        _announce(f"metric S={s} hint={h}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=s, max_pages_per_seq=h)
         torch.cuda.synchronize()
-        _check(out, want, rows=subset, label=f"metric S={s}")
+        _check(out, want, label=f"metric S={s} hint={h}")
 
 
 # ---------------------------------------------------------------- balanced mode

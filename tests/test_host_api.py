@@ -83,3 +83,38 @@ def test_caller_out_and_a_side_stream_use_their_own_plan():
         got = attention.decode_attention(*a, split_kv=0, out=out)
     torch.cuda.synchronize()
     assert got is out and torch.equal(out, want)
+
+
+def test_decode_plan_rejects_a_different_layout_before_any_device_work():
+    # the guard runs before the launch: CPU tensors are enough to exercise it (the plan
+    # itself needs GPU tensors, so build one around a fake plan object)
+    plan = attention.DecodePlan.__new__(attention.DecodePlan)
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    kv = torch.zeros(4, 2, 16, 8, 128, dtype=torch.float16)
+    tabs = (torch.zeros(3, dtype=torch.int32), torch.zeros(4, dtype=torch.int32),
+            torch.ones(2, dtype=torch.int32))
+    plan._guard = attention.DecodePlan._layout(q, kv, *tabs)
+    plan._out_strides = None
+    with pytest.raises(dk_lib.DecodeArgumentError, match="shape or strides"):
+        plan.run(torch.zeros(3, 32, 128, dtype=torch.float16), kv, *tabs)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="shape or strides"):
+        plan.run(q, torch.zeros(4, 2, 16, 8, 256, dtype=torch.float16)[..., ::2], *tabs)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="out differs"):
+        plan.run(q, kv, *tabs, out=torch.zeros(2, 32, 128, dtype=torch.float16))
+
+
+@pytest.mark.gpu
+def test_decode_plan_runs_like_decode_attention():
+    a = _inputs([700, 1500, 33], seed=5)
+    for split in (0, 1, 4):
+        hint = attention.plan_hint(a[2].cpu())
+        plan = attention.DecodePlan(*a, split_kv=split, max_pages_per_seq=hint)
+        got = plan.run(*a)
+        want = attention.decode_attention(*a, split_kv=split, max_pages_per_seq=hint)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), split
+        out = torch.empty_like(a[0])
+        plan2 = attention.DecodePlan(*a, split_kv=split, out=out)
+        assert plan2.run(*a, out=out) is out
+        torch.cuda.synchronize()
+        assert float((out.float() - want.float()).abs().max()) < 1e-3
