@@ -960,7 +960,16 @@ constexpr int min_waves_per_simd() {
 // page about to be used; the last pages are peeled off after it. Buffer 0 must already
 // hold (or be loading) page 0; page(i) is the base address of page i, valid(i) its valid
 // token count.
-template <int DEPTH, bool CAP, class W, class PageFn, class ValidFn>
+//
+// GATED (DEPTH 2): page 1's loads are issued only when there is a page 1. The compiler's
+// wait counts at the loop head then merge the path without them, so the first compute of
+// every round of three pages waits until the second page has landed too, and the next
+// loads go out later: at most about two pages in flight instead of three. Measured on
+// MI355X (µs per call, fp16 32/8/128): one pass at B=32 ctx 8192 157.3 gated vs 162.0
+// not; the balanced schedule at the same shape 160.8 vs 158.6, ragged B=128 350.4 vs
+// 343.8, B=16 ctx 4096 51.9 vs 50.7, B=256 ctx 1024 175.7 vs 181.6. So the one-pass /
+// explicit-split kernel streams gated and the balanced kernel does not.
+template <int DEPTH, bool CAP, bool GATED, class W, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[W::VB],
                                              int n, PageFn page, ValidFn valid) {
   u32 kb[W::KB], vb[W::VB];
@@ -981,7 +990,11 @@ __device__ __forceinline__ void stream_pages(W& wv, u32 (&ka)[W::KB], u32 (&va)[
     }
   } else {
     u32 kc[W::KB], vc[W::VB];
-    if (n > 1) wv.load_page(kb, vb, page(1));
+    if constexpr (GATED) {
+      if (n > 1) wv.load_page(kb, vb, page(1));
+    } else {
+      wv.load_page(kb, vb, page(n > 1 ? 1 : 0), n > 1);   // zero extent without a page 1
+    }
     int k = 0;
     for (; k + 4 < n; k += 3) {
       wv.load_page(kc, vc, page(k + 2));
@@ -1151,8 +1164,8 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
 }
 
 // Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages
-// (through its LDS ring when LDS is set).
-template <int D, bool KV8, bool CAP, bool LDS = false, class WV, class PageFn, class ValidFn>
+// (through its LDS ring when LDS is set; GATED: see stream_pages).
+template <int D, bool KV8, bool CAP, bool LDS, bool GATED, class WV, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n, PageFn page,
                                                    ValidFn valid, uint8_t* ring = nullptr) {
   const int nk = n > w ? (n - w + NW - 1) / NW : 0;
@@ -1165,12 +1178,36 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
     } else if constexpr (depth <= 2) {
       u32 ka[WV::KB], va[WV::VB];
       wv.load_page(ka, va, pk(0));
-      stream_pages<depth, CAP>(wv, ka, va, nk, pk, vk);
+      stream_pages<depth, CAP, GATED>(wv, ka, va, nk, pk, vk);
     } else {
       stream_ring<depth, CAP>(wv, nk, pk, vk);
     }
   }
   (void)ring;
+}
+
+// Whether a kernel streams through registers with its first page loaded by the caller
+// (stream_loaded below): the register ring of depth <= 2 on the VALU q.k path (16-bit
+// caches at D <= 128). (The MFMA q.k path stages K through LDS and has no registers to
+// spare for it: two of its kernels spilled.)
+template <int D, bool KV8, bool LDS, bool MFMA>
+constexpr bool first_page_by_caller() {
+  return !LDS && !MFMA && prefetch_depth<D, KV8>() <= 2;
+}
+
+// stream_interleaved with this wavefront's first page (page w of the run) already loading
+// into ka / va; the balanced kernel issues that load before it has found the sequence the
+// run belongs to (first_page_by_caller kernels only).
+template <int D, bool KV8, bool CAP, class WV, class PageFn, class ValidFn>
+__device__ __forceinline__ void stream_loaded(WV& wv, int NW, int w, int n, PageFn page,
+                                              ValidFn valid, u32 (&ka)[WV::KB],
+                                              u32 (&va)[WV::VB]) {
+  const int nk = n > w ? (n - w + NW - 1) / NW : 0;
+  if (nk > 0) {
+    auto pk = [&](int k) { return page(w + NW * k); };
+    auto vk = [&](int k) { return valid(w + NW * k); };
+    stream_pages<prefetch_depth<D, KV8>(), CAP, false>(wv, ka, va, nk, pk, vk);
+  }
 }
 
 
@@ -1240,9 +1277,9 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
     return pg == npages - 1 ? enc_last : (pg == lo_page ? enc_lo : kPage);
   };
   if (a.cap_out != 0.f)
-    stream_interleaved<D, KV8, true, LDSP>(wv, NW, w, n, page, valid, wring);
+    stream_interleaved<D, KV8, true, LDSP, true>(wv, NW, w, n, page, valid, wring);
   else
-    stream_interleaved<D, KV8, false, LDSP>(wv, NW, w, n, page, valid, wring);
+    stream_interleaved<D, KV8, false, LDSP, true>(wv, NW, w, n, page, valid, wring);
   wv.reduce_rows();
   combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
@@ -1304,18 +1341,6 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   const int u_end = min(u + L, P);
   if (u >= u_end) return;
 
-  // sequence containing unit u: the largest b with start(b) <= u (binary search)
-  int lo = 0, hi = a.batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (seq_begin(a, mid) - base <= u) lo = mid; else hi = mid - 1;
-  }
-  int b = lo;
-  int seq0 = seq_begin(a, b);
-  int np = max(seq_begin(a, b + 1), seq0) - seq0;
-  int pg = u - (seq0 - base);
-  if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
-
   const int kvh = hc % a.hkv, chunk = hc / a.hkv;
   const int qh0 = kvh * a.group + chunk * a.per;
   wv.hv = min(a.per, a.group - chunk * a.per);
@@ -1325,12 +1350,33 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     pid = pid < a.num_pages ? pid : 0u;
     return kvh_base + (int64_t)pid * a.kv_p;
   };
+  // The range's units are kv_indices[base + u ..]: this wavefront's first page (unit
+  // u + w) is known before the sequence it belongs to, so its load is issued now and the
+  // binary search and the sequence's bounds (dependent memory trips) run while it is in
+  // flight. A range shorter than the wavefront index loads nothing (zero extent).
+  constexpr bool PRE = first_page_by_caller<D, KV8, LDSP, MFMA>();
+  u32 ka[WV::KB], va[WV::VB];   // unused (and allocated no registers) unless PRE
+  if constexpr (PRE) wv.load_page(ka, va, page_at(base + min(u + w, u_end - 1)), u + w < u_end);
+
+  // sequence containing unit u: the largest b with start(b) <= u (binary search)
+  int lo = 0, hi = a.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (seq_begin(a, mid) - base <= u) lo = mid; else hi = mid - 1;
+  }
+  int b = lo;
+  // q of that sequence, in flight with its bounds below
+  wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+  int seq0 = seq_begin(a, b);
+  int np = max(seq_begin(a, b + 1), seq0) - seq0;
+  int pg = u - (seq0 - base);
+  if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
   // Segment after segment; the next segment's q is loaded before the current segment's
   // reduction and workgroup combine, so its memory latency overlaps that work. (Loading
   // the next segment's first page there too measured slower: the page buffers then stay
   // live across the combine and the kernel needs ~40 more registers.)
-  wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+  bool preloaded = PRE;
   while (true) {
     const int n = min(np - pg, u_end - u);   // pages of this segment (>= 1)
     wv.reset();
@@ -1338,10 +1384,19 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     const int first = pg, cur_seq0 = seq0, cur_np = np, cur_b = b;
     auto page = [&](int i) -> const uint8_t* { return page_at(cur_seq0 + first + i); };
     auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
-    if (a.cap_out != 0.f)
-      stream_interleaved<D, KV8, true, LDSP>(wv, NW, w, n, page, valid, wring);
-    else
-      stream_interleaved<D, KV8, false, LDSP>(wv, NW, w, n, page, valid, wring);
+    if (PRE && preloaded) {
+      // first segment: ka / va hold (or are loading) its page w, the range's unit u + w
+      preloaded = false;
+      if (a.cap_out != 0.f)
+        stream_loaded<D, KV8, true>(wv, NW, w, n, page, valid, ka, va);
+      else
+        stream_loaded<D, KV8, false>(wv, NW, w, n, page, valid, ka, va);
+    } else {
+      if (a.cap_out != 0.f)
+        stream_interleaved<D, KV8, true, LDSP, false>(wv, NW, w, n, page, valid, wring);
+      else
+        stream_interleaved<D, KV8, false, LDSP, false>(wv, NW, w, n, page, valid, wring);
+    }
 
     // the next non-empty sequence of the range, if any
     bool more = false;
