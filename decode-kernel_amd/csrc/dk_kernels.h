@@ -1196,8 +1196,9 @@ constexpr bool first_page_by_caller() {
 }
 
 // stream_interleaved with this wavefront's first page (page w of the run) already loading
-// into ka / va; the balanced kernel issues that load before it has found the sequence the
-// run belongs to (first_page_by_caller kernels only).
+// into ka / va; the balanced kernel issues that load before it has found the sequence of
+// its first segment, and before the previous segment's combine for the others
+// (first_page_by_caller kernels only).
 template <int D, bool KV8, bool CAP, class WV, class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_loaded(WV& wv, int NW, int w, int n, PageFn page,
                                               ValidFn valid, u32 (&ka)[WV::KB],
@@ -1353,7 +1354,8 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   // The range's units are kv_indices[base + u ..]: this wavefront's first page (unit
   // u + w) is known before the sequence it belongs to, so its load is issued now and the
   // binary search and the sequence's bounds (dependent memory trips) run while it is in
-  // flight. A range shorter than the wavefront index loads nothing (zero extent).
+  // flight. A range shorter than the wavefront index loads nothing (zero extent); a page
+  // loaded for a segment too short to have a page w is not used.
   constexpr bool PRE = first_page_by_caller<D, KV8, LDSP, MFMA>();
   u32 ka[WV::KB], va[WV::VB];   // unused (and allocated no registers) unless PRE
   if constexpr (PRE) wv.load_page(ka, va, page_at(base + min(u + w, u_end - 1)), u + w < u_end);
@@ -1372,11 +1374,9 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   int pg = u - (seq0 - base);
   if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
-  // Segment after segment; the next segment's q is loaded before the current segment's
-  // reduction and workgroup combine, so its memory latency overlaps that work. (Loading
-  // the next segment's first page there too measured slower: the page buffers then stay
-  // live across the combine and the kernel needs ~40 more registers.)
-  bool preloaded = PRE;
+  // Segment after segment; the next segment's q (and, PRE, this wavefront's first page of
+  // it) is loaded before the current segment's reduction and workgroup combine, so its
+  // memory latency overlaps that work.
   while (true) {
     const int n = min(np - pg, u_end - u);   // pages of this segment (>= 1)
     wv.reset();
@@ -1384,9 +1384,8 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     const int first = pg, cur_seq0 = seq0, cur_np = np, cur_b = b;
     auto page = [&](int i) -> const uint8_t* { return page_at(cur_seq0 + first + i); };
     auto valid = [&](int i) -> int { return first + i == cur_np - 1 ? valid_last : kPage; };
-    if (PRE && preloaded) {
-      // first segment: ka / va hold (or are loading) its page w, the range's unit u + w
-      preloaded = false;
+    if constexpr (PRE) {
+      // ka / va hold (or are loading) this segment's page w, the range's unit u + w
       if (a.cap_out != 0.f)
         stream_loaded<D, KV8, true>(wv, NW, w, n, page, valid, ka, va);
       else
@@ -1410,7 +1409,11 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
       more = np > 0;   // np == 0 only for an invalid kv_indptr
       pg = 0;
     }
-    if (more) wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+    if (more) {
+      wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+      if constexpr (PRE)
+        wv.load_page(ka, va, page_at(base + min(u + w, u_end - 1)), u + w < u_end);
+    }
 
     wv.reduce_rows();
     const int start = cur_seq0 - base;
