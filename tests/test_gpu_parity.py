@@ -347,6 +347,30 @@ def test_balanced_ragged_with_empty_sequences(waves_per_cu, dtype):
             assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[5]) == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 32, 8), (128, 8, 8), (64, 32, 8), (128, 64, 8)])
+def test_balanced_many_short_sequences_one_wave(dtype, d, hq, hkv):
+    # one wavefront per workgroup: the page ring runs on from one sequence to the next
+    # inside a workgroup's range, so segments of 1-7 pages (every remainder of the ring's
+    # groups of three, with and without steady-state rounds), a 0-page sequence between
+    # two others, and ranges cut inside sequences must all come out right
+    rng = np.random.default_rng(d + hq)
+    lens = [int(x) for x in rng.integers(1, 7 * 16 + 1, size=150)]
+    lens[10] = 0
+    lens[11] = 16 * 3
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        len(lens), lens, hq, hkv, d, dtype=dtype, device=DEV, page_table="permuted",
+        seed=d + hq + hkv)
+    want = _oracle(q, kv, indptr, ids, last)
+    for wpc in (1, 2, 3):
+        _announce(f"short sequences one wave {dtype} d={d} {hq}/{hkv} wpc={wpc}")
+        out = decode_attention(q, kv, indptr, ids, last, split_kv=0, waves_per_group=1,
+                               waves_per_cu=wpc, schedule=1)
+        torch.cuda.synchronize()
+        _check(out, want, label=f"wpc={wpc}")
+        assert torch.count_nonzero(out[10]) == 0
+
+
 @pytest.mark.parametrize("d,hq,hkv", [(64, 32, 8), (64, 8, 1), (128, 64, 4), (256, 16, 4),
                                       (128, 6, 2)])
 def test_balanced_head_layouts(d, hq, hkv):
