@@ -18,7 +18,12 @@ clocks reach their steady state.
 Modes:
   (default)        one JSON line for the metric workload (or the shape given by --batch,
                    --ctx, --num-q-heads, --num-kv-heads, --head-dim, --dtype, --kv-dtype,
-                   --ragged-min, --split ...), with `roofline` and `cpu_baseline`
+                   --ragged-min, --split ...), with `roofline` and `cpu_baseline`; on
+                   the metric workload it also carries `baseline_configs`: the headline
+                   point of every BASELINE config (its stated split, else the automatic
+                   schedule) and the fp8 cache at the metric shape, timed the same way in
+                   the same run after the metric and checked against the CPU oracle on
+                   sampled sequences (--no-extra-configs leaves them out)
   --config N       BASELINE.json config N (1-5) on its own workloads: one JSON line per
                    (shape, split_kv) of the config's sweep, each with p50/p95 us, TB/s,
                    the fraction of 8 TB/s and the max-abs error against the CPU oracle on
@@ -123,6 +128,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-plan-hint", action="store_true",
                     help="do not pass the host-side max_pages_per_seq plan hint")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="default run: leave out the BASELINE configs' headline points")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="after the run, copy a MIB-MiB device buffer twice (a kernel of "
                          "known traffic that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -485,6 +492,12 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
         base["tb_s"] = round(wl.bytes / (base["value"] * 1e-6) / 1e12, 6)
         rec["cpu_baseline"] = base
         rec["max_abs_err_vs_fp32"] = max_abs_err(c.out, want, seqs)
+    if metric_workload and not wl.kv8 and not args.single_call and not args.no_extra_configs:
+        # the other BASELINE configs, measured in the same run after the metric
+        del c, wl
+        torch.cuda.empty_cache()
+        rec["baseline_configs"] = extra_points_run(args, torch, lib, dk_lib, attention,
+                                                   layout, dev, stream, host_cpu()[1])
     print(json.dumps(rec), flush=True)
     if args.calibration_copy > 0:
         src = torch.ones(args.calibration_copy << 20, dtype=torch.uint8, device=dev)
@@ -494,55 +507,125 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
         torch.cuda.synchronize()
 
 
+def config_workload(torch, layout, dev, shape, kv_dtype="same"):
+    """The Workload of one CONFIGS shape (a dict without its "splits")."""
+    shape = dict(shape)
+    shape.pop("splits", None)
+    return Workload(torch, layout, dev, shape.pop("batch"), shape.pop("ctx"),
+                    d=shape.pop("d", 128), kv_dtype=kv_dtype, **shape)
+
+
+def oracle_sequences(wl):
+    """Sequences the CPU oracle checks: the first and the last (one for very long
+    contexts)."""
+    return [0] if wl.batch == 1 or max(wl.lens) > 65536 else [0, wl.batch - 1]
+
+
+def measure_point(args, dk_lib, attention, lib, timer, wl, split, stream, want=None,
+                  seqs=None, settle=False):
+    """p50 / p95 us of the full call (flush + events; settling steps when `settle`, then
+    the warm-up), the dominant kernel's average, and the max-abs error of the output
+    against `want` (the CPU oracle's rows of sequences `seqs`) when given."""
+    torch = wl.torch
+    opts, hint = make_opts(dk_lib, args, wl, split)
+    c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
+    dk_lib.check(c.full(), "decode_attention")
+    if settle:
+        timer.settle(c.full)
+    timer.run(c.full, args.warmup)
+    us = sorted(timer.run(c.full, args.steps))
+    p1 = timer.run(c.dominant(), args.steps)
+    dk_lib.check(c.full(), "decode_attention")
+    torch.cuda.synchronize()
+    p50, p95 = statistics.median(us), percentile(us, 95)
+    tbs = wl.bytes / (p50 * 1e-6) / 1e12
+    res = {"split_kv": split, "schedule": c.schedule_name(), "plan_hint_max_pages": hint,
+           "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
+           "tb_s": round(tbs, 4), "frac": round(tbs * 1e12 / (PEAK_GBPS * 1e9), 4),
+           "dominant_kernel_us_avg": round(statistics.fmean(p1), 2),
+           "bytes_per_call": wl.bytes, "output_finite": bool(torch.isfinite(c.out).all())}
+    if want is not None:
+        res["max_abs_err_vs_fp32"] = max_abs_err(c.out, want, seqs)
+        res["oracle_sequences"] = seqs
+    del c
+    return res
+
+
+# The BASELINE configs' headline points carried in the default run's line (each config's
+# stated split where it names one, else the library's automatic schedule), plus the fp8
+# cache at the metric shape (an extension).
+EXTRA_POINTS = [
+    (1, dict(CONFIGS[1][0]), 4, "same"),
+    (1, dict(CONFIGS[1][0]), 0, "same"),
+    *[(2, dict(s), 0, "same") for s in CONFIGS[2]],
+    *[(3, dict(s), 0, "same") for s in CONFIGS[3]],
+    (4, dict(CONFIGS[4][0]), 0, "same"),
+    (5, dict(CONFIGS[5][0]), 0, "same"),
+    (0, dict(batch=32, ctx=8192, dtype="fp16", table="permuted"), 0, "fp8"),
+]
+
+
+def extra_points_run(args, torch, lib, dk_lib, attention, layout, dev, stream, threads):
+    """The EXTRA_POINTS, each checked against the CPU oracle on sampled sequences."""
+    timer = Timer(torch, dev, stream, args.flush)
+    out = []
+    for cid, shape, split, kv_dtype in EXTRA_POINTS:
+        wl = config_workload(torch, layout, dev, shape, kv_dtype)
+        seqs = oracle_sequences(wl)
+        want = None
+        if not args.no_cpu_baseline:
+            _, want = cpu_baseline_masked(wl, seqs, threads, reps=1)
+        r = {"config_id": cid, "workload": wl.label()}
+        # settled on each point: a point's first timed steps otherwise ran up to 5 % slow
+        # after a different shape
+        r.update(measure_point(args, dk_lib, attention, lib, timer, wl, split, stream, want,
+                               seqs, settle=True))
+        out.append(r)
+        # each point's buffers come from fresh device allocations, as in a run of its own
+        del wl, want
+        torch.cuda.empty_cache()
+    return out
+
+
 def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     """BASELINE config N: one JSON line per (shape, split_kv) point of its sweep."""
     ncpu, threads, model = host_cpu()
     timer = Timer(torch, dev, stream, args.flush)
     settled = False
     for shape in CONFIGS[args.config]:
-        shape = dict(shape)
-        splits = shape.pop("splits")
-        wl = Workload(torch, layout, dev, shape.pop("batch"), shape.pop("ctx"),
-                      d=shape.pop("d", 128), **shape)
-        # the CPU oracle on sampled sequences: the first and the last (one for very long
-        # contexts), the checker of every split of this shape and its CPU baseline
-        seqs = [0] if wl.batch == 1 or max(wl.lens) > 65536 else [0, wl.batch - 1]
+        splits = shape["splits"]
+        wl = config_workload(torch, layout, dev, shape)
+        # the CPU oracle on sampled sequences: the checker of every split of this shape
+        # and its CPU baseline
+        seqs = oracle_sequences(wl)
         cpu_s, want = None, None
         if not args.no_cpu_baseline:
             cpu_s, want = cpu_baseline_masked(wl, seqs, threads, reps=1)
         for split in splits:
-            opts, hint = make_opts(dk_lib, args, wl, split)
-            c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
-            dk_lib.check(c.full(), "decode_attention")
             if not settled:
-                timer.settle(c.full)
+                opts, _ = make_opts(dk_lib, args, wl, split)
+                timer.settle(Caller(lib, dk_lib, attention, wl, split, opts, stream).full)
                 settled = True
-            timer.run(c.full, args.warmup)
-            us = sorted(timer.run(c.full, args.steps))
-            p1 = timer.run(c.dominant(), args.steps)
-            dk_lib.check(c.full(), "decode_attention")
-            torch.cuda.synchronize()
-            p50, p95 = statistics.median(us), percentile(us, 95)
-            tbs = wl.bytes / (p50 * 1e-6) / 1e12
+            m = measure_point(args, dk_lib, attention, lib, timer, wl, split, stream, want,
+                              seqs)
             rec = {
-                "metric": CONFIG_METRIC.format(n=args.config), "value": round(tbs, 4),
+                "metric": CONFIG_METRIC.format(n=args.config), "value": m["tb_s"],
                 "unit": "TB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-                "ms_per_step": round(p50 / 1e3, 5), "higher_is_better": True,
+                "ms_per_step": round(m["us_per_call"] / 1e3, 5), "higher_is_better": True,
                 "dtype": wl.dtype_name, "data": "synthetic",
                 "config": {"config_id": args.config, "workload": wl.label(),
                            "batch": wl.batch, "context_length":
                                f"U[{wl.ragged_min},{wl.ctx}]" if wl.ragged_min else wl.ctx,
                            "num_q_heads": wl.hq, "num_kv_heads": wl.hkv, "head_dim": wl.d,
-                           "split_kv": split, "schedule": c.schedule_name(),
-                           "plan_hint_max_pages": hint},
-                "us_per_call": round(p50, 2), "us_per_call_p95": round(p95, 2),
-                "frac": round(tbs * 1e12 / (PEAK_GBPS * 1e9), 4),
-                "pct_of_peak": round(100 * tbs * 1e12 / (PEAK_GBPS * 1e9), 2),
-                "dominant_kernel_us_avg": round(statistics.fmean(p1), 2),
-                "bytes_per_call": wl.bytes, "output_finite": bool(torch.isfinite(c.out).all()),
+                           "split_kv": split, "schedule": m["schedule"],
+                           "plan_hint_max_pages": m["plan_hint_max_pages"]},
+                "us_per_call": m["us_per_call"], "us_per_call_p95": m["us_per_call_p95"],
+                "frac": m["frac"], "pct_of_peak": round(100 * m["frac"], 2),
+                "dominant_kernel_us_avg": m["dominant_kernel_us_avg"],
+                "bytes_per_call": wl.bytes, "output_finite": m["output_finite"],
             }
             if want is not None:
-                rec["max_abs_err_vs_fp32"] = max_abs_err(c.out, want, seqs)
+                rec["max_abs_err_vs_fp32"] = m["max_abs_err_vs_fp32"]
                 rec["oracle_sequences"] = seqs
                 rec["cpu_baseline"] = {
                     "value": round(cpu_s * 1e6, 1), "unit": "us for the sampled sequences",
@@ -550,7 +633,8 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                     "sample": f"numpy fp32 per-sequence oracle (oracle/reference.py) on "
                               f"sequences {seqs}, one run"}
             print(json.dumps(rec), flush=True)
-            del c
+        del wl
+        torch.cuda.empty_cache()
 
 
 def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):

@@ -287,7 +287,13 @@ __device__ __forceinline__ X ld_const(const X* p, int64_t i) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* base, u32 extent) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)extent, 0x00020000);
 }
-constexpr int kBufNT = 2;   // buffer-load cache policy: non-temporal (streamed once)
+// Buffer-load cache policy of the K/V pages: non-temporal (nt, bit 1; streamed once). A
+// build may set another policy word with DK_LOAD_POLICY (bit 0 sc0, bit 4 sc1) for
+// comparisons.
+#ifndef DK_LOAD_POLICY
+#define DK_LOAD_POLICY 2
+#endif
+constexpr int kBufNT = DK_LOAD_POLICY;
 
 // NWORDS consecutive words at base + voff + soff (NWORDS in {2, 4, 8}), streaming.
 template <int NWORDS>

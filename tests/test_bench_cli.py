@@ -90,3 +90,28 @@ def test_cpu_baseline_legs_agree_with_the_oracle(ragged):
         assert np.abs(got.numpy() - want).max() < 2e-6
         assert bench.max_abs_err(torch.from_numpy(np.zeros((5, 8, 64), np.float16)), got, seqs) \
             == float(got.abs().max())
+
+
+def test_default_line_carries_every_baseline_config():
+    # the metric run's `baseline_configs`: config 1 at its stated split 4 and automatic,
+    # every config 2 batch, all four config 3 shapes, the ragged mix and config 5, plus
+    # the fp8 cache at the metric shape
+    pts = bench.EXTRA_POINTS
+    assert {cid for cid, *_ in pts} == {0, 1, 2, 3, 4, 5}
+    assert [(s["batch"], split) for cid, s, split, _ in pts if cid == 1] == [(2, 4), (2, 0)]
+    assert sorted(s["batch"] for cid, s, _, _ in pts if cid == 2) == [1, 4, 16, 32, 64]
+    assert {(s["batch"], s["ctx"]) for cid, s, _, _ in pts if cid == 3} == {
+        (1, 32768), (1, 131072), (4, 32768), (4, 131072)}
+    assert [kv for cid, _, _, kv in pts if cid == 0] == ["fp8"]
+    # shapes build as the config sweeps build them (on the CPU, at a small context; the
+    # ragged mix's 65536-page free list is left out here)
+    import torch
+
+    import layout
+    for cid, shape, _, kv in pts:
+        if shape.get("ragged_min"):
+            continue
+        small = dict(shape, batch=2, ctx=64)
+        wl = bench.config_workload(torch, layout, "cpu", small, "same")
+        assert wl.d == shape.get("d", 128) and wl.dtype_name == shape["dtype"]
+        assert bench.oracle_sequences(wl) == [0, 1]
