@@ -435,12 +435,13 @@ class DecodePlan:
         for layer in layers:
             out = plan.run(q_l, kv_l, kv_indptr, kv_indices, kv_last_page_len, out=out_l)
 
-    run() takes tensors with the planned shapes, strides, dtypes and devices: the shapes
-    and strides of q, the cache, the page tables and `out` are compared with the plan's
-    (the strides are what the kernels address memory with), dtypes and devices are not.
-    `out` may be None (a contiguous one is allocated; then the plan must have been made
-    without one) and `workspace` must hold at least the planned bytes (the library checks
-    its size on every call). Keyword options are those of decode_attention.
+    run() takes tensors with the planned shapes, strides, dtypes and devices: those of q,
+    the cache, the page tables, `out` and the workspace's device are compared with the
+    plan's (the strides are what the kernels address memory with; a tensor on another
+    device would be addressed as if it were on the planned one). `out` may be None (a
+    contiguous one is allocated; then the plan must have been made without one) and
+    `workspace` must hold at least the planned bytes (the library checks its size on every
+    call). Keyword options are those of decode_attention.
     """
 
     def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=1, *,
@@ -457,18 +458,27 @@ class DecodePlan:
 
     @staticmethod
     def _layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
-        kv = (kv_data.shape, kv_data.stride()) if isinstance(kv_data, torch.Tensor) else \
-            tuple((t.shape, t.stride()) for t in kv_data)
-        return (q.shape, q.stride(), kv, kv_indptr.shape, kv_indptr.stride(), kv_indices.shape,
-                kv_indices.stride(), kv_last_page_len.shape, kv_last_page_len.stride())
+        kv = (kv_data.shape, kv_data.stride(), kv_data.dtype, kv_data.device) \
+            if isinstance(kv_data, torch.Tensor) else \
+            tuple((t.shape, t.stride(), t.dtype, t.device) for t in kv_data)
+        return (q.shape, q.stride(), q.dtype, q.device, kv, kv_indptr.shape, kv_indptr.stride(),
+                kv_indptr.device, kv_indices.shape, kv_indices.stride(), kv_indices.device,
+                kv_last_page_len.shape, kv_last_page_len.stride(), kv_last_page_len.device)
 
     def run(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out=None,
             workspace=None):
         if self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) != self._guard:
-            _fail("DecodePlan.run: the tensors differ in shape or strides from the planned call")
-        if (None if out is None else out.stride()) != self._out_strides or \
-                (out is not None and out.shape != q.shape):
-            _fail("DecodePlan.run: out differs from the planned call (none, or its strides)")
+            _fail("DecodePlan.run: the tensors differ in shape, strides, dtype or device from "
+                  "the planned call")
+        if out is None:
+            if self._out_strides is not None:
+                _fail("DecodePlan.run: the plan was made with an out tensor")
+        elif out.stride() != self._out_strides or out.shape != q.shape or \
+                out.dtype != q.dtype or out.device != q.device:
+            _fail("DecodePlan.run: out differs from the planned call (none, or its shape, "
+                  "strides, dtype or device)")
+        if workspace is not None and workspace.device != q.device:
+            _fail(f"DecodePlan.run: workspace must be on {q.device}, got {workspace.device}")
         return _launch(self._plan, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out,
                        workspace)
 
@@ -517,9 +527,15 @@ def merge_partials(partial_o: torch.Tensor, partial_m: torch.Tensor, partial_l: 
     src/cuda_/attention_ext.cu:363-406) into a (B, Hq, D) tensor of `dtype`."""
     if dtype not in _DTYPE_CODE:
         _fail(f"dtype must be fp16 or bf16, got {dtype}")
+    if not isinstance(partial_o, torch.Tensor) or partial_o.dim() != 4:
+        _fail("partial_o must be a (B, Hq, S, D) tensor")
     batch, hq, split, d = partial_o.shape
     if partial_m.shape != (batch, hq, split) or partial_l.shape != (batch, hq, split):
         _fail("partial_m / partial_l must be (B, Hq, S)")
+    if not partial_o.is_cuda:
+        _fail("partial_o must be on CUDA (the merge runs on its device)")
+    if d not in SUPPORTED_HEAD_DIMS:
+        _fail(f"head_dim must be 64, 128, or 256; got {d}")
     lib = dk_lib.load()
     off_o, off_m, off_l, total = dk_lib.partials_layout(batch, hq, d, split)
     ws = torch.empty(total, dtype=torch.uint8, device=partial_o.device)

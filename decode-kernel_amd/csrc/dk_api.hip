@@ -607,6 +607,9 @@ int dk_merge_partials(const void* workspace, size_t workspace_bytes, void* out, 
     return dk::set_error(DK_EINVAL, "dk_merge_partials: bad argument");
   if (batch == 0) return DK_OK;
   if (!workspace || !out) return dk::set_error(DK_ENULL, "workspace and out must be non-NULL");
+  // the partials are read as float vectors from 256-byte aligned arrays
+  if (((uintptr_t)workspace % 256) != 0)
+    return dk::set_error(DK_EWORKSPACE, "workspace must be 256-byte aligned");
   if ((int64_t)batch * num_q_heads > INT32_MAX / 4)
     return dk::set_error(DK_EINVAL, "dk_merge_partials: batch*num_q_heads too large");
   size_t off_o, off_m, off_l, need;

@@ -153,6 +153,9 @@ def test_null_strides_and_partials_entry_point():
     assert rc == dk_lib.DK_EWORKSPACE
     rc = lib.dk_merge_partials(None, 0, None, 1, 32, 96, 0, 0, 0, 4, None)
     assert rc == dk_lib.DK_EINVAL
+    # a workspace not 256-byte aligned is refused before any launch (like pass 1's)
+    rc = lib.dk_merge_partials(0x10010, 1 << 20, 0x20000, 1, 32, 128, 0, 4096, 128, 4, None)
+    assert rc == dk_lib.DK_EWORKSPACE and b"aligned" in lib.dk_last_error()
 
 
 # ---------------------------------------------------------------- Python-side checks
@@ -251,3 +254,14 @@ def test_options_struct_matches_header():
     for (ty, n), (_, cty) in zip(declared, fields):
         base = cty._type_ if issubclass(cty, ctypes.Array) else cty
         assert base is ctype[ty], n
+
+
+def test_python_merge_partials_refuses_cpu_partials_and_bad_shapes():
+    po = torch.zeros(1, 4, 2, 128)
+    pm, pl = torch.zeros(1, 4, 2), torch.ones(1, 4, 2)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="on CUDA"):
+        attention.merge_partials(po, pm, pl)
+    with pytest.raises(dk_lib.DecodeArgumentError, match=r"\(B, Hq, S\)"):
+        attention.merge_partials(po, pm[:, :3], pl)
+    with pytest.raises(dk_lib.DecodeArgumentError, match=r"\(B, Hq, S, D\)"):
+        attention.merge_partials(po[0], pm, pl)

@@ -95,12 +95,30 @@ def test_decode_plan_rejects_a_different_layout_before_any_device_work():
             torch.ones(2, dtype=torch.int32))
     plan._guard = attention.DecodePlan._layout(q, kv, *tabs)
     plan._out_strides = None
-    with pytest.raises(dk_lib.DecodeArgumentError, match="shape or strides"):
+    with pytest.raises(dk_lib.DecodeArgumentError, match="shape, strides"):
         plan.run(torch.zeros(3, 32, 128, dtype=torch.float16), kv, *tabs)
-    with pytest.raises(dk_lib.DecodeArgumentError, match="shape or strides"):
+    with pytest.raises(dk_lib.DecodeArgumentError, match="shape, strides"):
         plan.run(q, torch.zeros(4, 2, 16, 8, 256, dtype=torch.float16)[..., ::2], *tabs)
     with pytest.raises(dk_lib.DecodeArgumentError, match="out differs"):
         plan.run(q, kv, *tabs, out=torch.zeros(2, 32, 128, dtype=torch.float16))
+    # another dtype (q or the cache) or device (a page table) than planned
+    with pytest.raises(dk_lib.DecodeArgumentError, match="dtype or device"):
+        plan.run(q.to(torch.bfloat16), kv, *tabs)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="dtype or device"):
+        plan.run(q, kv.to(torch.bfloat16), *tabs)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="dtype or device"):
+        plan.run(q, kv, tabs[0].to("meta"), *tabs[1:])
+    # a plan made with `out`: out must keep its strides, dtype and device
+    plan._out_strides = q.stride()
+    with pytest.raises(dk_lib.DecodeArgumentError, match="made with an out"):
+        plan.run(q, kv, *tabs)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="out differs"):
+        plan.run(q, kv, *tabs, out=torch.zeros(2, 32, 128, dtype=torch.bfloat16))
+    with pytest.raises(dk_lib.DecodeArgumentError, match="out differs"):
+        plan.run(q, kv, *tabs, out=torch.zeros(2, 32, 128, dtype=torch.float16, device="meta"))
+    with pytest.raises(dk_lib.DecodeArgumentError, match="workspace must be on"):
+        plan.run(q, kv, *tabs, out=torch.zeros(2, 32, 128, dtype=torch.float16),
+                 workspace=torch.zeros(16, dtype=torch.uint8, device="meta"))
 
 
 @pytest.mark.gpu
