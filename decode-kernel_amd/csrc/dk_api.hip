@@ -158,25 +158,46 @@ int64_t balanced_groups(const Problem& p, const Plan& pl, int cus, int hp = 1) {
   return std::min(max_groups, std::max(hc, (groups + hc / 2) / hc * hc));
 }
 
-// Whether split_kv == 0 runs the one-pass kernel: forced by options.schedule; else only
-// with the max_pages_per_seq hint, when one workgroup per (sequence, head chunk) fits in
-// the balanced grid and no sequence is longer than a balanced workgroup's share of
-// pages (then one pass finishes no later and needs no merge). Pass-1-only calls always
-// take the balanced schedule (they return partials).
-bool auto_one_pass(const Problem& p, const Plan& pl, int cus) {
-  if (!p.need_out || p.opt.schedule == 1) return false;
-  if (p.opt.schedule == 2) return true;
-  // rows of at most 64 bytes: the balanced schedule with grouped kv heads
-  if ((int64_t)p.head_dim * p.kv_esize() <= kGroupedAlwaysRowBytes &&
-      grouped_kv_heads(p, pl, cus) > 1)
-    return false;
-  const int64_t hint = p.opt.max_pages_per_seq;
-  if (hint <= 0) return false;
+// Whether one workgroup per (sequence, head chunk) with pl's wavefronts per workgroup fits
+// in the balanced grid of the same shape, and no sequence (plan hint) is longer than a
+// balanced workgroup's share of pages: then one pass finishes no later and needs no merge.
+bool one_pass_fits(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t groups = balanced_groups(p, pl, cus);
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   const int64_t per_group = groups / pl.pairs_per_seq;   // workgroups per head chunk
   const int64_t share = (p.num_indices + per_group - 1) / per_group;
   return pairs <= groups && hint <= share;
+}
+
+// Wavefronts per workgroup of the one-pass kernel that split_kv == 0 runs, or 0 for the
+// balanced schedule. Forced by options.schedule; else only with the max_pages_per_seq
+// hint, when one pass fits (one_pass_fits) at the default wavefronts per workgroup, or, for
+// 256-byte rows (16-bit caches at D = 128) with the default wave counts, at one wavefront
+// per workgroup: twice the workgroups at the same wavefronts per CU, so that uniform
+// batches of up to twice the CUs' (sequence, kv head) pairs run without the merge (B=64
+// ctx 4096, us, balanced vs one pass NW=1: 32/8 161.2 vs 160.0, bf16 161.9 vs 160.3, 64/8
+// 177.9 vs 165.3; B=64 ctx 8192 317.4 vs 314.4; slower where the pairs do not fill the
+// CUs evenly, e.g. B=48 127.2 vs 148.1, which the share condition excludes, and over
+// narrow rows, e.g. fp8 96.1 vs 157.7). Pass-1-only calls always take the balanced
+// schedule (they return partials).
+int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
+  if (!p.need_out || p.opt.schedule == 1) return 0;
+  if (p.opt.schedule == 2) return pl.waves;
+  // rows of at most 64 bytes: the balanced schedule with grouped kv heads
+  if ((int64_t)p.head_dim * p.kv_esize() <= kGroupedAlwaysRowBytes &&
+      grouped_kv_heads(p, pl, cus) > 1)
+    return 0;
+  const int64_t hint = p.opt.max_pages_per_seq;
+  if (hint <= 0) return 0;
+  if (one_pass_fits(p, pl, cus, hint)) return pl.waves;
+  const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
+  if (auto_waves && pl.waves == kDefaultWavesPerGroup &&
+      waves_per_cu(p, pl) == kDefaultWavesPerCU && p.head_dim == 128 && p.kv_esize() == 2) {
+    Plan one = pl;
+    one.waves = 1;
+    if (one_pass_fits(p, one, cus, hint)) return 1;
+  }
+  return 0;
 }
 
 }  // namespace
@@ -218,9 +239,10 @@ int run(Problem p, bool do_merge, void* stream) {
     const int dev = current_device(-1);
     const int cus = cu_count(dev);
     if (cus <= 0) return hip_fail(hipErrorNoDevice, "compute-unit count");
-    if (auto_one_pass(p, pl, cus)) {
+    if (const int one_pass_waves = auto_one_pass(p, pl, cus)) {
       p.split = 1;
       pl.balanced = false;
+      pl.waves = one_pass_waves;
       pl.grid = split_grid(p.batch, p.hkv, 1, pl.chunks);
     } else {
       hp = grouped_kv_heads(p, pl, cus);
@@ -496,7 +518,7 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, i
   const int dev = dk::current_device(device);
   const int cus = dk::cu_count(dev);
   if (cus <= 0) return dk::hip_fail(hipErrorNoDevice, "dk_plan_schedule");
-  return dk::auto_one_pass(p, dk::make_plan(p), cus) ? 1 : 0;
+  return dk::auto_one_pass(p, dk::make_plan(p), cus) > 0 ? 1 : 0;
 }
 
 int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv_indptr,

@@ -595,3 +595,33 @@ def test_plan_hint_one_pass_on_uniform_batch(dtype):
     torch.cuda.synchronize()
     _check(a, want, rows=list(range(0, 32, 5)), label="hinted")
     assert torch.allclose(a.float(), b.float(), atol=2e-3)
+
+
+@pytest.mark.parametrize("hq", [32, 64])
+def test_plan_hint_one_pass_one_wave_on_twice_the_pairs(hq):
+    # a uniform batch of twice the pairs the two-wavefront grid holds: with the hint the
+    # automatic schedule is the one pass at one wavefront per workgroup (no merge); a batch
+    # whose pairs do not fill the CUs evenly stays balanced; results agree with the oracle
+    # and with the balanced schedule
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    batch = 2 * cus // 8                      # 2 * CUs (sequence, kv head) pairs
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, 1000, hq, 8, 128, device=DEV, page_table="permuted", seed=hq)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[torch.float16]
+    opts = dk_lib.options(max_pages_per_seq=hint)
+    assert dk_lib.plan_schedule(batch, hq, 8, 128, ids.shape[0], code, 0, opts) == 1
+    # user-set wave counts, or three quarters of the batch: the balanced schedule
+    assert dk_lib.plan_schedule(batch, hq, 8, 128, ids.shape[0], code, 0,
+                                dk_lib.options(waves_per_cu=2, max_pages_per_seq=hint)) == 0
+    b3 = batch * 3 // 4
+    assert dk_lib.plan_schedule(b3, hq, 8, 128, b3 * 63, code, 0, opts) == 0
+    rows = list(range(0, batch, 7))
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
+    _announce(f"one pass one wave hq={hq} batch={batch}")
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0, schedule=1)
+    torch.cuda.synchronize()
+    _check(a, want, rows=rows, label="one pass, one wave")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
