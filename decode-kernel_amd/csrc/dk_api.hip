@@ -209,6 +209,7 @@ int run(Problem p, bool do_merge, void* stream) {
   if (rc != DK_OK || p.batch == 0) return rc;
   Plan pl = make_plan(p);
   int waves_per_pair = 0;   // balanced: workgroups per head chunk
+  int seg_cost = 0;         // balanced: pages charged per change of sequence
   int hp = 1;               // balanced: kv heads per workgroup
   if (pl.balanced && p.opt.window > 0) {
     // a sliding window bounds every sequence's pages: explicit splits of the window's
@@ -264,6 +265,12 @@ int run(Problem p, bool do_merge, void* stream) {
       }
       pl.grid = balanced_groups(p, pl, cus, hp);
       waves_per_pair = (int)(pl.grid / (pl.pairs_per_seq / hp));
+      // a ragged batch (plan hint: the longest sequence well above the mean): charge each
+      // change of sequence in the range split, so that ranges crossing more sequences get
+      // fewer pages (a kernel build of its own, for one kv head per workgroup)
+      if (hp == 1 && p.need_out && hint > 0 && p.batch > 1 &&
+          hint * (int64_t)p.batch * 4 > p.num_indices * (int64_t)5)
+        seg_cost = kSegmentCostPerWave * pl.waves;
     }
   }
   const bool direct = p.need_out && (p.split == 1 || pl.balanced);
@@ -315,6 +322,7 @@ int run(Problem p, bool do_merge, void* stream) {
   a.page_extent = (uint32_t)(((int64_t)(kPageSize - 1) * p.st.kv_s + p.head_dim) * kes);
   a.direct = direct ? 1 : 0;
   a.ranges = waves_per_pair;
+  a.seg_cost = pl.balanced ? seg_cost : 0;
   const bool kv8 = pl.kv8;
   const float k_scale = kv8 && p.opt.k_scale != 0.f ? p.opt.k_scale : 1.f;
   const float score_scale =
@@ -336,6 +344,7 @@ int run(Problem p, bool do_merge, void* stream) {
   L.balanced = pl.balanced;
   L.kv8 = pl.kv8;
   L.hp = hp;
+  L.cost = a.seg_cost > 0;
   L.grid = (int)pl.grid;
   if (pl.balanced && pl.chunks > 1) {
     // the chunks of a (range, kv-head group) unit sit kXcds workgroup ids apart: whole
@@ -373,6 +382,7 @@ int run(Problem p, bool do_merge, void* stream) {
     m.chunks = pl.chunks;
     m.hkv = p.hkv;
     m.waves_per_pair = waves_per_pair;
+    m.seg_cost = a.seg_cost;
     TraceRange tr("dk_merge %s B=%d Hq=%d D=%d", pl.balanced ? "balanced" : "split",
                   p.batch, p.hq, p.head_dim);
     e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)

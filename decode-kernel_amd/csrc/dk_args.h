@@ -39,6 +39,12 @@ constexpr int kSmallUnitsPerCU = 32;
 // us: B=128 ctx 2048 166 vs 174, B=256 ctx 1024 176 vs 185, 64/8 B=256 ctx 1024 188 vs
 // 204, 16/4 93 vs 99; sequences of 1/2 to 1/4 of a range, or ragged, ~1 % either way)
 constexpr int kShortSegments = 4;
+// Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
+// (its reduction, combine, stores and pipeline refill), which at two wavefronts per
+// workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5
+// / 7 sequences ended at 323.6 / 331.0 / 336.7 us); the range split charges each sequence
+// start this many pages per wavefront of the workgroup.
+constexpr int kSegmentCostPerWave = 5;
 // Balanced schedule over narrow rows: 4 neighbouring kv heads per workgroup, 2 wavefronts
 // each, one such workgroup per CU (64- and 128-byte row segments 512 B or 1 KB apart
 // stream far better when the segments of neighbouring heads are fetched together). B=32

@@ -7,5 +7,5 @@
 #endif
 
 namespace dk {
-template const void* pass1_sym_g<BF16, DK_HEAD_DIM, true, true>(int, int, bool, int);
+template const void* pass1_sym_g<BF16, DK_HEAD_DIM, true, true>(int, int, bool, int, bool);
 }  // namespace dk

@@ -116,6 +116,8 @@ struct Pass1Args {
   float cap_in, cap_out;              // logit soft-cap: x = cap_out * tanh(q.k * cap_in)
                                       // (cap_out == 0: off, x = q.k * kscale)
   float vscale;                       // V dequant scale (1 unless the cache is fp8)
+  int32_t seg_cost;                   // balanced, COST build: pages a change of sequence is
+                                      // charged in the range split
 };
 
 struct MergeArgs {
@@ -128,6 +130,7 @@ struct MergeArgs {
   const int32_t* indptr;              // balanced: recompute each pair's slots
   int32_t num_indices, pairs_per_seq, heads, waves_per_pair;
   int32_t group, per, chunks, hkv;    // balanced: q head -> (head chunk, slot row)
+  int32_t seg_cost;                   // balanced: pass 1's seg_cost (0: equal page ranges)
 };
 
 // ---------------------------------------------------------------- element types
@@ -1295,17 +1298,61 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
 }
 
 // ---------------------------------------------------------------- pass 1, balanced
+// Range split of the balanced schedule. A head chunk's units (its pages in sequence order,
+// x = 0 .. P-1) carry the cost x + A * seq(x), where seq(x) is the largest b with
+// start(b) <= x (start(b) = kv_indptr[b] - kv_indptr[0]): every sequence start is charged
+// A pages, what a change of sequence costs a workgroup. The cost space [0, C), C = P +
+// A * (batch - 1), is cut into Wg ranges of Lc = ceil(C / Wg); range j holds the units with
+// floor(cost / Lc) == j, contiguous since the cost grows with x. With A = 0 these are the
+// equal page ranges. The merge kernel finds a sequence's ranges with the same formula.
+__device__ __forceinline__ int64_t range_cost_len(int P, int A, int batch, int Wg) {
+  const int64_t C = (int64_t)P + (int64_t)A * max(batch - 1, 0);
+  return (C + Wg - 1) / Wg;
+}
+
+// First unit of the cost interval starting at T (A > 0): the smallest x with
+// x + A * seq(x) >= T, or P. *b_out = the largest b with f(b) = start(b) + A * b <= T (the
+// sequence holding x, or the last one before it). A search over kv_indptr by one wavefront,
+// 64 candidates per step (f grows with b: one step up to 64 sequences, two up to 4096);
+// every lane returns the same values.
+__device__ __forceinline__ int cost_boundary(const Pass1Args& a, int base, int P, int A,
+                                             int64_t T, int* b_out) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, S = a.batch;   // the answer is in [lo, lo + S); f(lo) <= T
+  while (S > 1) {
+    const int st = (S + 63) / 64;
+    const bool in = lane * st < S;
+    const int bi = min(lo + lane * st, a.batch);   // kv_indptr has batch + 1 entries
+    const int64_t fb = (int64_t)(seq_begin(a, bi) - base) + (int64_t)A * bi;
+    const int64_t f = in ? fb : INT64_MAX;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(f <= T);
+    const int k = m ? 63 - __builtin_clzll(m) : 0;   // lane 0 holds f(lo) <= T
+    lo += k * st;
+    S = min(st, S - k * st);
+  }
+  const int b = uniform(lo);
+  const int sb = seq_begin(a, b) - base;
+  const int se = max(seq_begin(a, b + 1) - base, sb);
+  const int64_t f = (int64_t)sb + (int64_t)A * b;
+  *b_out = b;
+  const int64_t x = min((int64_t)sb + max(T - f, (int64_t)0), (int64_t)se);
+  return (int)min(max(x, (int64_t)0), (int64_t)P);
+}
+
 // Head-major persistent schedule over workgroups. Each of the HC = hkv * chunks head
 // chunks (hc = chunk * hkv + kv head) has Wg = a.ranges workgroups; consecutive
 // workgroups -- and the XCDs they are dispatched to round-robin -- cover all kv heads of
 // the same pages at the same time. The Wg workgroups of a head chunk split its pages in sequence
 // order ((b, page) is linear unit seq_begin(b) - seq_begin(0) + page) into Wg ranges of
-// L = ceil(P / Wg) pages; workgroup j takes range j and its NW wavefronts interleave the
-// pages of each segment (maximal run of the range inside one sequence). A sequence covered
-// by a single segment is written out directly (when a.direct); otherwise the segment is
-// stored as a partial at slot hc * (Wg + batch) + j + b (unique, < HC * (Wg + batch)) for the
-// merge kernel.
-template <class T, int D, int G, int NW, bool MFMA, bool KV8, int HP>
+// equal cost (range_cost_len: equal pages, or with a.seg_cost pages charged per sequence
+// start); workgroup j takes range j and its NW wavefronts interleave the pages of each
+// segment (maximal run of the range inside one sequence). A sequence covered by a single
+// segment is written out directly (when a.direct); otherwise the segment is stored as a
+// partial at slot hc * (Wg + batch) + j + b (unique, < HC * (Wg + batch), as the ranges are
+// contiguous and ordered) for the merge kernel.
+// COST: the build whose range split charges sequence starts (a.seg_cost, ragged batches);
+// the other one splits equal pages and carries none of that code.
+template <class T, int D, int G, int NW, bool MFMA, bool KV8, int HP, bool COST = false>
 __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) void dk_pass1_balanced(Pass1Args a) {
   using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> smh[HP];
@@ -1342,10 +1389,23 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   }
   const int base = seq_begin(a, 0);
   const int P = max(seq_begin(a, a.batch) - base, 0);        // pages per head chunk
-  const int L = (P + Wg - 1) / Wg;
-  if (L <= 0) return;                                        // whole workgroup
-  int u = (int)min((int64_t)j * L, (int64_t)P);
-  const int u_end = min(u + L, P);
+  const int A = COST ? a.seg_cost : 0;
+  int u, u_end, b = 0;   // the range's units [u, u_end); b: the sequence search's result
+  int L = 0;             // A == 0: pages per range
+  int64_t Lc = 0;        // A > 0: cost per range
+  if (A == 0) {
+    L = (P + Wg - 1) / Wg;
+    if (L <= 0) return;                                      // whole workgroup
+    u = (int)min((int64_t)j * L, (int64_t)P);
+    u_end = min(u + L, P);
+  } else {
+    Lc = range_cost_len(P, A, a.batch, Wg);
+    if (Lc <= 0) return;
+    u = cost_boundary(a, base, P, A, (int64_t)j * Lc, &b);
+    int b_end;
+    u_end = (int64_t)(j + 1) * Lc >= (int64_t)P + (int64_t)A * max(a.batch - 1, 0)
+                ? P : cost_boundary(a, base, P, A, (int64_t)(j + 1) * Lc, &b_end);
+  }
   if (u >= u_end) return;
 
   const int kvh = hc % a.hkv, chunk = hc / a.hkv;
@@ -1366,18 +1426,31 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   u32 ka[WV::KB], va[WV::VB];   // unused (and allocated no registers) unless PRE
   if constexpr (PRE) wv.load_page(ka, va, page_at(base + min(u + w, u_end - 1)), u + w < u_end);
 
-  // sequence containing unit u: the largest b with start(b) <= u (binary search)
-  int lo = 0, hi = a.batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (seq_begin(a, mid) - base <= u) lo = mid; else hi = mid - 1;
+  if (A == 0) {
+    // sequence containing unit u: the largest b with start(b) <= u (binary search)
+    int lo = 0, hi = a.batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seq_begin(a, mid) - base <= u) lo = mid; else hi = mid - 1;
+    }
+    b = lo;
   }
-  int b = lo;
   // q of that sequence, in flight with its bounds below
   wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
   int seq0 = seq_begin(a, b);
   int np = max(seq_begin(a, b + 1), seq0) - seq0;
   int pg = u - (seq0 - base);
+  if (A != 0 && pg >= np) {
+    // the range starts at the next non-empty sequence (its first cost fell in the charge of
+    // sequence b's start)
+    do {
+      ++b;
+      seq0 = seq_begin(a, b);
+      np = max(seq_begin(a, b + 1), seq0) - seq0;
+      pg = u - (seq0 - base);
+    } while (pg >= np && b < a.batch - 1);
+    wv.load_q(a.q + (int64_t)b * a.q_b + (int64_t)qh0 * a.q_h, a.q_h);
+  }
   if (np <= 0 || pg < 0 || pg >= np) return;   // only for a decreasing kv_indptr (invalid)
 
   // Segment after segment; the next segment's q (and, PRE, this wavefront's first page of
@@ -1422,8 +1495,15 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     }
 
     wv.reduce_rows();
+    // ranges holding this sequence's units (cost = unit + A * sequence)
     const int start = cur_seq0 - base;
-    const int nslots = (start + cur_np - 1) / L - start / L + 1;
+    int nslots;
+    if (A == 0) {
+      nslots = (start + cur_np - 1) / L - start / L + 1;
+    } else {
+      const int64_t c0 = (int64_t)start + (int64_t)A * cur_b;
+      nslots = (int)((c0 + cur_np - 1) / Lc - c0 / Lc + 1);
+    }
     combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
                                a.out + (int64_t)cur_b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
                                ((int64_t)hc * (Wg + a.batch) + j + cur_b) * G, 1, w,
@@ -1506,7 +1586,8 @@ __global__ __launch_bounds__(256) void dk_merge_split(MergeArgs m) {
   merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, m.split, 1);
 }
 
-template <class T, int D>
+// COST: pass 1 ran the charged range split (m.seg_cost); the other build carries none of it.
+template <class T, int D, bool COST = false>
 __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= m.batch * m.hq) return;
@@ -1515,19 +1596,31 @@ __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
   auto sb = [&](int bb) { return min(max(ld_const(m.indptr, bb), 0), m.num_indices); };
   const int base = sb(0);
   const int P = max(sb(m.batch) - base, 0);
-  const int L = (P + Wg - 1) / Wg;
   const int seq0 = sb(b);
   const int np = max(sb(b + 1), seq0) - seq0;
   const int kvh = qh / m.group, r = qh % m.group;
   const int hc = (r / m.per) * m.hkv + kvh, g = r % m.per;   // chunk-major; slot row g of G
   int nslots = 0;
   int64_t r0 = 0;
-  if (np > 0 && L > 0) {
-    const int start = seq0 - base;
-    const int j0 = start / L;
-    nslots = (start + np - 1) / L - j0 + 1;
-    r0 = ((int64_t)hc * (Wg + m.batch) + j0 + b) * G + g;
+  // the ranges of pass 1 that hold this sequence's units (its range split: equal pages, or
+  // the charged split's cost)
+  int j0 = 0;
+  if constexpr (!COST) {
+    const int L = (P + Wg - 1) / Wg;
+    if (np > 0 && L > 0) {
+      const int start = seq0 - base;
+      j0 = start / L;
+      nslots = (start + np - 1) / L - j0 + 1;
+    }
+  } else {
+    const int64_t Lc = range_cost_len(P, m.seg_cost, m.batch, Wg);
+    if (np > 0 && Lc > 0) {
+      const int64_t c0 = (int64_t)(seq0 - base) + (int64_t)m.seg_cost * b;
+      j0 = (int)(c0 / Lc);
+      nslots = (int)((c0 + np - 1) / Lc) - j0 + 1;
+    }
   }
+  if (nslots > 0) r0 = ((int64_t)hc * (Wg + m.batch) + j0 + b) * G + g;
   if (nslots == 1) return;   // pass 1 wrote this head's output
   // slot k of this pair is r0 + k * G (rows of G heads per slot); none -> zeros
   merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, nslots, (int64_t)G);
