@@ -157,8 +157,10 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *   split_kv == 0: automatic: the balanced schedule (a persistent grid of about
  *                  options.waves_per_cu wavefronts per compute unit whose workgroups each
  *                  stream an equal share of all (sequence, kv head, page) units whatever
- *                  the lengths; sequences one workgroup covers are written directly, the
- *                  rest merged), or the split_kv == 1 pass when options.max_pages_per_seq
+ *                  the lengths -- for a batch the plan hint shows to be ragged, equal
+ *                  shares of pages plus a charge per sequence start; sequences one
+ *                  workgroup covers are written directly, the rest merged), or the
+ *                  split_kv == 1 pass when options.max_pages_per_seq
  *                  shows that one workgroup per pair fits that grid and is no longer
  *                  (never for kv-head rows of <= 64 bytes, which stream faster with
  *                  grouped kv heads in the balanced schedule).
