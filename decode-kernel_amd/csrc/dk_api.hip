@@ -267,10 +267,10 @@ int run(Problem p, bool do_merge, void* stream) {
       waves_per_pair = (int)(pl.grid / (pl.pairs_per_seq / hp));
       // a ragged batch (plan hint: the longest sequence well above the mean): charge each
       // change of sequence in the range split, so that ranges crossing more sequences get
-      // fewer pages (a kernel build of its own, for one kv head per workgroup)
-      if (hp == 1 && p.need_out && hint > 0 && p.batch > 1 &&
+      // fewer pages (a kernel build of its own)
+      if (p.need_out && hint > 0 && p.batch > 1 &&
           hint * (int64_t)p.batch * 4 > p.num_indices * (int64_t)5)
-        seg_cost = kSegmentCostPerWave * pl.waves;
+        seg_cost = kSegmentCostPerWave * pl.waves;   // per head's pages (any kv heads per group)
     }
   }
   const bool direct = p.need_out && (p.split == 1 || pl.balanced);

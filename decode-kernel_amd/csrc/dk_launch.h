@@ -68,11 +68,14 @@ const void* pass1_sym(bool balanced, int hp, bool cost) {
   if (hp == 1)
     return cost ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 1, true>)
                 : reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 1>);
-  if (cost) return nullptr;   // the charged split is built for one kv head per workgroup
   // several kv heads per workgroup: rows of at most kNarrowRowBytes, two wavefronts each
   if constexpr (D * (KV8 ? 1 : 2) <= kNarrowRowBytes && NW == 2) {
-    if (hp == 2) return reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 2>);
-    if (hp == 4) return reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 4>);
+    if (hp == 2)
+      return cost ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 2, true>)
+                  : reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 2>);
+    if (hp == 4)
+      return cost ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 4, true>)
+                  : reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 4>);
   }
   return nullptr;
 }

@@ -269,3 +269,31 @@ def test_fp8_partials_match_oracle():
         O, m, l = skv.split_partials(to_np(q).astype(np.float32), deq, to_np(indptr),
                                      to_np(ids), to_np(last), S)
         check_partials(po, pm, pl, O, m, l, q.dtype)
+
+
+@pytest.mark.parametrize("batch", [65, 2000])
+def test_ragged_fp8_charged_range_split_matches_oracle(batch):
+    # a ragged batch over an fp8 cache with the plan hint: the balanced schedule groups
+    # kv heads (128-byte rows) and charges each sequence start in its range split
+    rng = np.random.default_rng(batch + 3)
+    hi = 40 if batch > 100 else 2500
+    lens = [int(x) for x in rng.integers(0, hi, size=batch)]
+    lens[-1] = 3 * hi
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, lens, 32, 8, 128, device=DEV, page_table="permuted", seed=batch)
+    codes = _quantize(kv, 0.5, 0.25)
+    deq = _dequantize(codes, 0.5, 0.25)
+    rows = list(range(0, batch, max(batch // 50, 1))) + [batch - 1]
+    want = ref.reference_attention_paged(to_np(q).astype(np.float32), deq, to_np(indptr),
+                                         to_np(ids), to_np(last), batch_subset=rows)
+    kv8 = _codes_to_device(codes)
+    hint = attention.plan_hint(indptr.cpu())
+    _announce(f"fp8 ragged charged split batch={batch}")
+    out = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=0, schedule=1,
+                                     max_pages_per_seq=hint, k_scale=0.5, v_scale=0.25)
+    ref_out = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=0, schedule=1,
+                                         k_scale=0.5, v_scale=0.25)
+    torch.cuda.synchronize()
+    mx, mean = err_stats(out[rows], want[rows])
+    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+    assert torch.allclose(out.float(), ref_out.float(), atol=2e-3)

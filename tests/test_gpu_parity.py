@@ -627,26 +627,28 @@ def test_plan_hint_one_pass_one_wave_on_twice_the_pairs(hq):
     assert torch.allclose(a.float(), b.float(), atol=2e-3)
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("batch", [5, 63, 64, 65, 300, 5000])
-def test_balanced_ragged_split_charges_sequence_starts(batch):
+def test_balanced_ragged_split_charges_sequence_starts(batch, d):
     # a ragged batch with the plan hint: the balanced schedule charges each sequence start
     # in its range split (pass 1 searches kv_indptr for its range, one to three search
     # steps for these batch sizes, and the merge finds each sequence's ranges with the same
     # formula); empty sequences and ranges that begin in the charge of a sequence start
-    # included. Checked against the oracle and against the equal-page split (no hint)
+    # included; D=64 rows also with grouped kv heads (several per workgroup). Checked
+    # against the oracle and against the equal-page split (no hint)
     rng = np.random.default_rng(batch)
     hi = 60 if batch >= 300 else 3000
     lens = [int(x) for x in rng.integers(0, hi, size=batch)]
     lens[batch // 2] = 0
     lens[-1] = hi * 3                      # one long sequence: the hint shows a ragged mix
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-        batch, lens, 32, 8, 128, device=DEV, page_table="permuted", seed=batch)
+        batch, lens, 32, 8, d, device=DEV, page_table="permuted", seed=batch)
     hint = attention.plan_hint(indptr.cpu())
     rows = list(range(batch)) if batch <= 65 else \
         sorted(set(range(0, batch, max(batch // 40, 1))) | {batch // 2, batch - 1})
     want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
     for wpg in (0, 1, 2, 4):
-        _announce(f"ragged cost split batch={batch} wpg={wpg}")
+        _announce(f"ragged cost split batch={batch} d={d} wpg={wpg}")
         out = decode_attention(q, kv, indptr, ids, last, split_kv=0, waves_per_group=wpg,
                                schedule=1, max_pages_per_seq=hint)
         ref = decode_attention(q, kv, indptr, ids, last, split_kv=0, waves_per_group=wpg,
