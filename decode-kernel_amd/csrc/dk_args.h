@@ -44,7 +44,10 @@ constexpr int kShortSegments = 4;
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5
 // / 7 sequences ended at 323.6 / 331.0 / 336.7 us); the range split charges each sequence
 // start this many pages per wavefront of the workgroup.
-constexpr int kSegmentCostPerWave = 5;
+#ifndef DK_SEGMENT_COST_PER_WAVE
+#define DK_SEGMENT_COST_PER_WAVE 5
+#endif
+constexpr int kSegmentCostPerWave = DK_SEGMENT_COST_PER_WAVE;
 // Balanced schedule over narrow rows: 4 neighbouring kv heads per workgroup, 2 wavefronts
 // each, one such workgroup per CU (64- and 128-byte row segments 512 B or 1 KB apart
 // stream far better when the segments of neighbouring heads are fetched together). B=32
