@@ -268,7 +268,7 @@ int run(Problem p, bool do_merge, void* stream) {
       // a ragged batch (plan hint: the longest sequence well above the mean): charge each
       // change of sequence in the range split, so that ranges crossing more sequences get
       // fewer pages (a kernel build of its own)
-      if (p.need_out && hint > 0 && p.batch > 1 &&
+      if (hint > 0 && p.batch > 1 &&
           hint * (int64_t)p.batch * 4 > p.num_indices * (int64_t)5)
         seg_cost = kSegmentCostPerWave * pl.waves;   // per head's pages (any kv heads per group)
     }
