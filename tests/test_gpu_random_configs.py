@@ -8,7 +8,8 @@ soft-capping or a sliding window; the automatic schedule then picks one pass or 
 balanced schedule, head chunks, grouped kv heads, the small-problem and short-sequence
 wave counts by itself. A few cases use many short sequences, where the plan hint selects
 one wavefront per balanced workgroup. Bar: max-abs 1e-2 and mean-abs 1e-3 against the
-fp32 oracle on the values the kernel reads (the dequantised cache for fp8).
+fp32 oracle on the values the kernel reads (the dequantised cache for fp8), with half an
+ulp of the output's type added to the max-abs bound (short sequences give large outputs).
 """
 
 import os
@@ -60,11 +61,13 @@ def _case(i: int):
     return c
 
 
-# 96 cases by default; DK_RANDOM_CASES=N runs the first N seeds of the same generator
-CASES = [_case(i) for i in range(int(os.environ.get("DK_RANDOM_CASES", "96")))]
+# 96 cases by default; DK_RANDOM_CASES=N runs the first N seeds of the same generator,
+# DK_RANDOM_START=K starts at seed K
+_START = int(os.environ.get("DK_RANDOM_START", "0"))
+CASES = {i: _case(i) for i in range(_START, _START + int(os.environ.get("DK_RANDOM_CASES", "96")))}
 
 
-@pytest.mark.parametrize("i", range(len(CASES)))
+@pytest.mark.parametrize("i", sorted(CASES))
 def test_random_configuration_matches_oracle(i):
     c = CASES[i]
     label = (f"random case {i}: B={c['batch']} {c['hq']}/{c['hkv']}/{c['d']} {c['dtype']} "
@@ -100,7 +103,13 @@ def test_random_configuration_matches_oracle(i):
     torch.cuda.synchronize()
     rows = [b for b, n in enumerate(c["lens"]) if n > 0]
     mx, mean = err_stats(out[rows], want[rows])
-    assert mx <= 1e-2 and mean <= 1e-3, (label, mx, mean)
+    # 1e-2, plus the rounding of the output itself to q's type (half an ulp: 2^-8 |x| for
+    # bf16, 2^-11 |x| for fp16): one- and two-token sequences with large V give outputs of
+    # magnitude ~4-5, where a bf16 output's rounding alone reaches 0.016
+    half_ulp = 2.0 ** -8 if c["dtype"] == torch.bfloat16 else 2.0 ** -11
+    d = np.abs(out[rows].float().cpu().numpy().astype(np.float64) - want[rows])
+    bound = 1e-2 + half_ulp * np.abs(want[rows])
+    assert (d <= bound).all() and mean <= 1e-3, (label, mx, mean)
     # sequences without pages: zeros (the reference's empty-split merge gives 0)
     empty = [b for b, n in enumerate(c["lens"]) if n == 0]
     if empty:
