@@ -12,8 +12,11 @@ Infinity Cache, as the reference flushes L2 before each timed call
 (bench/microbench_cuda.py:75-90,140-157); HIP events on the launch stream bracket the call
 itself. The flush is enqueued without a host sync, so host launch overhead is hidden
 behind it and the events measure GPU time. The W warm-up steps are such flush + call
-steps too, after an untimed settling phase of the same steps (0.3 s) that lets the GPU
-clocks reach their steady state.
+steps too, after an untimed settling phase of the same steps (at least 0.3 s, then until
+three sets of 20 agree within 2 %, at most 2 s) that lets the GPU clocks reach their
+steady state. Between workloads the run hands the previous one's device memory back to
+the driver and waits for the driver's background clearing of it, which otherwise slows
+the next workload's first ~0.1-0.5 s of steps by ~6.5 %.
 
 Modes:
   (default)        one JSON line for the metric workload (or the shape given by --batch,
@@ -68,7 +71,14 @@ METRIC = ("µs/call + achieved HBM TB/s (% peak), decode B=32 ctx=8k Hq32/Hkv8 d
 CONFIG_METRIC = "µs/call + achieved HBM TB/s (% peak), BASELINE config {n}"
 PEAK_GBPS = 8000.0          # MI355X HBM3E
 FLUSH_BYTES = 1 << 30
-SETTLE_S = 0.3              # untimed flush + call steps before the warm-up
+SETTLE_S = 0.3              # untimed flush + call steps before the warm-up, at least
+SETTLE_MAX_S = 2.0          # ... and at most, while consecutive sets still disagree
+SETTLE_AGREE = 1.02         # settled: the last 3 sets' p50s within 2 % of each other
+# Device memory handed back to the driver (torch.cuda.empty_cache) is cleared by it in the
+# background, and meanwhile HBM-bound kernels run ~6.5 % slower (metric shape 168 vs
+# 157.7 us; 2 GiB released -> ~0.08 s of slow steps, 8 GiB -> ~0.25 s, 16 GiB -> ~0.5 s,
+# i.e. ~32 GiB/s). After a release the run waits for that at half the rate.
+RELEASE_WAIT_GIB_S = 16.0
 # Host threads of the CPU baseline: the GPU box gives each GPU a 16-thread CPU share
 # (whatever os.cpu_count() reports there), so at most that many.
 CPU_THREADS_CAP = 16
@@ -303,11 +313,27 @@ class Timer:
         return [e0.elapsed_time(e1) * 1e3 for e0, e1 in evs]     # microseconds
 
     def settle(self, fn):
-        # untimed flush + call steps until the GPU clocks reach their steady state; without
-        # it the first timed steps run slow
+        # untimed flush + call steps until the GPU clocks reach their steady state (without
+        # it the first timed steps run slow): at least SETTLE_S, then until the last three
+        # sets of 20 agree, at most SETTLE_MAX_S
         t0 = time.perf_counter()
-        while time.perf_counter() - t0 < SETTLE_S:
-            self.run(fn, 20)
+        p50s = []
+        while True:
+            p50s.append(statistics.median(self.run(fn, 20)))
+            t = time.perf_counter() - t0
+            last = p50s[-3:]
+            if t >= SETTLE_MAX_S or (t >= SETTLE_S and len(last) == 3
+                                     and max(last) <= SETTLE_AGREE * min(last)):
+                return
+
+
+def release_device_memory(torch):
+    """torch.cuda.empty_cache(), then a wait for the driver's background clearing of the
+    released memory (it slows HBM-bound kernels while it runs)."""
+    before = torch.cuda.memory_reserved()
+    torch.cuda.empty_cache()
+    released = max(before - torch.cuda.memory_reserved(), 0)
+    time.sleep(released / (RELEASE_WAIT_GIB_S * 2**30))
 
 
 # ---------------------------------------------------------------- CPU baseline leg
@@ -495,7 +521,7 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     if metric_workload and not wl.kv8 and not args.single_call and not args.no_extra_configs:
         # the other BASELINE configs, measured in the same run after the metric
         del c, wl
-        torch.cuda.empty_cache()
+        release_device_memory(torch)
         rec["baseline_configs"] = extra_points_run(args, torch, lib, dk_lib, attention,
                                                    layout, dev, stream, host_cpu()[1])
     print(json.dumps(rec), flush=True)
@@ -583,7 +609,7 @@ def extra_points_run(args, torch, lib, dk_lib, attention, layout, dev, stream, t
         out.append(r)
         # each point's buffers come from fresh device allocations, as in a run of its own
         del wl, want
-        torch.cuda.empty_cache()
+        release_device_memory(torch)
     return out
 
 
@@ -591,7 +617,6 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     """BASELINE config N: one JSON line per (shape, split_kv) point of its sweep."""
     ncpu, threads, model = host_cpu()
     timer = Timer(torch, dev, stream, args.flush)
-    settled = False
     for shape in CONFIGS[args.config]:
         splits = shape["splits"]
         wl = config_workload(torch, layout, dev, shape)
@@ -601,6 +626,8 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
         cpu_s, want = None, None
         if not args.no_cpu_baseline:
             cpu_s, want = cpu_baseline_masked(wl, seqs, threads, reps=1)
+        # each shape settles its first split (the CPU oracle above left the GPU idle)
+        settled = False
         for split in splits:
             if not settled:
                 opts, _ = make_opts(dk_lib, args, wl, split)
@@ -634,7 +661,7 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                               f"sequences {seqs}, one run"}
             print(json.dumps(rec), flush=True)
         del wl
-        torch.cuda.empty_cache()
+        release_device_memory(torch)
 
 
 def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
