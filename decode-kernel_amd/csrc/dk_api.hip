@@ -169,6 +169,24 @@ bool one_pass_fits(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   return pairs <= groups && hint <= share;
 }
 
+// A uniform batch (the longest sequence within 1/32 of the mean, by the plan hint) whose
+// (sequence, head chunk) pairs are a whole multiple of kOnePassPairsPerCU per CU: one pass
+// beats the balanced schedule and its merge there, at one wavefront per workgroup (two at
+// exactly that many pairs, i.e. 8 wavefronts per CU). 32/8/128 fp16 unless noted, us,
+// automatic (balanced) vs one pass: pairs 4 per CU, B=128 ctx 2048 / 4096 / 8192: 175.1 vs
+// 170.8, 342.9 vs 331.2, 665.9 vs 651.8; 8 per CU, B=256 ctx 1024 / 2048 / 4096: 179.3 vs
+// 173.2, 340.5 vs 337.8, 661.9 vs 658.1 (bf16 ctx 1024 180.0 vs 173.8, 64/8 190.9 vs
+// 174.4, 16/8 178.9 vs 169.7); 12 per CU (B=384 ctx 1024) 270.5 vs 260.2; 16, 24 and 32
+// per CU (B=512 ctx 1024, 768 and 1024 ctx 512): 355.4 vs 346.3, 295.7 vs 278.3, 397.3 vs
+// 373.4. Other counts stay balanced: 3, 5, 6, 6.25 and 10 per CU measured 1-18 % slower
+// or equal in one pass (B=96 ctx 4096, B=160 and 192 ctx 2048, B=200 and 320 ctx 1024).
+bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
+  const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
+  const int64_t unit = (int64_t)kOnePassPairsPerCU * cus;
+  return unit > 0 && pairs >= unit && pairs % unit == 0 &&
+         hint * p.batch * 32 <= p.num_indices * 33;
+}
+
 // Wavefronts per workgroup of the one-pass kernel that split_kv == 0 runs, or 0 for the
 // balanced schedule. Forced by options.schedule; else only with the max_pages_per_seq
 // hint, when one pass fits (one_pass_fits) at the default wavefronts per workgroup, or, for
@@ -178,8 +196,9 @@ bool one_pass_fits(const Problem& p, const Plan& pl, int cus, int64_t hint) {
 // ctx 4096, us, balanced vs one pass NW=1: 32/8 161.2 vs 160.0, bf16 161.9 vs 160.3, 64/8
 // 177.9 vs 165.3; B=64 ctx 8192 317.4 vs 314.4; slower where the pairs do not fill the
 // CUs evenly, e.g. B=48 127.2 vs 148.1, which the share condition excludes, and over
-// narrow rows, e.g. fp8 96.1 vs 157.7). Pass-1-only calls always take the balanced
-// schedule (they return partials).
+// narrow rows, e.g. fp8 96.1 vs 157.7). With the same rows and wave counts, uniform
+// batches of many pairs run one pass too (uniform_many_pairs). Pass-1-only calls always
+// take the balanced schedule (they return partials).
 int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return 0;
   if (p.opt.schedule == 2) return pl.waves;
@@ -196,6 +215,8 @@ int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
     Plan one = pl;
     one.waves = 1;
     if (one_pass_fits(p, one, cus, hint)) return 1;
+    if (uniform_many_pairs(p, pl, cus, hint))
+      return (int64_t)p.batch * pl.pairs_per_seq == (int64_t)kOnePassPairsPerCU * cus ? 2 : 1;
   }
   return 0;
 }

@@ -39,6 +39,9 @@ constexpr int kSmallUnitsPerCU = 32;
 // us: B=128 ctx 2048 166 vs 174, B=256 ctx 1024 176 vs 185, 64/8 B=256 ctx 1024 188 vs
 // 204, 16/4 93 vs 99; sequences of 1/2 to 1/4 of a range, or ragged, ~1 % either way)
 constexpr int kShortSegments = 4;
+// Uniform batches over 256-byte rows whose (sequence, head chunk) pairs are a whole
+// multiple of this many per CU run one pass (measured in dk_api.hip, uniform_many_pairs)
+constexpr int kOnePassPairsPerCU = 4;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5

@@ -627,6 +627,39 @@ def test_plan_hint_one_pass_one_wave_on_twice_the_pairs(hq):
     assert torch.allclose(a.float(), b.float(), atol=2e-3)
 
 
+@pytest.mark.parametrize("per_cu,ctx,dtype", [(4, 1000, torch.float16),
+                                              (8, 500, torch.bfloat16),
+                                              (12, 300, torch.float16)])
+def test_plan_hint_one_pass_uniform_whole_multiple_of_pairs_per_cu(per_cu, ctx, dtype):
+    # a uniform batch whose (sequence, kv head) pairs are a whole multiple of 4 per CU:
+    # with the hint the automatic schedule is one pass (two wavefronts per workgroup at 4
+    # per CU, one above); 5 per CU, or the same batch made ragged, stays balanced; results
+    # agree with the oracle and with the balanced schedule
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    batch = per_cu * cus // 8
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, ctx, 32, 8, 128, dtype=dtype, device=DEV, page_table="permuted", seed=per_cu)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[dtype]
+    opts = dk_lib.options(max_pages_per_seq=hint)
+    n = ids.shape[0]
+    assert dk_lib.plan_schedule(batch, 32, 8, 128, n, code, 0, opts) == 1
+    b5 = 5 * cus // 8
+    assert dk_lib.plan_schedule(b5, 32, 8, 128, b5 * hint, code, 0, opts) == 0
+    # the longest sequence more than 1/32 above the mean: not uniform
+    assert dk_lib.plan_schedule(batch, 32, 8, 128, n, code, 0,
+                                dk_lib.options(max_pages_per_seq=hint + hint // 16 + 1)) == 0
+    rows = list(range(0, batch, 11)) + [batch - 1]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
+    _announce(f"one pass uniform per_cu={per_cu} batch={batch} ctx={ctx}")
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0, schedule=1)
+    torch.cuda.synchronize()
+    _check(a, want, rows=rows, label=f"one pass, {per_cu} pairs per CU")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
+
+
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("batch", [5, 63, 64, 65, 300, 5000])
 def test_balanced_ragged_split_charges_sequence_starts(batch, d):
