@@ -161,9 +161,11 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *                  shares of pages plus a charge per sequence start; sequences one
  *                  workgroup covers are written directly, the rest merged), or the
  *                  split_kv == 1 pass when options.max_pages_per_seq
- *                  shows that one workgroup per pair fits that grid and is no longer
- *                  (never for kv-head rows of <= 64 bytes, which stream faster with
- *                  grouped kv heads in the balanced schedule).
+ *                  shows that one workgroup per pair fits that grid and is no longer,
+ *                  or (256-byte kv-head rows) that the batch is uniform and its pairs
+ *                  are a whole multiple of 4 per compute unit (never for kv-head rows
+ *                  of <= 64 bytes, which stream faster with grouped kv heads in the
+ *                  balanced schedule).
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
  * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
  * functions behind src/attention.py:50-58. Differences: the caller allocates `out`
