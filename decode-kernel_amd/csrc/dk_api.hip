@@ -180,6 +180,20 @@ bool one_pass_fits(const Problem& p, const Plan& pl, int cus, int64_t hint) {
 // per CU (B=512 ctx 1024, 768 and 1024 ctx 512): 355.4 vs 346.3, 295.7 vs 278.3, 397.3 vs
 // 373.4. Other counts stay balanced: 3, 5, 6, 6.25 and 10 per CU measured 1-18 % slower
 // or equal in one pass (B=96 ctx 4096, B=160 and 192 ctx 2048, B=200 and 320 ctx 1024).
+// A uniform batch of short sequences (at most kShortOnePassPages pages, the longest within
+// 1/32 of the mean) with CUs/4 to CUs (sequence, head chunk) pairs: one pass at 4
+// wavefronts per workgroup, which needs no merge kernel and leaves each wavefront a chain
+// of at most 8 pages. 32/8/128 fp16, us, automatic (balanced + merge) vs one pass at 4 / 2
+// wavefronts per workgroup: B=8 ctx 256 13.4 vs 11.9 / 12.2, ctx 512 14.4 vs 13.9 / 17.5;
+// B=16 ctx 256 14.6 vs 12.3 / 12.6, ctx 512 17.8 vs 14.6 / 17.9; at ctx 1024 the balanced
+// schedule is faster (B=8 17.6 vs 20.5, B=16 22.2 vs 21.9 / 25.6), and so it is with fewer
+// pairs (B=2 ctx 512: 12.8 vs 13.5).
+bool short_uniform_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
+  const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
+  return hint <= kShortOnePassPages && 4 * pairs >= cus && pairs <= cus &&
+         hint * p.batch * 32 <= p.num_indices * 33;
+}
+
 bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   const int64_t unit = (int64_t)kOnePassPairsPerCU * cus;
@@ -197,8 +211,9 @@ bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint)
 // 177.9 vs 165.3; B=64 ctx 8192 317.4 vs 314.4; slower where the pairs do not fill the
 // CUs evenly, e.g. B=48 127.2 vs 148.1, which the share condition excludes, and over
 // narrow rows, e.g. fp8 96.1 vs 157.7). With the same rows and wave counts, uniform
-// batches of many pairs run one pass too (uniform_many_pairs). Pass-1-only calls always
-// take the balanced schedule (they return partials).
+// batches of short sequences (short_uniform_pairs) and of many pairs (uniform_many_pairs)
+// run one pass too. Pass-1-only calls always take the balanced schedule (they return
+// partials).
 int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return 0;
   if (p.opt.schedule == 2) return pl.waves;
@@ -212,6 +227,7 @@ int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
   if (auto_waves && pl.waves == kDefaultWavesPerGroup &&
       waves_per_cu(p, pl) == kDefaultWavesPerCU && p.head_dim == 128 && p.kv_esize() == 2) {
+    if (short_uniform_pairs(p, pl, cus, hint)) return kDefaultWavesPerGroupNarrow;
     Plan one = pl;
     one.waves = 1;
     if (one_pass_fits(p, one, cus, hint)) return 1;

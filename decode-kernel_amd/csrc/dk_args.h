@@ -42,6 +42,9 @@ constexpr int kShortSegments = 4;
 // Uniform batches over 256-byte rows whose (sequence, head chunk) pairs are a whole
 // multiple of this many per CU run one pass (measured in dk_api.hip, uniform_many_pairs)
 constexpr int kOnePassPairsPerCU = 4;
+// ... and uniform batches of sequences of at most this many pages with CUs/4 to CUs pairs
+// run one pass at 4 wavefronts per workgroup (dk_api.hip, short_uniform_pairs)
+constexpr int kShortOnePassPages = 32;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5

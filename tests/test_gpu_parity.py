@@ -627,6 +627,43 @@ def test_plan_hint_one_pass_one_wave_on_twice_the_pairs(hq):
     assert torch.allclose(a.float(), b.float(), atol=2e-3)
 
 
+@pytest.mark.parametrize("batch,ctx,dtype,hq", [(16, 500, torch.float16, 32),
+                                                 (8, 256, torch.bfloat16, 32),
+                                                 (32, 300, torch.float16, 16),
+                                                 (16, 512, torch.float16, 64)])
+def test_plan_hint_one_pass_four_waves_short_uniform(batch, ctx, dtype, hq):
+    # a uniform batch of sequences of at most 32 pages with CUs/4 to CUs (sequence, kv
+    # head) pairs: with the hint the automatic schedule is one pass (4 wavefronts per
+    # workgroup, no merge); longer sequences or fewer pairs stay balanced; results agree
+    # with the oracle and with the balanced schedule (64 q heads: the MFMA q.k path)
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, ctx, hq, 8, 128, dtype=dtype, device=DEV, page_table="permuted", seed=batch)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[dtype]
+    n = ids.shape[0]
+    assert 4 * batch * 8 >= cus and batch * 8 <= cus
+    assert dk_lib.plan_schedule(batch, hq, 8, 128, n, code, 0,
+                                dk_lib.options(max_pages_per_seq=hint)) == 1
+    # sequences of 33 pages or more (fewer pairs than CUs), or a quarter of the pairs:
+    # balanced
+    if batch * 8 < cus:
+        assert dk_lib.plan_schedule(batch, hq, 8, 128, batch * 64, code, 0,
+                                    dk_lib.options(max_pages_per_seq=64)) == 0
+    b2 = max(cus // 64, 1)
+    assert dk_lib.plan_schedule(b2, hq, 8, 128, b2 * 32, code, 0,
+                                dk_lib.options(max_pages_per_seq=32)) == 0
+    rows = list(range(batch))
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
+    _announce(f"one pass four waves short uniform batch={batch} ctx={ctx} hq={hq}")
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0, schedule=1)
+    torch.cuda.synchronize()
+    _check(a, want, rows=rows, label="one pass, four waves")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
+
+
 @pytest.mark.parametrize("per_cu,ctx,dtype", [(4, 1000, torch.float16),
                                               (8, 500, torch.bfloat16),
                                               (12, 300, torch.float16)])
