@@ -194,6 +194,23 @@ bool short_uniform_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint
          hint * p.batch * 32 <= p.num_indices * 33;
 }
 
+// The same over an fp8 cache at D = 128 (128-byte rows), at any pair count from CUs/4 up:
+// one pass, at 4 wavefronts per workgroup below 8 pairs per CU and at one from there
+// (0: not such a batch). 32/8/128, fp16 q, us, automatic (balanced + merge, grouped kv
+// heads) vs one pass at 4 / 1 wavefronts per workgroup: B=8 ctx 256 14.6 vs 11.3 / 16.4,
+// ctx 512 15.5 vs 14.0 / 25.4; B=16 ctx 256 15.7 vs 11.6 / 16.4, ctx 512 17.2 vs 14.2 /
+// 25.6; B=64 ctx 256 22.6 vs 16.1 / 17.5, ctx 512 28.9 vs 22.1 / 27.0; B=128 ctx 256 30.7
+// vs 24.4 / 25.9, ctx 512 37.7 vs 35.4 / 41.5; B=256 ctx 256 45.2 vs 41.9 / 38.5, ctx 512
+// 67.1 vs 62.7 / 65.4; B=512 ctx 256 80.8 vs 75.0 / 61.2, ctx 512 125.5 vs 116.1 / 105.5;
+// B=1024 ctx 256 156.8 vs 140.5 / 121.7. At ctx 1024 the balanced schedule stays faster
+// (B=256 105.8 vs 109.2 / 119.9).
+int short_uniform_fp8_waves(const Problem& p, const Plan& pl, int cus, int64_t hint) {
+  const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
+  if (hint > kShortOnePassPages || 4 * pairs < cus || hint * p.batch * 32 > p.num_indices * 33)
+    return 0;
+  return pairs < 8 * (int64_t)cus ? 4 : 1;
+}
+
 bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   const int64_t unit = (int64_t)kOnePassPairsPerCU * cus;
@@ -212,7 +229,8 @@ bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint)
 // CUs evenly, e.g. B=48 127.2 vs 148.1, which the share condition excludes, and over
 // narrow rows, e.g. fp8 96.1 vs 157.7). With the same rows and wave counts, uniform
 // batches of short sequences (short_uniform_pairs) and of many pairs (uniform_many_pairs)
-// run one pass too. Pass-1-only calls always take the balanced schedule (they return
+// run one pass too, and over an fp8 cache at D = 128 uniform batches of short sequences
+// (short_uniform_fp8_waves). Pass-1-only calls always take the balanced schedule (they return
 // partials).
 int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return 0;
@@ -234,6 +252,10 @@ int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
     if (uniform_many_pairs(p, pl, cus, hint))
       return (int64_t)p.batch * pl.pairs_per_seq == (int64_t)kOnePassPairsPerCU * cus ? 2 : 1;
   }
+  // fp8 cache at D = 128 (128-byte rows), VALU q.k, default wave counts
+  if (auto_waves && p.head_dim == 128 && p.kv_esize() == 1 && !pl.mfma &&
+      pl.waves == kDefaultWavesPerGroupNarrow)
+    return short_uniform_fp8_waves(p, pl, cus, hint);
   return 0;
 }
 

@@ -297,3 +297,39 @@ def test_ragged_fp8_charged_range_split_matches_oracle(batch):
     mx, mean = err_stats(out[rows], want[rows])
     assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
     assert torch.allclose(out.float(), ref_out.float(), atol=2e-3)
+
+
+@pytest.mark.parametrize("batch,ctx", [(8, 500), (64, 256), (512, 200)])
+def test_short_uniform_fp8_one_pass_matches_oracle(batch, ctx):
+    # a uniform batch of sequences of at most 32 pages over an fp8 cache at D=128 with the
+    # plan hint: the automatic schedule is one pass (4 wavefronts per workgroup below 8
+    # pairs per CU, one from there); ctx 1024 stays balanced; checked against the oracle
+    # and against the balanced schedule
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, ctx, 32, 8, 128, device=DEV, page_table="permuted", seed=batch + 7)
+    codes = _quantize(kv, 0.5, 0.25)
+    deq = _dequantize(codes, 0.5, 0.25)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[torch.float16]
+    opts = dk_lib.options(max_pages_per_seq=hint, kv_dtype=dk_lib.DK_KV_FP8_E4M3)
+    if 4 * batch * 8 >= cus:
+        assert dk_lib.plan_schedule(batch, 32, 8, 128, ids.shape[0], code, 0, opts) == 1
+    b256 = cus
+    assert dk_lib.plan_schedule(b256, 32, 8, 128, b256 * 64, code, 0,
+                                dk_lib.options(max_pages_per_seq=64,
+                                               kv_dtype=dk_lib.DK_KV_FP8_E4M3)) == 0
+    rows = list(range(0, batch, max(batch // 40, 1))) + [batch - 1]
+    want = ref.reference_attention_paged(to_np(q).astype(np.float32), deq, to_np(indptr),
+                                         to_np(ids), to_np(last), batch_subset=rows)
+    kv8 = _codes_to_device(codes)
+    _announce(f"fp8 short uniform one pass batch={batch} ctx={ctx}")
+    out = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=0,
+                                     max_pages_per_seq=hint, k_scale=0.5, v_scale=0.25)
+    bal = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=0, schedule=1,
+                                     k_scale=0.5, v_scale=0.25)
+    torch.cuda.synchronize()
+    mx, mean = err_stats(out[rows], want[rows])
+    assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+    assert torch.allclose(out.float(), bal.float(), atol=2e-3)
