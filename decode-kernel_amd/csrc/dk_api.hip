@@ -211,6 +211,20 @@ int short_uniform_fp8_waves(const Problem& p, const Plan& pl, int cus, int64_t h
   return pairs < 8 * (int64_t)cus ? 4 : 1;
 }
 
+// The same at D = 64 (16-bit rows of 128 bytes, fp8 rows of 64): one pass at 4
+// wavefronts per workgroup for CUs/4 to 2 * CUs pairs. 32/8/64, us, automatic (balanced +
+// merge, grouped kv heads where the rows are narrow) vs one pass at 4 / 1 wavefronts per
+// workgroup: fp16 B=16 ctx 256 13.1 vs 10.7 / 14.1, ctx 512 15.0 vs 11.9 / 20.0; B=64 ctx
+// 256 19.0 vs 14.4 / 15.2, ctx 512 23.1 vs 18.5 / 21.8; fp8 B=16 ctx 256 14.2 vs 10.4 /
+// 14.3, ctx 512 15.7 vs 12.3 / 21.3; B=64 ctx 256 20.0 vs 14.4 / 15.2, ctx 512 25.4 vs 19.6
+// / 22.9. At 8 pairs per CU it is mixed (B=256 ctx 256 / 512: fp16 34.9 vs 32.6 / 31.8,
+// 54.9 vs 52.7 / 54.9; fp8 32.8 vs 31.1 / 32.8, 45.3 vs 52.7 / 56.2), so not there.
+bool short_uniform_d64(const Problem& p, const Plan& pl, int cus, int64_t hint) {
+  const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
+  return hint <= kShortOnePassPages && 4 * pairs >= cus && pairs <= 2 * (int64_t)cus &&
+         hint * p.batch * 32 <= p.num_indices * 33;
+}
+
 bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   const int64_t unit = (int64_t)kOnePassPairsPerCU * cus;
@@ -229,20 +243,24 @@ bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint)
 // CUs evenly, e.g. B=48 127.2 vs 148.1, which the share condition excludes, and over
 // narrow rows, e.g. fp8 96.1 vs 157.7). With the same rows and wave counts, uniform
 // batches of short sequences (short_uniform_pairs) and of many pairs (uniform_many_pairs)
-// run one pass too, and over an fp8 cache at D = 128 uniform batches of short sequences
-// (short_uniform_fp8_waves). Pass-1-only calls always take the balanced schedule (they return
+// run one pass too, and over an fp8 cache at D = 128 (short_uniform_fp8_waves) or at
+// D = 64 (short_uniform_d64) uniform batches of short sequences. Pass-1-only calls always take the balanced schedule (they return
 // partials).
 int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return 0;
   if (p.opt.schedule == 2) return pl.waves;
+  const int64_t hint = p.opt.max_pages_per_seq;
+  const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
+  // D = 64 (rows of 128 or 64 bytes), VALU q.k, default wave counts: short uniform batches
+  if (hint > 0 && auto_waves && p.head_dim == 64 && !pl.mfma &&
+      pl.waves == kDefaultWavesPerGroupNarrow && short_uniform_d64(p, pl, cus, hint))
+    return kDefaultWavesPerGroupNarrow;
   // rows of at most 64 bytes: the balanced schedule with grouped kv heads
   if ((int64_t)p.head_dim * p.kv_esize() <= kGroupedAlwaysRowBytes &&
       grouped_kv_heads(p, pl, cus) > 1)
     return 0;
-  const int64_t hint = p.opt.max_pages_per_seq;
   if (hint <= 0) return 0;
   if (one_pass_fits(p, pl, cus, hint)) return pl.waves;
-  const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
   if (auto_waves && pl.waves == kDefaultWavesPerGroup &&
       waves_per_cu(p, pl) == kDefaultWavesPerCU && p.head_dim == 128 && p.kv_esize() == 2) {
     if (short_uniform_pairs(p, pl, cus, hint)) return kDefaultWavesPerGroupNarrow;

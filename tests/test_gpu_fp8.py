@@ -299,25 +299,26 @@ def test_ragged_fp8_charged_range_split_matches_oracle(batch):
     assert torch.allclose(out.float(), ref_out.float(), atol=2e-3)
 
 
-@pytest.mark.parametrize("batch,ctx", [(8, 500), (64, 256), (512, 200)])
-def test_short_uniform_fp8_one_pass_matches_oracle(batch, ctx):
-    # a uniform batch of sequences of at most 32 pages over an fp8 cache at D=128 with the
-    # plan hint: the automatic schedule is one pass (4 wavefronts per workgroup below 8
-    # pairs per CU, one from there); ctx 1024 stays balanced; checked against the oracle
-    # and against the balanced schedule
+@pytest.mark.parametrize("batch,ctx,d", [(8, 500, 128), (64, 256, 128), (512, 200, 128),
+                                         (16, 512, 64), (64, 200, 64)])
+def test_short_uniform_fp8_one_pass_matches_oracle(batch, ctx, d):
+    # a uniform batch of sequences of at most 32 pages over an fp8 cache with the plan
+    # hint: the automatic schedule is one pass (D=128: 4 wavefronts per workgroup below 8
+    # pairs per CU, one from there; D=64: 4, up to 2 pairs per CU); ctx 1024 stays
+    # balanced; checked against the oracle and against the balanced schedule
     import dk_lib
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-        batch, ctx, 32, 8, 128, device=DEV, page_table="permuted", seed=batch + 7)
+        batch, ctx, 32, 8, d, device=DEV, page_table="permuted", seed=batch + 7)
     codes = _quantize(kv, 0.5, 0.25)
     deq = _dequantize(codes, 0.5, 0.25)
     hint = attention.plan_hint(indptr.cpu())
     code = attention._DTYPE_CODE[torch.float16]
     opts = dk_lib.options(max_pages_per_seq=hint, kv_dtype=dk_lib.DK_KV_FP8_E4M3)
-    if 4 * batch * 8 >= cus:
-        assert dk_lib.plan_schedule(batch, 32, 8, 128, ids.shape[0], code, 0, opts) == 1
+    if 4 * batch * 8 >= cus and (d == 128 or batch * 8 <= 2 * cus):
+        assert dk_lib.plan_schedule(batch, 32, 8, d, ids.shape[0], code, 0, opts) == 1
     b256 = cus
-    assert dk_lib.plan_schedule(b256, 32, 8, 128, b256 * 64, code, 0,
+    assert dk_lib.plan_schedule(b256, 32, 8, d, b256 * 64, code, 0,
                                 dk_lib.options(max_pages_per_seq=64,
                                                kv_dtype=dk_lib.DK_KV_FP8_E4M3)) == 0
     rows = list(range(0, batch, max(batch // 40, 1))) + [batch - 1]

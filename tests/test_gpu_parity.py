@@ -664,6 +664,35 @@ def test_plan_hint_one_pass_four_waves_short_uniform(batch, ctx, dtype, hq):
     assert torch.allclose(a.float(), b.float(), atol=2e-3)
 
 
+@pytest.mark.parametrize("batch,ctx,dtype", [(16, 500, torch.float16),
+                                             (64, 256, torch.bfloat16)])
+def test_plan_hint_one_pass_short_uniform_d64(batch, ctx, dtype):
+    # D=64 (128-byte rows): a uniform batch of sequences of at most 32 pages with CUs/4 to
+    # 2 * CUs pairs runs one pass at 4 wavefronts per workgroup instead of the balanced
+    # schedule; four times the pairs stays balanced; checked against the oracle and the
+    # balanced schedule
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, ctx, 32, 8, 64, dtype=dtype, device=DEV, page_table="permuted", seed=batch)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[dtype]
+    if 4 * batch * 8 >= cus and batch * 8 <= 2 * cus:
+        assert dk_lib.plan_schedule(batch, 32, 8, 64, ids.shape[0], code, 0,
+                                    dk_lib.options(max_pages_per_seq=hint)) == 1
+    b8 = cus                                   # 8 pairs per CU
+    assert dk_lib.plan_schedule(b8, 32, 8, 64, b8 * 32, code, 0,
+                                dk_lib.options(max_pages_per_seq=32)) == 0
+    rows = list(range(0, batch, 3)) + [batch - 1]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
+    _announce(f"one pass short uniform D=64 batch={batch} ctx={ctx}")
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0, schedule=1)
+    torch.cuda.synchronize()
+    _check(a, want, rows=rows, label="one pass D=64, four waves")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
+
+
 @pytest.mark.parametrize("per_cu,ctx,dtype", [(4, 1000, torch.float16),
                                               (8, 500, torch.bfloat16),
                                               (12, 300, torch.float16)])
