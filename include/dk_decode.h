@@ -165,7 +165,8 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *                  or (256-byte kv-head rows) that the batch is uniform and its pairs
  *                  are a whole multiple of 4 per compute unit, or that its sequences
  *                  are uniform, at most 32 pages, with CUs/4 to CUs pairs (over an
- *                  fp8 cache at D = 128: CUs/4 pairs or more) (never for kv-head rows
+ *                  fp8 cache at D = 128: CUs/4 pairs or more; at D = 64: CUs/4 to
+ *                  2 * CUs pairs, either cache) (otherwise never for kv-head rows
  *                  of <= 64 bytes, which stream faster with grouped kv heads in the
  *                  balanced schedule).
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
