@@ -19,11 +19,13 @@ An fp8_e4m3 KV cache (SGLang stores it as uint8 and hands out float8_e4m3fn view
 read with the layer's k_scale / v_scale, which the pool also divides by when it writes.
 
 Registration (the reference's entry points, integration/sglang_backend.py:112-137):
-`register_backend()` adds the class under BACKEND_NAME to SGLang's attention-backend table,
-through `register_attention_backend` where SGLang exports it and into the module's
-`_BACKEND_REGISTRY` dict on versions that only have the dict; importing this module with
-SGLANG_ATTENTION_BACKEND=split_kv_hip does it once. SGLang is looked up lazily; without it
-the backend class has a plain base, so the module imports (and is tested) anywhere.
+`register_backend()` adds the class under BACKEND_NAME to SGLang's attention-backend table:
+through `register_attention_backend` where SGLang exports it (its decorator form,
+`register_attention_backend(name)(factory)` with a factory called with the model runner,
+or a `(name, cls)` function), else into the module's `ATTENTION_BACKENDS` or
+`_BACKEND_REGISTRY` dict; importing this module with SGLANG_ATTENTION_BACKEND=split_kv_hip
+does it once. SGLang is looked up lazily; without it the backend class has a plain base,
+so the module imports (and is tested) anywhere.
 """
 from __future__ import annotations
 
@@ -50,10 +52,16 @@ DEFAULT_SPLIT_KV = int(os.environ.get("SPLIT_KV", "0"))
 _log = logging.getLogger(__name__)
 
 # Where SGLang keeps its attention-backend base class and its backend table, newest
-# layout first (the class moved into base_attn_backend in later releases).
+# layout first (the class moved into base_attn_backend, the table into
+# attention_registry, in later releases).
 _SGLANG_BASE_MODULES = ("sglang.srt.layers.attention.base_attn_backend",
                         "sglang.srt.layers.attention")
-_SGLANG_REGISTRY_MODULE = "sglang.srt.layers.attention"
+_SGLANG_REGISTRY_MODULES = ("sglang.srt.layers.attention.attention_registry",
+                            "sglang.srt.layers.attention")
+# backend tables by name, newest first
+_REGISTRY_TABLES = ("ATTENTION_BACKENDS", "_BACKEND_REGISTRY")
+# forward()'s is_prefill when the caller leaves it out (None is a value a caller may pass)
+_UNSET = object()
 
 
 def _optional_module(path: str):
@@ -269,20 +277,23 @@ class SplitKVHipBackend(_backend_base()):
 
     # ---------------------------------------------------------------- reference shim API
     def forward(self, q, kv_data=None, kv_indptr=None, kv_indices=None, kv_last_page_len=None,
-                is_prefill: bool = False, **kwargs):
+                is_prefill=_UNSET, **kwargs):
         """The reference adapter's entry (integration/sglang_backend.py:85-101): page
         tables given by the caller; decode runs the HIP kernel. Called with SGLang's
-        (q, k, v, layer, forward_batch) it dispatches like SGLang's own backends."""
+        (q, k, v, layer, forward_batch[, save_kv_cache]) it dispatches like SGLang's own
+        backends."""
         fb = kwargs.pop("forward_batch", None)
         if fb is None and hasattr(kv_last_page_len, "forward_mode"):
             fb = kv_last_page_len
         if fb is not None:
-            # SGLang's signature: forward(q, k, v, layer, forward_batch, save_kv_cache=True)
+            # SGLang's signature: forward(q, k, v, layer, forward_batch, save_kv_cache=True);
+            # RadixAttention passes save_kv_cache by position, i.e. in is_prefill's slot
             layer = kwargs.pop("layer", kv_indices)
             k = kwargs.pop("k", kv_data)
             v = kwargs.pop("v", kv_indptr)
-            return self.forward_sglang(q, k, v, layer, fb, kwargs.pop("save_kv_cache", True))
-        if is_prefill:
+            save = kwargs.pop("save_kv_cache", True if is_prefill is _UNSET else is_prefill)
+            return self.forward_sglang(q, k, v, layer, fb, bool(save))
+        if is_prefill is not _UNSET and is_prefill:
             raise NotImplementedError(
                 "prefill is not on the decode path; use forward_extend with SGLang's batch")
         return decode_attention(q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
@@ -355,32 +366,65 @@ def _scale(layer, d) -> Optional[float]:
     return float(s)
 
 
+def _registry_module():
+    """The first of SGLang's modules that holds an attention-backend table (a
+    registration hook or a table dict), else the first that imports, else None."""
+    first = None
+    for path in _SGLANG_REGISTRY_MODULES:
+        mod = _optional_module(path)
+        if mod is None:
+            continue
+        first = first or mod
+        if callable(getattr(mod, "register_attention_backend", None)) or any(
+                isinstance(getattr(mod, t, None), dict) for t in _REGISTRY_TABLES):
+            return mod
+    return first
+
+
+def _register_through_hook(hook) -> str:
+    """Call SGLang's register_attention_backend. Its decorator form takes the name and
+    returns a decorator for a factory called with the model runner (the class is such a
+    factory: SplitKVHipBackend(model_runner)); other versions take (name, cls). Returns
+    the form used; raises what the hook raises."""
+    try:
+        deco = hook(BACKEND_NAME)
+    except TypeError:
+        hook(BACKEND_NAME, SplitKVHipBackend)
+        return "register_attention_backend(name, cls)"
+    if not callable(deco):
+        raise TypeError("register_attention_backend(name) returned no decorator")
+    deco(SplitKVHipBackend)
+    return "register_attention_backend(name)(factory)"
+
+
 def register_backend(registry=None) -> bool:
     """Make SplitKVHipBackend selectable under BACKEND_NAME (the reference's
     register_backend, integration/sglang_backend.py:112-137). `registry` is the module
-    holding SGLang's backend table (default: sglang.srt.layers.attention). Uses its
-    `register_attention_backend(name, cls)` when present, else sets the entry of its
+    holding SGLang's backend table (default: sglang.srt.layers.attention.attention_registry,
+    else sglang.srt.layers.attention). Uses its `register_attention_backend` when present
+    (see _register_through_hook), else sets the entry of its `ATTENTION_BACKENDS` or
     `_BACKEND_REGISTRY` dict. Returns whether the backend is now registered; never raises
     for a missing or unfamiliar SGLang (the outcome is logged)."""
     if registry is None:
-        registry = _optional_module(_SGLANG_REGISTRY_MODULE)
+        registry = _registry_module()
     if registry is None:
         _log.warning("%s: SGLang is not importable, so there is no backend table to add "
                      "the decode backend to", BACKEND_NAME)
         return False
     name = getattr(registry, "__name__", type(registry).__name__)
     hook = getattr(registry, "register_attention_backend", None)
-    table = getattr(registry, "_BACKEND_REGISTRY", None)
+    table_name = next((t for t in _REGISTRY_TABLES
+                       if isinstance(getattr(registry, t, None), dict)), None)
     try:
         if callable(hook):
-            hook(BACKEND_NAME, SplitKVHipBackend)
-            how = "register_attention_backend"
-        elif isinstance(table, dict):
-            table[BACKEND_NAME] = SplitKVHipBackend
-            how = "_BACKEND_REGISTRY"
+            how = _register_through_hook(hook)
+        elif table_name is not None:
+            getattr(registry, table_name)[BACKEND_NAME] = SplitKVHipBackend
+            how = table_name
         else:
-            _log.warning("%s: %s has neither register_attention_backend nor a "
-                         "_BACKEND_REGISTRY dict; not registered", BACKEND_NAME, name)
+            _log.warning("%s: %s has neither register_attention_backend nor a backend "
+                         "table (%s); not registered", BACKEND_NAME, name,
+                         " / ".join(_REGISTRY_TABLES))
             return False
     except Exception as exc:  # noqa: BLE001 - SGLang's own checks: log them, do not fail import
         _log.warning("%s: %s refused the backend: %s", BACKEND_NAME, name, exc)

@@ -62,6 +62,60 @@ def test_register_backend_falls_back_to_the_registry_dict():
         SimpleNamespace(__name__="strict", register_attention_backend=refuse)) is False
 
 
+def test_register_backend_through_the_decorator_hook():
+    """SGLang's attention_registry form: register_attention_backend(name) returns a
+    decorator that stores a factory called with the model runner."""
+    from types import SimpleNamespace
+    table = {}
+
+    def register_attention_backend(name):
+        def deco(fn):
+            table[name] = fn
+            return fn
+        return deco
+    mod = SimpleNamespace(__name__="fake_registry", ATTENTION_BACKENDS=table,
+                          register_attention_backend=register_attention_backend)
+    assert sglang_backend.register_backend(mod) is True
+    factory = table["split_kv_hip"]
+    backend = factory(SimpleNamespace(page_size=16))      # how SGLang builds a backend
+    assert isinstance(backend, sglang_backend.SplitKVHipBackend) and backend.page_size == 16
+    # a table without a hook: ATTENTION_BACKENDS before the legacy dict
+    mod = SimpleNamespace(__name__="tables", ATTENTION_BACKENDS={}, _BACKEND_REGISTRY={})
+    assert sglang_backend.register_backend(mod) is True
+    assert "split_kv_hip" in mod.ATTENTION_BACKENDS and mod._BACKEND_REGISTRY == {}
+
+
+@pytest.mark.parametrize("args,kwargs,save", [
+    ((), {}, True),                                  # save_kv_cache left out
+    ((False,), {}, False),                           # RadixAttention: by position
+    ((True,), {}, True),
+    ((), {"save_kv_cache": False}, False),           # by keyword
+])
+def test_sglang_forward_passes_save_kv_cache(monkeypatch, args, kwargs, save):
+    """forward(q, k, v, layer, forward_batch, save_kv_cache) reaches forward_sglang with
+    the caller's save_kv_cache, whether given by position (the reference shim's is_prefill
+    slot) or by keyword."""
+    from types import SimpleNamespace
+    seen = {}
+
+    def record(self, q, k, v, layer, fb, save_kv_cache=True):
+        seen.update(q=q, k=k, v=v, layer=layer, fb=fb, save=save_kv_cache)
+        return "out"
+    monkeypatch.setattr(sglang_backend.SplitKVHipBackend, "forward_sglang", record)
+    fb = SimpleNamespace(forward_mode=object())
+    b = sglang_backend.SplitKVHipBackend()
+    assert b.forward("q", "k", "v", "layer", fb, *args, **kwargs) == "out"
+    assert seen == dict(q="q", k="k", v="v", layer="layer", fb=fb, save=save)
+
+
+def test_reference_shim_prefill_is_refused():
+    b = sglang_backend.SplitKVHipBackend()
+    with pytest.raises(NotImplementedError):
+        b.forward(None, None, None, None, None, True)
+    with pytest.raises(NotImplementedError):
+        b.forward(None, None, None, None, None, is_prefill=True)
+
+
 @pytest.mark.parametrize("runner,ok", [
     (dict(page_size=16), True), (dict(page_size=1), False), (dict(page_size=32), False),
     (dict(server_args=dict(page_size=16)), True), (dict(server_args=dict(page_size=1)), False),
