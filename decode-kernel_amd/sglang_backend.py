@@ -134,8 +134,10 @@ class SplitKVHipBackend(_backend_base()):
             hint = (int(torch.as_tensor(lens_cpu).max()) + PAGE_SIZE - 1) // PAGE_SIZE
         self.forward_metadata = DecodeMetadata(indptr, indices, last, hint)
 
-    def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
+    def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True,
+                       **kwargs):
         """One layer's decode attention; returns (batch, q_heads * head_dim)."""
+        _refuse_extras("forward_decode", kwargs)
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
             self._save(pool, layer, forward_batch.out_cache_loc, k, v)
@@ -180,9 +182,11 @@ class SplitKVHipBackend(_backend_base()):
             self._scales[key] = tuple(vals)
         return self._scales[key]
 
-    def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
+    def forward_extend(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True,
+                       **kwargs):
         """Prefill / extend: causal attention of the new tokens over each request's cached
         prefix and themselves, with PyTorch SDPA per request (outside the decode path)."""
+        _refuse_extras("forward_extend", kwargs)
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
             self._save(pool, layer, forward_batch.out_cache_loc, k, v)
@@ -224,11 +228,12 @@ class SplitKVHipBackend(_backend_base()):
             start += n_new
         return out.view(-1, hq * d)
 
-    def forward_sglang(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True):
+    def forward_sglang(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True,
+                       **kwargs):
         """SGLang's dispatch by forward mode."""
         if forward_batch.forward_mode.is_decode():
-            return self.forward_decode(q, k, v, layer, forward_batch, save_kv_cache)
-        return self.forward_extend(q, k, v, layer, forward_batch, save_kv_cache)
+            return self.forward_decode(q, k, v, layer, forward_batch, save_kv_cache, **kwargs)
+        return self.forward_extend(q, k, v, layer, forward_batch, save_kv_cache, **kwargs)
 
     # ---------------------------------------------------------------- HIP graphs
     # SGLang captures decode steps in graphs (its "CUDA graph" runner; HIP graphs here).
@@ -292,7 +297,7 @@ class SplitKVHipBackend(_backend_base()):
             k = kwargs.pop("k", kv_data)
             v = kwargs.pop("v", kv_indptr)
             save = kwargs.pop("save_kv_cache", True if is_prefill is _UNSET else is_prefill)
-            return self.forward_sglang(q, k, v, layer, fb, bool(save))
+            return self.forward_sglang(q, k, v, layer, fb, bool(save), **kwargs)
         if is_prefill is not _UNSET and is_prefill:
             raise NotImplementedError(
                 "prefill is not on the decode path; use forward_extend with SGLang's batch")
@@ -333,6 +338,15 @@ class SplitKVHipBackend(_backend_base()):
         if ws is None or ws.numel() < need or ws.device != q.device:
             ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
         return ws
+
+
+def _refuse_extras(where: str, kwargs: dict) -> None:
+    """Newer SGLang releases pass optional per-call inputs by keyword (attention sinks,
+    separate rope parts of q and k for MLA, ...). None of them is supported here: a call
+    that sets one is refused rather than attended without it; unset (None) ones pass."""
+    extras = sorted(k for k, v in kwargs.items() if v is not None)
+    if extras:
+        raise NotImplementedError(f"{BACKEND_NAME}.{where}: unsupported inputs {extras}")
 
 
 def _server_page_size(model_runner) -> Optional[int]:

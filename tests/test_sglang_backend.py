@@ -108,6 +108,21 @@ def test_sglang_forward_passes_save_kv_cache(monkeypatch, args, kwargs, save):
     assert seen == dict(q="q", k="k", v="v", layer="layer", fb=fb, save=save)
 
 
+def test_unsupported_sglang_inputs_are_refused():
+    """Keyword inputs of newer SGLang calls (attention sinks, MLA rope parts) are refused
+    when set, before anything is written or launched."""
+    from types import SimpleNamespace
+    b = sglang_backend.SplitKVHipBackend()
+    fb = SimpleNamespace(forward_mode=SimpleNamespace(is_decode=lambda: True))
+    with pytest.raises(NotImplementedError, match="sinks"):
+        b.forward_decode(None, None, None, None, fb, True, sinks=object())
+    with pytest.raises(NotImplementedError, match="q_rope"):
+        b.forward("q", "k", "v", "layer", fb, True, q_rope=object())
+    fb.forward_mode = SimpleNamespace(is_decode=lambda: False)
+    with pytest.raises(NotImplementedError, match="sinks"):
+        b.forward("q", "k", "v", "layer", fb, sinks=object())
+
+
 def test_reference_shim_prefill_is_refused():
     b = sglang_backend.SplitKVHipBackend()
     with pytest.raises(NotImplementedError):
