@@ -7,9 +7,11 @@ explicit), the plan hint (none, or exact), the q.k path, the wave count, and som
 soft-capping or a sliding window; the automatic schedule then picks one pass or the
 balanced schedule, head chunks, grouped kv heads, the small-problem and short-sequence
 wave counts by itself. A few cases use many short sequences, where the plan hint selects
-one wavefront per balanced workgroup. Bar: max-abs 1e-2 and mean-abs 1e-3 against the
-fp32 oracle on the values the kernel reads (the dequantised cache for fp8), with half an
-ulp of the output's type added to the max-abs bound (short sequences give large outputs).
+one wavefront per balanced workgroup, and a few are uniform batches (equal lengths, 64 to
+512 (sequence, kv head) pairs), where it selects the one-pass rules for uniform batches.
+Bar: max-abs 1e-2 and mean-abs 1e-3 against the fp32 oracle on the values the kernel reads
+(the dequantised cache for fp8), with half an ulp of the output's type added to the
+max-abs bound (short sequences give large outputs).
 """
 
 import os
@@ -58,6 +60,16 @@ def _case(i: int):
         seed=i)
     if many_short:   # the automatic schedule with the plan hint: its short-sequence rule
         c.update(split=0, hint=True, waves=0, window=None)
+    if i % 12 == 5:
+        # a uniform batch (every sequence the same length) of 64 to 512 (sequence, kv
+        # head) pairs, automatic schedule with the plan hint: the one-pass rules for
+        # uniform batches of short sequences (16-bit D=128, fp8 D=128, D=64) and the
+        # one-pass-or-balanced choice by pairs per CU
+        hkv = int(r.choice([4, 8]))
+        batch = int(r.choice([8, 16, 32, 64]))
+        n = int(r.choice([16, 100, 256, 500, 512, 1024]))
+        c.update(hkv=hkv, hq=hkv * min(group, 64 // hkv), batch=batch, lens=[n] * batch,
+                 split=0, hint=True, waves=0, window=None, qk_path=0)
     return c
 
 
