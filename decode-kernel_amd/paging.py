@@ -4,7 +4,8 @@
 ReqToTokenPool.req_to_token) into the CSR page table of src/layout.md:27-138 with one
 kernel launch (libdk_decode.so: dk_build_page_table), so a decode step needs no host round
 trip. Tokens are assumed to sit in 16-token pages: token t of a request at slot
-16 * page + t % 16, as a paged allocator with page_size 16 places them.
+16 * page + t % 16, as a paged allocator with page_size 16 places them (or one with a
+page_size that is a multiple of 16: each of its pages is a run of aligned 16-slot pages).
 """
 from __future__ import annotations
 

@@ -7,8 +7,8 @@ Two entry styles are provided:
 * SGLang's backend API — `init_forward_metadata(forward_batch)` once per batch, then
   `forward_decode(q, k, v, layer, forward_batch, save_kv_cache=True)` per layer — reading
   the token pool SGLang owns: per-layer K and V buffers of shape (slots, kv_heads,
-  head_dim) with 16-token pages (server `page_size=16`), the request-to-token map and the
-  batch's sequence lengths. The page table is built on the device once per batch
+  head_dim) with pages of 16 tokens or a multiple of 16 (server `page_size`), the
+  request-to-token map and the batch's sequence lengths. The page table is built on the device once per batch
   (paging.build_page_table) and shared by every layer; the pool is read in place as a
   (k_cache, v_cache) pair of (pages, 16, kv_heads, head_dim) views.
 * The reference shim's `forward(q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
@@ -105,11 +105,16 @@ class SplitKVHipBackend(_backend_base()):
         self._graph_workspace: Optional[torch.Tensor] = None   # captured calls' scratch
         self._retired_graph_workspaces: list = []   # outgrown, still read by old graphs
         self.page_size = _server_page_size(model_runner)
-        if self.page_size not in (None, PAGE_SIZE):
+        # A server page of a multiple of 16 slots holds whole, aligned 16-slot blocks, so
+        # a request's tokens 16p .. 16p+15 sit in slots 16 * id .. 16 * id + 15 with
+        # id = slot(16p) // 16: the kernel's 16-token page. Smaller pages (SGLang's
+        # default, 1) scatter them.
+        if self.page_size is not None and (self.page_size <= 0 or
+                                           self.page_size % PAGE_SIZE != 0):
             raise ValueError(
                 f"{BACKEND_NAME} reads the token pool as 16-token pages (page id = slot // "
-                f"16), so SGLang must run with page_size 16; this server has page_size "
-                f"{self.page_size} (start it with --page-size 16)")
+                f"16), so SGLang must run with a page_size that is a multiple of 16; this "
+                f"server has page_size {self.page_size} (start it with --page-size 16)")
 
     @classmethod
     def name(cls) -> str:

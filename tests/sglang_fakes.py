@@ -1,7 +1,8 @@
 """Minimal stand-ins for the SGLang objects the backend adapter reads (SGLang is not
 installed here): a token pool with per-layer K/V buffers, a request-to-token map filled
-by a 16-token-page allocator, a forward batch and a RadixAttention-like layer. Field
-names follow SGLang's (ForwardBatch, MHATokenToKVPool, ReqToTokenPool, RadixAttention).
+by a paged allocator, a forward batch and a RadixAttention-like layer. Field
+names follow SGLang's (ForwardBatch, MHATokenToKVPool, ReqToTokenPool, RadixAttention);
+the allocator's page size is the server's page_size (16 by default).
 """
 from __future__ import annotations
 
@@ -56,26 +57,28 @@ class TokenPool:
 
 def make_batch(lens, hq=32, hkv=8, d=128, layers=2, dtype=torch.float16, device="cuda",
                seed=0, pool_pages=None, rows=None, decode=True, kv_dtype=None, k_scale=None,
-               v_scale=None):
-    """Requests of `lens` tokens (the decode token included) with pages drawn from a
-    shuffled free list; returns (forward_batch, layer list, pool, req_to_token)."""
+               v_scale=None, server_page=PAGE):
+    """Requests of `lens` tokens (the decode token included) with pages of
+    `server_page` slots (the server's page_size) drawn from a shuffled free list; returns
+    (forward_batch, layer list, pool, req_to_token)."""
     gen = torch.Generator(device="cpu")
     gen.manual_seed(seed)
-    need = sum(math.ceil(n / PAGE) for n in lens)
+    sp = server_page
+    need = sum(math.ceil(n / sp) for n in lens)
     pool_pages = pool_pages or need + 8
     perm = torch.randperm(pool_pages, generator=gen).tolist()
-    max_ctx = max(lens) + PAGE if lens else PAGE
+    max_ctx = max(lens) + sp if lens else sp
     n_rows = rows or len(lens) + 3
     req_to_token = torch.zeros(n_rows, max_ctx, dtype=torch.int32)
     row_ids = torch.randperm(n_rows, generator=gen)[:len(lens)].tolist()
     for r, n in zip(row_ids, lens):
-        for p in range(math.ceil(n / PAGE)):
+        for p in range(math.ceil(n / sp)):
             page = perm.pop()
-            for t in range(p * PAGE, min(n, (p + 1) * PAGE)):
-                req_to_token[r, t] = page * PAGE + t % PAGE
+            for t in range(p * sp, min(n, (p + 1) * sp)):
+                req_to_token[r, t] = page * sp + t % sp
     dgen = torch.Generator(device=device)
     dgen.manual_seed(seed + 1)
-    pool = TokenPool(pool_pages * PAGE, layers, hkv, d, kv_dtype or dtype, device, dgen)
+    pool = TokenPool(pool_pages * sp, layers, hkv, d, kv_dtype or dtype, device, dgen)
     seq_lens = torch.tensor(lens, dtype=torch.int64)
     out_cache_loc = torch.tensor([int(req_to_token[r, n - 1]) for r, n in zip(row_ids, lens)],
                                  dtype=torch.int64)

@@ -132,10 +132,12 @@ def test_reference_shim_prefill_is_refused():
 
 
 @pytest.mark.parametrize("runner,ok", [
-    (dict(page_size=16), True), (dict(page_size=1), False), (dict(page_size=32), False),
+    (dict(page_size=16), True), (dict(page_size=1), False), (dict(page_size=32), True),
+    (dict(page_size=64), True), (dict(page_size=8), False), (dict(page_size=24), False),
+    (dict(page_size=0), False),
     (dict(server_args=dict(page_size=16)), True), (dict(server_args=dict(page_size=1)), False),
     (dict(), True)])
-def test_backend_requires_sixteen_token_pages(runner, ok):
+def test_backend_requires_pages_of_a_multiple_of_sixteen_tokens(runner, ok):
     from types import SimpleNamespace
     if "server_args" in runner:
         runner = dict(server_args=SimpleNamespace(**runner["server_args"]))
@@ -143,7 +145,7 @@ def test_backend_requires_sixteen_token_pages(runner, ok):
     if ok:
         assert sglang_backend.SplitKVHipBackend(mr).split_kv == sglang_backend.DEFAULT_SPLIT_KV
     else:
-        with pytest.raises(ValueError, match="page_size 16"):
+        with pytest.raises(ValueError, match="multiple of 16"):
             sglang_backend.SplitKVHipBackend(mr)
 
 
@@ -173,6 +175,25 @@ def _pool_as_combined(pool, layer_id):
     return np.stack([k, v], axis=1)
 
 
+def _want_by_slots(q, pool, layer_id, r2t, rows, lens):
+    """Attention of each request's q over its tokens gathered slot by slot from the
+    request-to-token map (no page table), in float64: independent of how the pool is
+    paged."""
+    kb = to_np(pool.get_key_buffer(layer_id)).astype(np.float64)
+    vb = to_np(pool.get_value_buffer(layer_id)).astype(np.float64)
+    qn = to_np(q).astype(np.float64)
+    hq, d = qn.shape[1], qn.shape[2]
+    g = hq // kb.shape[1]
+    out = np.zeros_like(qn)
+    for b, (r, n) in enumerate(zip(rows, lens)):
+        slots = np.asarray(r2t[r, :n], dtype=np.int64)
+        for h in range(hq):
+            s_ = kb[slots, h // g] @ qn[b, h] / math.sqrt(d)
+            w = np.exp(s_ - s_.max())
+            out[b, h] = (w / w.sum()) @ vb[slots, h // g]
+    return out
+
+
 def _want(q, pool, layer_id, r2t, rows, lens, scale_mult=1.0):
     indptr, indices, last = ptab.build_page_table(r2t, rows, lens)
     qn = to_np(q) * np.float32(scale_mult)
@@ -181,11 +202,13 @@ def _want(q, pool, layer_id, r2t, rows, lens, scale_mult=1.0):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("lens", [[1, 17, 300, 16, 1000, 33], [2048] * 12, [5]])
-def test_device_page_table_matches_oracle(lens):
-    fb, _, _, r2t = make_batch(lens, layers=1, seed=len(lens))
+@pytest.mark.parametrize("lens,server_page", [
+    ([1, 17, 300, 16, 1000, 33], 16), ([2048] * 12, 16), ([5], 16),
+    ([1, 17, 300, 16, 1000, 33], 32), ([2048, 7, 64] * 3, 64)])
+def test_device_page_table_matches_oracle(lens, server_page):
+    fb, _, _, r2t = make_batch(lens, layers=1, seed=len(lens), server_page=server_page)
     rows = fb.req_pool_indices.tolist()
-    print(f"[case] page table lens={lens[:4]}...", flush=True)
+    print(f"[case] page table lens={lens[:4]}... server page {server_page}", flush=True)
     indptr, indices, last = paging.build_page_table(
         fb.req_to_token_pool.req_to_token, fb.req_pool_indices, fb.seq_lens,
         seq_lens_sum=fb.seq_lens_sum)
@@ -209,18 +232,22 @@ def test_device_page_table_empty_requests_and_capacity_clamp():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("split_kv", [0, 1, 4])
-def test_decode_step_through_the_adapter(dtype, split_kv):
+@pytest.mark.parametrize("dtype,split_kv,server_page", [
+    (dt, s, 16) for dt in (torch.float16, torch.bfloat16) for s in (0, 1, 4)] + [
+    (torch.float16, 0, 32), (torch.bfloat16, 0, 64), (torch.float16, 4, 64)])
+def test_decode_step_through_the_adapter(dtype, split_kv, server_page):
+    """A decode step through SGLang's API; the server's pages hold 16 tokens or a
+    multiple of 16 (each then read as aligned 16-token pages)."""
     lens = [1, 17, 300, 16, 1000, 33, 129]
-    fb, layers, pool, r2t = make_batch(lens, dtype=dtype, seed=3)
+    fb, layers, pool, r2t = make_batch(lens, dtype=dtype, seed=3, server_page=server_page)
     rows = fb.req_pool_indices.tolist()
     backend = sglang_backend.SplitKVHipBackend(split_kv=split_kv)
     backend.init_forward_metadata(fb)
     g = torch.Generator(device=DEV)
     g.manual_seed(5)
     for layer in layers:
-        print(f"[case] adapter {dtype} split={split_kv} layer={layer.layer_id}", flush=True)
+        print(f"[case] adapter {dtype} split={split_kv} server page={server_page} "
+              f"layer={layer.layer_id}", flush=True)
         q = torch.randn(len(lens), 32 * 128, generator=g, device=DEV).to(dtype)
         k = torch.randn(len(lens), 8 * 128, generator=g, device=DEV).to(dtype)
         v = torch.randn(len(lens), 8 * 128, generator=g, device=DEV).to(dtype)
@@ -233,6 +260,11 @@ def test_decode_step_through_the_adapter(dtype, split_kv):
         want = _want(q.view(-1, 32, 128), pool, layer.layer_id, r2t.numpy(), rows, lens)
         mx, mean = err_stats(out.view(-1, 32, 128), want)
         assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+        if server_page != 16 or split_kv == 0:
+            want = _want_by_slots(q.view(-1, 32, 128), pool, layer.layer_id, r2t.numpy(),
+                                  rows, lens)
+            mx, mean = err_stats(out.view(-1, 32, 128), want)
+            assert mx <= 1e-2 and mean <= 1e-3, ("by slots", mx, mean)
 
 
 @pytest.mark.gpu
