@@ -81,6 +81,9 @@ def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     kv = _kv_layout(kv_data)
+    if kv.page_size != PAGE_SIZE:
+        _fail(f"page_size must be 16 for the HIP kernel (decode_attention also takes a "
+              f"multiple of 16), got {kv.page_size}")
     if not q.is_cuda:
         _fail("q must be on CUDA")
     if q.dtype not in _DTYPE_CODE:
@@ -90,8 +93,6 @@ def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
     if kv.dtype != q.dtype and kv.dtype != KV_FP8:
         _fail(f"kv_data dtype {kv.dtype} must match q dtype {q.dtype} (or be "
               f"torch.float8_e4m3fn)")
-    if kv.page_size != PAGE_SIZE:
-        _fail(f"page_size must be 16 for the HIP kernel, got {kv.page_size}")
     if q.shape[2] != kv.d:
         _fail(f"head_dim mismatch: q has {q.shape[2]}, kv_data has {kv.d}")
     if q.shape[2] not in SUPPORTED_HEAD_DIMS:
@@ -288,6 +289,64 @@ def _raw_stream(device) -> int:
         return torch.cuda.current_stream(device).cuda_stream
 
 
+def _page_size_of(kv_data) -> Optional[int]:
+    """Tokens per page of a cache in either form (None if it is neither)."""
+    if isinstance(kv_data, torch.Tensor):
+        return kv_data.shape[2] if kv_data.dim() == 5 else None
+    if isinstance(kv_data, (tuple, list)) and len(kv_data) == 2 and \
+            isinstance(kv_data[0], torch.Tensor) and kv_data[0].dim() == 4:
+        return kv_data[0].shape[1]
+    return None
+
+
+def _sub_page_view(t: torch.Tensor, page_dim: int, page_size: int):
+    """A view of the cache tensor `t` (pages of page_size = 16 s token rows along
+    page_dim, pages along dim 0) as 16-token pages: page p's sub-page j is view page
+    p * mult + j, mult = (page stride) / (16 token rows). The view ends at the last real
+    sub-page. Returns (view, mult)."""
+    row = t.stride(page_dim)
+    step = PAGE_SIZE * row
+    if row <= 0 or t.stride(0) % step != 0:
+        _fail(f"pages of {page_size} tokens are read as 16-token sub-pages, so the page "
+              f"stride ({t.stride(0)}) must be a multiple of 16 token rows ({step})")
+    mult = t.stride(0) // step
+    n = t.shape[0]
+    shape = list(t.shape)
+    shape[0] = (n - 1) * mult + page_size // PAGE_SIZE if n > 0 else 0
+    shape[page_dim] = PAGE_SIZE
+    stride = list(t.stride())
+    stride[0] = step
+    return t.as_strided(shape, stride), mult
+
+
+def _decode_over_sub_pages(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
+                           page_size, kw):
+    """decode_attention over a cache of pages of a multiple of 16 tokens: the same memory
+    viewed as 16-token pages, with the page table rewritten over them on the device
+    (paging.expand_page_table)."""
+    import paging
+    if isinstance(kv_data, torch.Tensor):
+        view, mult = _sub_page_view(kv_data, 2, page_size)
+        num_pages = kv_data.shape[0]
+    else:
+        k, v = kv_data
+        if k.stride() != v.stride() or k.shape != v.shape:
+            _fail("k_cache and v_cache must have the same shape and strides")
+        (kv_k, mult), (kv_v, _) = _sub_page_view(k, 1, page_size), _sub_page_view(v, 1, page_size)
+        view, num_pages = (kv_k, kv_v), k.shape[0]
+    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
+                    ("kv_last_page_len", kv_last_page_len)):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.int32 or t.dim() != 1:
+            _fail(f"{name} must be a 1-D int32 tensor")
+    indptr, indices, last = paging.expand_page_table(
+        _contig1d(kv_indptr), _contig1d(kv_indices), _contig1d(kv_last_page_len), page_size,
+        mult, num_pages)
+    kw = dict(kw)
+    if kw.get("max_pages_per_seq"):
+        kw["max_pages_per_seq"] *= page_size // PAGE_SIZE
+    return decode_attention(q, view, indptr, indices, last, split_kv, **kw)
+
+
 def decode_attention(
     q: torch.Tensor,
     kv_data: torch.Tensor,
@@ -351,9 +410,22 @@ def decode_attention(
     options); later calls with the same signature reuse the validated plan, so a model's
     layers pay only for the pointers and the library call.
 
+    Pages of a multiple of 16 tokens (32, 64, ...; FlashInfer allows any page size, the
+    reference only 16) are read in place as 16-token sub-pages: the page table is
+    rewritten over them on the device first (one more small kernel, no host sync), and an
+    explicit split_kv then partitions sub-pages.
+
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.
     """
+    ps = _page_size_of(kv_data)
+    if ps is not None and ps != PAGE_SIZE and ps > 0 and ps % PAGE_SIZE == 0:
+        return _decode_over_sub_pages(
+            q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, ps,
+            dict(out=out, workspace=workspace, qk_path=qk_path,
+                 waves_per_group=waves_per_group, waves_per_cu=waves_per_cu,
+                 schedule=schedule, max_pages_per_seq=max_pages_per_seq, sm_scale=sm_scale,
+                 k_scale=k_scale, v_scale=v_scale, logit_cap=logit_cap, window=window))
     kvs = _kv_sig(kv_data) if isinstance(q, torch.Tensor) else None
     key = None
     if kvs is not None and all(isinstance(t, torch.Tensor) for t in

@@ -88,6 +88,8 @@ SIGNATURES = {
                                               ctypes.POINTER(DkStrides), _I32,
                                               ctypes.POINTER(DkOptions), _P]),
     "dk_build_page_table": (ctypes.c_int, [_P, _I64, _P, _P, _I32, _I32, _P, _P, _I64, _P, _P]),
+    "dk_expand_page_table": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I64, _I64, _P, _P,
+                                            _I64, _P, _P]),
     "dk_append_kv": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _I32,
                                     _I32, _I32, _I32, _I32, _I32, _I64, _I64, _I32,
                                     ctypes.POINTER(DkStrides), _P]),

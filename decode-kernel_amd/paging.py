@@ -83,6 +83,41 @@ def build_page_table(req_to_token: torch.Tensor, req_pool_indices: torch.Tensor,
     return kv_indptr[:batch + 1], kv_indices[:int(capacity)], kv_last[:batch]
 
 
+def expand_page_table(kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                      kv_last_page_len: torch.Tensor, page_size: int, pages_mult: int,
+                      num_pages: int):
+    """The page table of a cache with pages of page_size = 16 * s tokens, rewritten over
+    its 16-token sub-pages (dk_expand_page_table): sub-page j of page p is id
+    p * pages_mult + j. Returns (kv_indptr (B+1,), kv_indices (len(kv_indices) * s,),
+    kv_last_page_len (B,)) int32 on the same device; entries past the new table's total
+    are left uninitialised. No host synchronisation."""
+    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
+                    ("kv_last_page_len", kv_last_page_len)):
+        if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous():
+            raise DecodeArgumentError(f"{name} must be a contiguous 1-D int32 tensor")
+    if page_size <= 0 or page_size % PAGE_SIZE:
+        raise DecodeArgumentError(f"page_size must be a positive multiple of 16, got {page_size}")
+    dev = kv_indptr.device
+    batch = int(kv_indptr.shape[0]) - 1
+    sub = page_size // PAGE_SIZE
+    capacity = int(kv_indices.shape[0]) * sub
+    out_indptr = torch.empty(batch + 1, dtype=torch.int32, device=dev)
+    out_indices = torch.empty(max(capacity, 1), dtype=torch.int32, device=dev)
+    out_last = torch.empty(max(batch, 0), dtype=torch.int32, device=dev)
+    if batch <= 0:
+        out_indptr.zero_()
+        return out_indptr, out_indices[:0], out_last
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = dk_lib.load().dk_expand_page_table(
+            kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_last_page_len.data_ptr(), batch,
+            int(page_size), int(pages_mult), int(num_pages), int(kv_indices.shape[0]),
+            out_indptr.data_ptr(), out_indices.data_ptr(), capacity, out_last.data_ptr(),
+            stream)
+    dk_lib.check(rc, "expand_page_table")
+    return out_indptr, out_indices[:capacity], out_last
+
+
 def rope_inv_freq(head_dim: int, theta: float = 10000.0, device="cuda") -> torch.Tensor:
     """Plain rotary frequencies theta^(-2i/head_dim), i < head_dim/2, fp32. Frequency
     scalings (Llama 3's, YaRN, ...) produce their own inv_freq and pass it instead."""

@@ -244,6 +244,27 @@ int dk_build_page_table(const int32_t* req_to_token, int64_t req_stride,
                         int32_t* kv_indices, int64_t capacity, int32_t* kv_last_page_len,
                         void* hip_stream);
 
+/* The page table of a cache with pages of page_size = 16 * s tokens (FlashInfer allows any
+ * page size; the reference checks page_size == 16, src/cuda_/attention_ext.cu:508,551)
+ * rewritten over its 16-token sub-pages, so the decode entry points (page_size 16) read
+ * the same cache in place: sub-page j < s of page id p is id p * pages_mult + j, for a
+ * view of the cache whose page stride is that of a sub-page (16 token rows) and
+ * pages_mult = (page stride) / (sub-page stride) (2 * s for the combined
+ * (num_pages, 2, page_size, Hkv, D) cache, s for separate K / V caches). Sequence b's
+ * pages kv_indices[kv_indptr[b] ..) become (pages - 1) * s + ceil(last / 16) sub-pages
+ * (last = kv_last_page_len[b] clamped to [0, page_size]); its last sub-page holds the
+ * last page's remainder (16 when last is 0 or a multiple of 16). Page ids outside
+ * [0, num_pages) become INT32_MAX (past any pool: read as page 0, as the decode kernels
+ * treat bad ids). Writes batch + 1 out_indptr entries, batch out_last_page_len entries (0
+ * for a sequence without pages) and min(total sub-pages, capacity) out_indices; size
+ * out_indices for num_indices * s. Device pointers; enqueued on hip_stream. No
+ * counterpart in the reference. */
+int dk_expand_page_table(const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, int32_t batch, int32_t page_size,
+                         int32_t pages_mult, int64_t num_pages, int64_t num_indices,
+                         int32_t* out_indptr, int32_t* out_indices, int64_t capacity,
+                         int32_t* out_last_page_len, void* hip_stream);
+
 /* Cache write before a decode step: for every sequence b, the new token is the last one
  * the page table describes (page kv_indices[kv_indptr[b+1] - 1], slot
  * kv_last_page_len[b] - 1; grow the table first). Writes its K row rotated by rotary
