@@ -319,12 +319,18 @@ def _sub_page_view(t: torch.Tensor, page_dim: int, page_size: int):
     return t.as_strided(shape, stride), mult
 
 
-def _decode_over_sub_pages(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
-                           page_size, kw):
-    """decode_attention over a cache of pages of a multiple of 16 tokens: the same memory
-    viewed as 16-token pages, with the page table rewritten over them on the device
-    (paging.expand_page_table)."""
+def sixteen_token_pages(kv_data, kv_indptr=None, kv_indices=None, kv_last_page_len=None):
+    """A cache with pages of a multiple of 16 tokens, as decode_attention reads it: the
+    same memory viewed as 16-token pages (no copy) and, when the page table is given, that
+    table rewritten over the 16-token sub-pages on the device (paging.expand_page_table,
+    one small kernel, no host sync). Returns (view, kv_indptr, kv_indices,
+    kv_last_page_len) (the tables None when not given). decode_attention does this on
+    every call with such a cache; a model whose layers share one page table can rewrite
+    it once per step and call decode_attention on each layer's view with that table."""
     import paging
+    page_size = _page_size_of(kv_data)
+    if page_size is None or page_size <= 0 or page_size % PAGE_SIZE:
+        _fail(f"pages must hold a multiple of 16 tokens, got {page_size}")
     if isinstance(kv_data, torch.Tensor):
         view, mult = _sub_page_view(kv_data, 2, page_size)
         num_pages = kv_data.shape[0]
@@ -334,6 +340,8 @@ def _decode_over_sub_pages(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, 
             _fail("k_cache and v_cache must have the same shape and strides")
         (kv_k, mult), (kv_v, _) = _sub_page_view(k, 1, page_size), _sub_page_view(v, 1, page_size)
         view, num_pages = (kv_k, kv_v), k.shape[0]
+    if kv_indptr is None:
+        return view, None, None, None
     for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
                     ("kv_last_page_len", kv_last_page_len)):
         if not isinstance(t, torch.Tensor) or t.dtype != torch.int32 or t.dim() != 1:
@@ -341,6 +349,15 @@ def _decode_over_sub_pages(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, 
     indptr, indices, last = paging.expand_page_table(
         _contig1d(kv_indptr), _contig1d(kv_indices), _contig1d(kv_last_page_len), page_size,
         mult, num_pages)
+    return view, indptr, indices, last
+
+
+def _decode_over_sub_pages(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
+                           page_size, kw):
+    """decode_attention over a cache of pages of a multiple of 16 tokens (see
+    sixteen_token_pages); the plan hint scales to sub-pages."""
+    view, indptr, indices, last = sixteen_token_pages(kv_data, kv_indptr, kv_indices,
+                                                      kv_last_page_len)
     kw = dict(kw)
     if kw.get("max_pages_per_seq"):
         kw["max_pages_per_seq"] *= page_size // PAGE_SIZE
@@ -412,8 +429,9 @@ def decode_attention(
 
     Pages of a multiple of 16 tokens (32, 64, ...; FlashInfer allows any page size, the
     reference only 16) are read in place as 16-token sub-pages: the page table is
-    rewritten over them on the device first (one more small kernel, no host sync), and an
-    explicit split_kv then partitions sub-pages.
+    rewritten over them on the device first (one more small kernel, no host sync; see
+    sixteen_token_pages to do that once for many layers), and an explicit split_kv then
+    partitions sub-pages.
 
     Returns:
         (batch, num_q_heads, head_dim) tensor, same dtype as q.

@@ -233,3 +233,23 @@ def test_decode_over_wide_pages_kv_pair_and_fp8(page_size):
     torch.cuda.synchronize()
     mx, mean = err_stats(out8, want8)
     assert mx <= 1e-2 and mean <= 1e-3, ("fp8", mx, mean)
+
+
+@pytest.mark.gpu
+def test_sixteen_token_pages_once_for_many_layers():
+    """The table rewritten once (sixteen_token_pages) and reused by every layer's call on
+    its own cache view gives what decode_attention gives on the wide pages directly."""
+    lens = [300, 65, 1000]
+    q, kv, indptr, ids, last = _wide_inputs(len(lens), lens, 64, 32, 8, 128, torch.float16,
+                                            seed=11)
+    qd, tabs = q.to(DEV), (indptr.to(DEV), ids.to(DEV), last.to(DEV))
+    layers = [kv.to(DEV), (kv * 0.5).to(DEV)]
+    print("[case] sixteen_token_pages reuse", flush=True)
+    _, e_ptr, e_ids, e_last = attention.sixteen_token_pages(layers[0], *tabs)
+    for layer_kv in layers:
+        view, _, _, _ = attention.sixteen_token_pages(layer_kv)
+        assert view.data_ptr() == layer_kv.data_ptr() and view.shape[2] == 16
+        a = attention.decode_attention(qd, view, e_ptr, e_ids, e_last, split_kv=0)
+        b = attention.decode_attention(qd, layer_kv, *tabs, split_kv=0)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
