@@ -119,6 +119,19 @@ def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
     return kv
 
 
+def _check_sinks(sinks, q) -> None:
+    """Attention sinks: None, or one fp32 logit per q head on q's device (contiguous)."""
+    if sinks is None:
+        return
+    if not isinstance(sinks, torch.Tensor):
+        raise TypeError(f"sinks must be a torch.Tensor, got {type(sinks).__name__}")
+    if sinks.dtype != torch.float32 or sinks.dim() != 1 or sinks.shape[0] != q.shape[1] or \
+            not sinks.is_contiguous() or sinks.device != q.device:
+        _fail(f"sinks must be a contiguous float32 tensor of num_q_heads ({q.shape[1]}) "
+              f"logits on {q.device}; got {tuple(sinks.shape)} {sinks.dtype} on "
+              f"{sinks.device}")
+
+
 def _contig1d(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
@@ -219,12 +232,15 @@ class _CallPlan:
     structs included), the scratch sizes, the entry point."""
 
     __slots__ = ("shape", "ws_need", "split_kv", "pair", "contig", "out_shape", "dtype",
-                 "device", "batch")
+                 "device", "batch", "opts", "sinks")
 
     def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, out,
                  workspace, qk_path, waves_per_group, waves_per_cu, schedule,
-                 max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window):
+                 max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window,
+                 sinks=None):
         kv = _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
+        _check_sinks(sinks, q)
+        self.sinks = None if sinks is None else (sinks.shape, sinks.dtype, sinks.device)
         if sm_scale is not None and (not math.isfinite(sm_scale) or sm_scale <= 0.0):
             _fail(f"sm_scale must be finite and > 0, got {sm_scale}")
         kv_dtype, k_sc, v_sc = _kv_options(kv, k_scale, v_scale)
@@ -253,7 +269,9 @@ class _CallPlan:
         strides.o_b, strides.o_h = (out.stride(0), out.stride(1)) if out is not None else \
             (hq * d, d)
         opts = dk_lib.options(qk_path, waves_per_group, waves_per_cu, schedule,
-                              max_pages_per_seq, sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap, win)
+                              max_pages_per_seq, sm_scale or 0.0, kv_dtype, k_sc, v_sc, cap, win,
+                              0 if sinks is None else sinks.data_ptr())
+        self.opts = opts
         self.shape = (batch, hq, kv.hkv, d, kv.page_size, kv.num_pages, kv_indices.shape[0],
                       _DTYPE_CODE[q.dtype], ctypes.byref(strides), split, ctypes.byref(opts),
                       strides, opts)      # the structs last, kept alive with the plan
@@ -384,6 +402,7 @@ def decode_attention(
     v_scale: Optional[float] = None,
     logit_cap: Optional[float] = None,
     window: Optional[int] = None,
+    sinks: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Decode attention over a paged KV cache (reference src/attention.py:26-58).
 
@@ -422,6 +441,9 @@ def decode_attention(
         window           : sliding window: attend to the last `window` tokens of each
                            sequence (the new one and window - 1 before it; Mistral,
                            Gemma); None or 0 = all tokens
+        sinks            : attention sinks (gpt-oss): (num_q_heads,) float32 logits on the
+                           device; head h's softmax gets one more term e^{sinks[h]} that
+                           takes weight and carries no value; None = off
 
     The argument checks run once per call signature (shapes, strides, dtypes, devices and
     options); later calls with the same signature reuse the validated plan, so a model's
@@ -443,7 +465,8 @@ def decode_attention(
             dict(out=out, workspace=workspace, qk_path=qk_path,
                  waves_per_group=waves_per_group, waves_per_cu=waves_per_cu,
                  schedule=schedule, max_pages_per_seq=max_pages_per_seq, sm_scale=sm_scale,
-                 k_scale=k_scale, v_scale=v_scale, logit_cap=logit_cap, window=window))
+                 k_scale=k_scale, v_scale=v_scale, logit_cap=logit_cap, window=window,
+                 sinks=sinks))
     kvs = _kv_sig(kv_data) if isinstance(q, torch.Tensor) else None
     key = None
     if kvs is not None and all(isinstance(t, torch.Tensor) for t in
@@ -454,12 +477,14 @@ def decode_attention(
                None if workspace is None else (workspace.numel() * workspace.element_size(),
                                                workspace.device),
                split_kv, qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq,
-               sm_scale, k_scale, v_scale, logit_cap, window)
+               sm_scale, k_scale, v_scale, logit_cap, window,
+               None if sinks is None else (sinks.data_ptr(), _tensor_sig(sinks)))
     plan = _PLANS.get(key) if key is not None else None
     if plan is None:
         plan = _CallPlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv, out,
                          workspace, qk_path, waves_per_group, waves_per_cu, schedule,
-                         max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window)
+                         max_pages_per_seq, sm_scale, k_scale, v_scale, logit_cap, window,
+                         sinks)
         if key is not None:
             if len(_PLANS) >= _PLANS_MAX:
                 _PLANS.clear()
@@ -537,11 +562,11 @@ class DecodePlan:
     def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=1, *,
                  out=None, workspace=None, qk_path=0, waves_per_group=0, waves_per_cu=0,
                  schedule=0, max_pages_per_seq=0, sm_scale=None, k_scale=None, v_scale=None,
-                 logit_cap=None, window=None):
+                 logit_cap=None, window=None, sinks=None):
         self._plan = _CallPlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
                                out, workspace, qk_path, waves_per_group, waves_per_cu,
                                schedule, max_pages_per_seq, sm_scale, k_scale, v_scale,
-                               logit_cap, window)
+                               logit_cap, window, sinks)
         self._guard = self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len)
         self._out_strides = None if out is None else out.stride()
         self.workspace_bytes = self._plan.ws_need
@@ -556,7 +581,10 @@ class DecodePlan:
                 kv_last_page_len.shape, kv_last_page_len.stride(), kv_last_page_len.device)
 
     def run(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out=None,
-            workspace=None):
+            workspace=None, sinks=None):
+        """One call with the plan. A plan made with sinks takes each call's sinks (a
+        layer's own; same shape, dtype and device as the planned ones); one made without
+        takes none."""
         if self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) != self._guard:
             _fail("DecodePlan.run: the tensors differ in shape, strides, dtype or device from "
                   "the planned call")
@@ -569,6 +597,15 @@ class DecodePlan:
                   "strides, dtype or device)")
         if workspace is not None and workspace.device != q.device:
             _fail(f"DecodePlan.run: workspace must be on {q.device}, got {workspace.device}")
+        if (sinks is None) != (self._plan.sinks is None):
+            _fail("DecodePlan.run: pass sinks exactly when the plan was made with them")
+        if sinks is not None:
+            if not isinstance(sinks, torch.Tensor) or \
+                    (sinks.shape, sinks.dtype, sinks.device) != self._plan.sinks or \
+                    not sinks.is_contiguous():
+                _fail("DecodePlan.run: sinks differ from the planned ones (shape, dtype, "
+                      "device) or are not contiguous")
+            self._plan.opts.sinks = sinks.data_ptr()
         return _launch(self._plan, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, out,
                        workspace)
 

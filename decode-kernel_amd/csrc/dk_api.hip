@@ -409,6 +409,7 @@ int run(Problem p, bool do_merge, void* stream) {
   a.cap_in = p.opt.logit_cap > 0.f ? score_scale / p.opt.logit_cap : 0.f;
   a.cap_out = p.opt.logit_cap > 0.f ? kLog2e * p.opt.logit_cap : 0.f;
   a.vscale = kv8 && p.opt.v_scale != 0.f ? p.opt.v_scale : 1.f;
+  a.sinks = p.need_out ? p.opt.sinks : nullptr;   // partials (pass 1 alone) stay plain
   // every launch that can store partials has them (or the library is inconsistent)
   if ((pl.balanced || !direct) && (!a.part_o || !a.part_m || !a.part_l))
     return set_error(DK_EWORKSPACE, "internal: partials not assigned for this schedule");
@@ -460,6 +461,7 @@ int run(Problem p, bool do_merge, void* stream) {
     m.hkv = p.hkv;
     m.waves_per_pair = waves_per_pair;
     m.seg_cost = a.seg_cost;
+    m.sinks = a.sinks;
     TraceRange tr("dk_merge %s B=%d Hq=%d D=%d", pl.balanced ? "balanced" : "split",
                   p.batch, p.hq, p.head_dim);
     e = p.dtype == DK_F16 ? launch_merge<F16>(m, p.head_dim, pl.balanced, L.stream)

@@ -197,6 +197,8 @@ int validate(const Problem& p) {
     return set_error(DK_EINVAL, "options.logit_cap must be finite and >= 0 (0 = off)");
   for (int r : o.reserved)
     if (r != 0) return set_error(DK_EINVAL, "options.reserved must be zero");
+  if (((uintptr_t)o.sinks % alignof(float)) != 0)
+    return set_error(DK_EINVAL, "options.sinks must be a 4-byte aligned device array");
   if (p.batch == 0) return DK_OK;   // nothing to do; pointers may be anything
 
   if (!p.q || !p.kv || !p.indptr || !p.last_len)

@@ -118,6 +118,7 @@ struct Pass1Args {
   float vscale;                       // V dequant scale (1 unless the cache is fp8)
   int32_t seg_cost;                   // balanced, COST build: pages a change of sequence is
                                       // charged in the range split
+  const float* sinks;                 // attention sinks: one fp32 logit per q head, or null
 };
 
 struct MergeArgs {
@@ -131,6 +132,7 @@ struct MergeArgs {
   int32_t num_indices, pairs_per_seq, heads, waves_per_pair;
   int32_t group, per, chunks, hkv;    // balanced: q head -> (head chunk, slot row)
   int32_t seg_cost;                   // balanced: pass 1's seg_cost (0: equal page ranges)
+  const float* sinks;                 // attention sinks: one fp32 logit per q head, or null
 };
 
 // ---------------------------------------------------------------- element types
@@ -904,13 +906,21 @@ struct Wave {
     }
   }
 
-  // After reduce_rows: normalised output of the G heads (q head h at out + h * o_h).
-  __device__ __forceinline__ void store_output(uint8_t* out, int64_t o_h) {
+  // After reduce_rows: normalised output of the G heads (q head h at out + h * o_h). With
+  // attention sinks (sink: the group's first q head's logit, else null) the denominator
+  // of head h has one more term, e^{sink[h]}: 2^(sink[h] log2(e) - mref) relative to the
+  // head's reference max (+inf, hence a zero output, when the head saw no token).
+  __device__ __forceinline__ void store_output(uint8_t* out, int64_t o_h,
+                                               const float* sink = nullptr) {
     if constexpr (WIDE) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = 4 * r16 + i;
-        const float L = col_value(lsum[0], i);
+        float L = col_value(lsum[0], i);
+        if (sink) {
+          const float mr = col_value(mref[0], i);
+          if (h < hv) L += __builtin_amdgcn_exp2f(sink[h] * kLog2e - mr);
+        }
         const float inv = L > 0.f ? 1.f / L : 0.f;
         if (h < hv) {
 #pragma unroll
@@ -922,7 +932,11 @@ struct Wave {
       static_for<KR>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         const int h = 4 * k + r16;
-        const float L = row_head_scalar<k>(lsum);
+        float L = row_head_scalar<k>(lsum);
+        if (sink) {
+          const float mr = row_head_scalar<k>(mref);
+          if (h < hv) L += __builtin_amdgcn_exp2f(sink[h] * kLog2e - mr);
+        }
         const float inv = L > 0.f ? 1.f / L : 0.f;
         if (h < hv) {
 #pragma unroll
@@ -1099,17 +1113,19 @@ struct CombineSmem {
 // head (w = this wavefront among them, tid = this thread among their NW * 64) for its G
 // heads, written normalised to out (head h at out + h * o_h) when `direct`, otherwise as a
 // partial with head h at row prow0 + h * phstride. Every wavefront of the workgroup calls
-// it the same number of times (it holds workgroup barriers).
+// it the same number of times (it holds workgroup barriers). qh0: the first q head (for
+// the attention sinks of the normalised output).
 template <class T, int D, int G, int NW, class WV>
 __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 ? NW : 1)>& sm,
                                               const Pass1Args& a, bool direct, uint8_t* out,
                                               int64_t o_h, int64_t prow0, int64_t phstride,
-                                              int w, int tid) {
+                                              int w, int tid, int qh0) {
   constexpr int DPL = WV::DPL, NS = WV::NS, GQ = WV::GQ;
+  const float* sink = a.sinks ? a.sinks + qh0 : nullptr;
   if constexpr (NW == 1) {
     (void)w;
     (void)tid;
-    if (direct) wv.store_output(out, o_h);
+    if (direct) wv.store_output(out, o_h, sink);
     else wv.store_partial(a, prow0, phstride);
   } else {
     if constexpr (WV::WIDE) {
@@ -1158,6 +1174,7 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
         }
       }
       if (direct) {
+        if (sink) L += __builtin_amdgcn_exp2f(sink[h] * kLog2e - mt);   // +inf when empty
         T::store(out + (int64_t)h * o_h + 2 * d, L > 0.f ? O / L : 0.f);
       } else {
         const int64_t row = prow0 + h * phstride;
@@ -1294,7 +1311,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0,
                              a.out + (int64_t)b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
                              ((int64_t)b * a.hq + qh0) * a.split + s, a.split, w,
-                             (int)threadIdx.x);
+                             (int)threadIdx.x, qh0);
 }
 
 // ---------------------------------------------------------------- pass 1, balanced
@@ -1507,7 +1524,7 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     combine_store<T, D, G, NW>(wv, sm, a, a.direct != 0 && nslots == 1,
                                a.out + (int64_t)cur_b * a.o_b + (int64_t)qh0 * a.o_h, a.o_h,
                                ((int64_t)hc * (Wg + a.batch) + j + cur_b) * G, 1, w,
-                               (int)(threadIdx.x & 63) + 64 * w);
+                               (int)(threadIdx.x & 63) + 64 * w, qh0);
     if (!more) break;
   }
 }
@@ -1573,6 +1590,9 @@ __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const flo
   }
   L = wave_sum(L);
   const int b = row / m.hq, qh = row % m.hq;
+  // attention sink of this q head: one more denominator term, e^{sink - M} (+inf, hence a
+  // zero output, when no slot saw a token)
+  if (m.sinks) L += __builtin_amdgcn_exp2f((m.sinks[qh] - M) * kLog2e);
   uint8_t* op = m.out + (int64_t)b * m.o_b + (int64_t)qh * m.o_h + 2 * lane * E;
 #pragma unroll
   for (int e = 0; e < E; ++e) T::store(op + 2 * e, L > 0.f ? acc[e] / L : 0.f);

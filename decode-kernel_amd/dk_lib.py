@@ -19,7 +19,7 @@ DK_F16 = 0
 DK_BF16 = 1
 DK_KV_SAME = 0
 DK_KV_FP8_E4M3 = 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 STATIC_SCRATCH_BYTES = 32 << 20     # DK_STATIC_SCRATCH_BYTES: dk_decode_attention_noalloc
 
 DK_OK = 0
@@ -53,7 +53,8 @@ class DkOptions(ctypes.Structure):
                 ("max_pages_per_seq", ctypes.c_int32), ("sm_scale", ctypes.c_float),
                 ("kv_dtype", ctypes.c_int32), ("k_scale", ctypes.c_float),
                 ("v_scale", ctypes.c_float), ("logit_cap", ctypes.c_float),
-                ("window", ctypes.c_int32), ("reserved", ctypes.c_int32 * 1)]
+                ("window", ctypes.c_int32), ("reserved", ctypes.c_int32 * 1),
+                ("sinks", ctypes.c_void_p)]
 
 
 _P = ctypes.c_void_p
@@ -182,8 +183,10 @@ SCHEDULE_ONE_PASS = 2
 def options(qk_path: int = 0, waves_per_group: int = 0, waves_per_cu: int = 0,
             schedule: int = SCHEDULE_AUTO, max_pages_per_seq: int = 0,
             sm_scale: float = 0.0, kv_dtype: int = DK_KV_SAME, k_scale: float = 0.0,
-            v_scale: float = 0.0, logit_cap: float = 0.0, window: int = 0) -> DkOptions:
+            v_scale: float = 0.0, logit_cap: float = 0.0, window: int = 0,
+            sinks: int = 0) -> DkOptions:
     o = DkOptions()
+    o.sinks = sinks or None       # device address of num_q_heads fp32 sink logits
     o.logit_cap = logit_cap
     o.window = window
     o.sm_scale = sm_scale

@@ -100,6 +100,7 @@ class SplitKVHipBackend(_backend_base()):
         self.forward_metadata: Optional[DecodeMetadata] = None
         self._workspace: Optional[torch.Tensor] = None
         self._scales: dict = {}           # layer_id -> (k_scale, v_scale) of an fp8 pool
+        self._sink_cache: dict = {}       # (layer_id, tensor) -> fp32 attention sinks
         self._graph_tables = None         # persistent page tables for HIP graph replay
         self._graph_max_bs = 0
         self._graph_workspace: Optional[torch.Tensor] = None   # captured calls' scratch
@@ -142,6 +143,7 @@ class SplitKVHipBackend(_backend_base()):
     def forward_decode(self, q, k, v, layer, forward_batch, save_kv_cache: bool = True,
                        **kwargs):
         """One layer's decode attention; returns (batch, q_heads * head_dim)."""
+        sinks = self._sinks(kwargs.pop("sinks", None), layer)
         _refuse_extras("forward_decode", kwargs)
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
@@ -159,7 +161,7 @@ class SplitKVHipBackend(_backend_base()):
             qv, (kc, vc), md.kv_indptr, md.kv_indices, md.kv_last_page_len,
             split_kv=self.split_kv, workspace=self._workspace_for(qv, kc.shape[2]),
             max_pages_per_seq=md.max_pages_per_seq, sm_scale=_scale(layer, d),
-            logit_cap=_logit_cap(layer), window=_window(layer), **scales)
+            logit_cap=_logit_cap(layer), window=_window(layer), sinks=sinks, **scales)
         return out.view(-1, hq * d)
 
     @staticmethod
@@ -170,6 +172,17 @@ class SplitKVHipBackend(_backend_base()):
             pool.set_kv_buffer(layer, loc, k, v)
         else:
             pool.set_kv_buffer(layer, loc, k, v, ks, vs)
+
+    def _sinks(self, sinks, layer):
+        """A layer's attention sinks as decode_attention takes them (contiguous float32,
+        one per q head), converted once per layer and source tensor; None stays None."""
+        if sinks is None:
+            return None
+        key = (getattr(layer, "layer_id", id(layer)), sinks.data_ptr(), sinks.dtype)
+        got = self._sink_cache.get(key)
+        if got is None:
+            got = self._sink_cache[key] = sinks.detach().reshape(-1).to(torch.float32).contiguous()
+        return got
 
     def _kv_scales(self, layer):
         """(k_scale, v_scale) floats of a layer (1.0 when unset), read once per layer:
@@ -191,6 +204,7 @@ class SplitKVHipBackend(_backend_base()):
                        **kwargs):
         """Prefill / extend: causal attention of the new tokens over each request's cached
         prefix and themselves, with PyTorch SDPA per request (outside the decode path)."""
+        sinks = self._sinks(kwargs.pop("sinks", None), layer)
         _refuse_extras("forward_extend", kwargs)
         pool = forward_batch.token_to_kv_pool
         if k is not None and save_kv_cache:
@@ -223,9 +237,19 @@ class SplitKVHipBackend(_backend_base()):
                 mask &= kpos > pos_q - win
             scale = _scale(layer, d) or 1.0 / math.sqrt(d)
             cap = _logit_cap(layer)
-            if cap:      # soft-capped scores: SDPA has no such mode, so attend explicitly
-                s_ = torch.tanh(torch.matmul(qq, kk.transpose(1, 2)) * (scale / cap)) * cap
-                o = torch.matmul(torch.softmax(s_.masked_fill(~mask, float("-inf")), -1), vv)
+            if cap or sinks is not None:
+                # soft-capped scores or attention sinks: SDPA has neither, so attend
+                # explicitly (a sink is one more logit per head, with no value)
+                s_ = torch.matmul(qq, kk.transpose(1, 2)) * scale
+                if cap:
+                    s_ = torch.tanh(s_ / cap) * cap
+                s_ = s_.masked_fill(~mask, float("-inf"))
+                if sinks is not None:
+                    col = sinks.view(hq, 1, 1).expand(hq, s_.shape[1], 1)
+                    p_ = torch.softmax(torch.cat([s_, col], dim=-1), -1)[..., :-1]
+                else:
+                    p_ = torch.softmax(s_, -1)
+                o = torch.matmul(p_, vv)
             else:
                 o = torch.nn.functional.scaled_dot_product_attention(
                     qq, kk, vv, attn_mask=mask, scale=scale)
@@ -346,9 +370,10 @@ class SplitKVHipBackend(_backend_base()):
 
 
 def _refuse_extras(where: str, kwargs: dict) -> None:
-    """Newer SGLang releases pass optional per-call inputs by keyword (attention sinks,
-    separate rope parts of q and k for MLA, ...). None of them is supported here: a call
-    that sets one is refused rather than attended without it; unset (None) ones pass."""
+    """Newer SGLang releases pass optional per-call inputs by keyword (separate rope parts
+    of q and k for MLA, ...); attention sinks are taken before this check. The others are
+    not supported here: a call that sets one is refused rather than attended without it;
+    unset (None) ones pass."""
     extras = sorted(k for k, v in kwargs.items() if v is not None)
     if extras:
         raise NotImplementedError(f"{BACKEND_NAME}.{where}: unsupported inputs {extras}")

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define DK_ABI_VERSION 2
+#define DK_ABI_VERSION 3
 
 /* Element type of q / kv_data / out. The reference is fp16 only
  * (src/cuda_/attention_ext.cu:507,550); bf16 is an extension. */
@@ -105,6 +105,15 @@ typedef struct {
                               whole sequence. split_kv 0 then picks explicit splits of the
                               window's pages. No counterpart in the reference             */
   int32_t reserved[1];     /* must be 0                                                     */
+  const float* sinks;      /* attention sinks (gpt-oss style): NULL = off, else a device
+                              array of num_q_heads fp32 logits; head h's softmax then has
+                              one more term, exp(sinks[h]), that takes weight but has no
+                              value (out = sum_i e^{s_i} v_i / (sum_i e^{s_i} + e^{sinks[h]}),
+                              the scores s_i already scaled and soft-capped). Applied where
+                              the output is normalised (one pass, and the merge of
+                              decode_attention); dk_decode_partials' partials and
+                              dk_merge_partials do not see it. No counterpart in the
+                              reference                                                   */
 } dk_options;
 
 /* ABI version of the loaded library (DK_ABI_VERSION). */

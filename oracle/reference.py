@@ -19,7 +19,8 @@ Pinned by tests/test_oracle.py against: the hand-worked example of
 writeup/cuda_primer.md:31-43,505-540; closed forms (ctx=1, constant V, equal K);
 torch.nn.functional.scaled_dot_product_attention(enable_gqa=True) in float64;
 brute-force float64 golden fixtures (tests/golden/); the soft-capped form against
-transformers' Gemma 2 eager attention (softcap) in float64.
+transformers' Gemma 2 eager attention (softcap) in float64; the attention-sink form
+against transformers' gpt-oss eager attention (sinks) in float64.
 
 Inputs are numpy arrays: q (B, Hq, D) and kv_data (N_p, 2, P, Hkv, D) as float16 /
 float32 (bfloat16 callers pass float32 upcasts — exact), and int32 page tables.
@@ -70,9 +71,11 @@ def gather_paged_to_dense(kv_data, kv_indptr, kv_indices, kv_last_page_len):
 
 
 def _softmax_attend(qs: np.ndarray, k: np.ndarray, v: np.ndarray,
-                    logit_cap=None) -> np.ndarray:
+                    logit_cap=None, sinks=None) -> np.ndarray:
     """qs (Hkv, G, D) already scaled; k, v (S, Hkv, D) -> (Hkv, G, D), fp32 throughout.
-    logit_cap: scores s become cap * tanh(s / cap) before the softmax (an extension)."""
+    logit_cap: scores s become cap * tanh(s / cap) before the softmax (an extension).
+    sinks (Hkv, G): one more logit per q head in the softmax, with no value (an extension,
+    gpt-oss's attention sinks): its weight only enlarges the denominator."""
     if k.shape[0] == 0:
         return np.zeros(qs.shape, np.float32)
     kt = np.ascontiguousarray(k.transpose(1, 2, 0))            # (Hkv, D, S)
@@ -80,19 +83,26 @@ def _softmax_attend(qs: np.ndarray, k: np.ndarray, v: np.ndarray,
     if logit_cap:
         cap = np.float32(logit_cap)
         scores = (cap * np.tanh(scores / cap)).astype(np.float32)
-    scores = scores - scores.max(axis=-1, keepdims=True)
-    w = np.exp(scores, dtype=np.float32)
-    w /= w.sum(axis=-1, keepdims=True, dtype=np.float32)
+    top = scores.max(axis=-1, keepdims=True)
+    if sinks is not None:
+        sk = np.asarray(sinks, np.float32)[..., None]          # (Hkv, G, 1)
+        top = np.maximum(top, sk)
+    w = np.exp(scores - top, dtype=np.float32)
+    den = w.sum(axis=-1, keepdims=True, dtype=np.float32)
+    if sinks is not None:
+        den = den + np.exp(sk - top, dtype=np.float32)
+    w /= den
     return np.matmul(w, np.ascontiguousarray(v.transpose(1, 0, 2)))  # (Hkv, G, D)
 
 
-def reference_attention(Q, K, V, seq_lens=None, sm_scale=None, logit_cap=None) -> np.ndarray:
+def reference_attention(Q, K, V, seq_lens=None, sm_scale=None, logit_cap=None,
+                        sinks=None) -> np.ndarray:
     """fp32 decode attention with GQA (src/reference.py:61-96).
 
     Q (B, Hq, D); K, V (B, S, Hkv, D). With `seq_lens`, sequence b attends over its first
     seq_lens[b] positions only (a length of 0 gives zeros); without, over all S positions
-    (the reference's unmasked form). Returns (B, Hq, D) float32. sm_scale and logit_cap
-    are the extensions of reference_attention_paged.
+    (the reference's unmasked form). Returns (B, Hq, D) float32. sm_scale, logit_cap and
+    sinks are the extensions of reference_attention_paged.
     """
     Q = np.asarray(Q, dtype=np.float32)
     B, Hq, D = Q.shape
@@ -103,22 +113,25 @@ def reference_attention(Q, K, V, seq_lens=None, sm_scale=None, logit_cap=None) -
     for b in range(B):
         n = K.shape[1] if seq_lens is None else int(seq_lens[b])
         qs = (Q[b] * scale).reshape(Hkv, G, D)                 # q head h -> kv head h // G
+        sk = None if sinks is None else np.asarray(sinks, np.float32).reshape(Hkv, G)
         out[b] = _softmax_attend(qs, np.asarray(K[b, :n], np.float32),
-                                 np.asarray(V[b, :n], np.float32), logit_cap).reshape(Hq, D)
+                                 np.asarray(V[b, :n], np.float32), logit_cap,
+                                 sk).reshape(Hq, D)
     return out
 
 
 def reference_attention_paged(Q, kv_data, kv_indptr, kv_indices, kv_last_page_len,
                               literal: bool = False, batch_subset=None, sm_scale=None,
-                              logit_cap=None, window=None) -> np.ndarray:
+                              logit_cap=None, window=None, sinks=None) -> np.ndarray:
     """Paged decode attention (src/reference.py:99-108), per-sequence masked by default.
 
     literal=True gathers to the zero-padded dense form and attends over all positions,
     exactly as the reference does. batch_subset restricts the work to some sequences
     (the other rows of the result are NaN); it is only meaningful with literal=False.
     sm_scale (default 1/sqrt(D), the reference's), logit_cap (scores s -> cap *
-    tanh(s / cap) before the softmax, Gemma 2 style) and window (attend to each
-    sequence's last `window` tokens only) are extensions beyond the reference, for the
+    tanh(s / cap) before the softmax, Gemma 2 style), window (attend to each
+    sequence's last `window` tokens only) and sinks ((Hq,) logits, one more softmax term
+    per q head with no value, gpt-oss style) are extensions beyond the reference, for the
     masked form only.
     """
     Q = np.asarray(Q, dtype=np.float32)
@@ -136,5 +149,6 @@ def reference_attention_paged(Q, kv_data, kv_indptr, kv_indices, kv_last_page_le
         if window:
             k, v = k[-window:], v[-window:]
         qs = (Q[b] * scale).reshape(Hkv, G, D)
-        out[b] = _softmax_attend(qs, k, v, logit_cap).reshape(Hq, D)
+        sk = None if sinks is None else np.asarray(sinks, np.float32).reshape(Hkv, G)
+        out[b] = _softmax_attend(qs, k, v, logit_cap, sk).reshape(Hq, D)
     return out

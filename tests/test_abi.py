@@ -115,6 +115,7 @@ def _call(lib, **kw):
     (dict(opts=dk_lib.options(logit_cap=-1.0)), dk_lib.DK_EINVAL, "logit_cap"),
     # a negative scale would flip the kernels' -inf masking of dead tokens to +inf
     (dict(opts=dk_lib.options(sm_scale=-0.1)), dk_lib.DK_EINVAL, "sm_scale"),
+    (dict(opts=dk_lib.options(sinks=0x1002)), dk_lib.DK_EINVAL, "sinks"),
     (dict(opts=dk_lib.options(sm_scale=float("inf"))), dk_lib.DK_EINVAL, "sm_scale"),
     (dict(opts=dk_lib.options(logit_cap=float("nan"))), dk_lib.DK_EINVAL, "logit_cap"),
     (dict(opts=dk_lib.options(k_scale=2.0)), dk_lib.DK_EINVAL, "fp8 cache only"),
@@ -243,13 +244,14 @@ def test_plan_hint_reads_host_indptr_only():
 def test_options_struct_matches_header():
     # dk_options: qk_path, waves_per_group, waves_per_cu, schedule, max_pages_per_seq
     # (int32), sm_scale (float), kv_dtype (int32), k_scale, v_scale, logit_cap (float),
-    # reserved[2] (int32): 48 bytes
-    assert ctypes.sizeof(dk_lib.DkOptions) == 48
+    # window, reserved[1] (int32), sinks (const float*): 56 bytes
+    assert ctypes.sizeof(dk_lib.DkOptions) == 56
+    assert dk_lib.DkOptions.sinks.offset == 48
     fields = [(f[0], f[1]) for f in dk_lib.DkOptions._fields_]
     hdr = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     body = hdr[hdr.index("int32_t qk_path"):hdr.index("} dk_options;")]
-    declared = re.findall(r"(int32_t|float) (\w+)", body)
-    ctype = {"int32_t": ctypes.c_int32, "float": ctypes.c_float}
+    declared = re.findall(r"(int32_t|float\*|float) (\w+)", body)
+    ctype = {"int32_t": ctypes.c_int32, "float": ctypes.c_float, "float*": ctypes.c_void_p}
     assert [n for _, n in declared] == [n for n, _ in fields]
     for (ty, n), (_, cty) in zip(declared, fields):
         base = cty._type_ if issubclass(cty, ctypes.Array) else cty

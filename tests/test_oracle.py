@@ -557,6 +557,68 @@ def test_planted_softcap_mistake_is_caught_by_transformers():
     np.testing.assert_allclose(good, want[0, 0].numpy(), rtol=2e-5, atol=2e-6)
 
 
+# ---- attention sinks (an extension of the oracle)
+
+@pytest.mark.parametrize("sink_scale,window", [(0.0, None), (1.0, None), (4.0, None),
+                                               (1.0, 20)])
+def test_sinks_match_transformers_gpt_oss(sink_scale, window):
+    """The sink form against transformers' gpt-oss eager attention (its softmax over the
+    scores and one sink logit per q head, sink column dropped), in float64; window: the
+    last `window` tokens, as gpt-oss's sliding layers see them."""
+    from types import SimpleNamespace
+    from transformers.models.gpt_oss.modeling_gpt_oss import eager_attention_forward
+    lens = [1, 16, 37, 60]
+    q, kv, indptr, ids, last = _paged(lens, 8, 2, 64, 16, seed=21, pool=12, dtype=np.float32)
+    q = q * 2
+    rng = np.random.default_rng(5)
+    sinks = (rng.standard_normal(8) * sink_scale).astype(np.float32)
+    got = ref.reference_attention_paged(q, kv, indptr, ids, last, sinks=sinks, window=window)
+    module = SimpleNamespace(num_key_value_groups=4, training=False,
+                             sinks=torch.from_numpy(sinks.astype(np.float64)))
+    for b, n in enumerate(lens):
+        k, v = ref._sequence_kv(kv, indptr, ids, last, b)
+        if window:
+            k, v = k[-window:], v[-window:]
+        qt = torch.from_numpy(q[b].astype(np.float64))[None, :, None, :]      # (1, Hq, 1, D)
+        kt = torch.from_numpy(k.astype(np.float64)).permute(1, 0, 2)[None]   # (1, Hkv, S, D)
+        vt = torch.from_numpy(v.astype(np.float64)).permute(1, 0, 2)[None]
+        want, _ = eager_attention_forward(module, qt, kt, vt, None, scaling=64 ** -0.5)
+        np.testing.assert_allclose(got[b], want[0, 0].numpy(), rtol=2e-5, atol=2e-6)
+
+
+def test_sink_limits_and_planted_mistake():
+    """A sink of -inf changes nothing; a very large one drives the output to zero; adding
+    the sink to the numerator's weights as well (a plausible slip) fails the gpt-oss pin."""
+    from types import SimpleNamespace
+    from transformers.models.gpt_oss.modeling_gpt_oss import eager_attention_forward
+    q, kv, indptr, ids, last = _paged([40, 7], 4, 1, 64, 16, seed=3, dtype=np.float32)
+    plain = ref.reference_attention_paged(q, kv, indptr, ids, last)
+    off = ref.reference_attention_paged(q, kv, indptr, ids, last,
+                                        sinks=np.full(4, -np.inf, np.float32))
+    np.testing.assert_array_equal(off, plain)
+    big = ref.reference_attention_paged(q, kv, indptr, ids, last,
+                                        sinks=np.full(4, 80.0, np.float32))
+    assert np.abs(big).max() < 1e-20
+    sinks = np.array([0.5, -1.0, 2.0, 0.0], np.float32)
+    k, v = ref._sequence_kv(kv, indptr, ids, last, 0)
+    s_ = (q[0].astype(np.float64) * 64 ** -0.5) @ k[:, 0].T.astype(np.float64)   # (Hq, S)
+    top = np.maximum(s_.max(-1, keepdims=True), sinks[:, None])
+    w = np.exp(s_ - top)
+    # the slip: the sink's weight also multiplies a value (here the mean of V)
+    den = w.sum(-1, keepdims=True) + np.exp(sinks[:, None] - top)
+    wrong = (w @ v[:, 0].astype(np.float64) +
+             np.exp(sinks[:, None] - top) * v[:, 0].mean(0)) / den
+    module = SimpleNamespace(num_key_value_groups=4, training=False,
+                             sinks=torch.from_numpy(sinks.astype(np.float64)))
+    qt = torch.from_numpy(q[0].astype(np.float64))[None, :, None, :]
+    kt = torch.from_numpy(k.astype(np.float64)).permute(1, 0, 2)[None]
+    vt = torch.from_numpy(v.astype(np.float64)).permute(1, 0, 2)[None]
+    want, _ = eager_attention_forward(module, qt, kt, vt, None, scaling=64 ** -0.5)
+    assert np.abs(wrong - want[0, 0].numpy()).max() > 1e-3
+    good = ref.reference_attention_paged(q, kv, indptr, ids, last, sinks=sinks)[0]
+    np.testing.assert_allclose(good, want[0, 0].numpy(), rtol=2e-5, atol=2e-6)
+
+
 # ---- sliding window (an extension of the oracle)
 
 def _repage_last(kv, indptr, ids, last, b, window, P=16):

@@ -109,18 +109,18 @@ def test_sglang_forward_passes_save_kv_cache(monkeypatch, args, kwargs, save):
 
 
 def test_unsupported_sglang_inputs_are_refused():
-    """Keyword inputs of newer SGLang calls (attention sinks, MLA rope parts) are refused
-    when set, before anything is written or launched."""
+    """Keyword inputs of newer SGLang calls that the backend does not support (MLA rope
+    parts) are refused when set, before anything is written or launched."""
     from types import SimpleNamespace
     b = sglang_backend.SplitKVHipBackend()
     fb = SimpleNamespace(forward_mode=SimpleNamespace(is_decode=lambda: True))
-    with pytest.raises(NotImplementedError, match="sinks"):
-        b.forward_decode(None, None, None, None, fb, True, sinks=object())
+    with pytest.raises(NotImplementedError, match="k_rope"):
+        b.forward_decode(None, None, None, None, fb, True, k_rope=object(), sinks=None)
     with pytest.raises(NotImplementedError, match="q_rope"):
         b.forward("q", "k", "v", "layer", fb, True, q_rope=object())
     fb.forward_mode = SimpleNamespace(is_decode=lambda: False)
-    with pytest.raises(NotImplementedError, match="sinks"):
-        b.forward("q", "k", "v", "layer", fb, sinks=object())
+    with pytest.raises(NotImplementedError, match="q_rope"):
+        b.forward("q", "k", "v", "layer", fb, q_rope=object())
 
 
 def test_reference_shim_prefill_is_refused():
@@ -492,3 +492,47 @@ def test_hip_graph_capture_and_replay():
         torch.cuda.synchronize()
         assert torch.equal(big, big_keep), "a graph replay wrote into an eager tensor"
         del big_fb, big_layers, big_pool, big, big_keep
+
+
+@pytest.mark.gpu
+def test_sinks_layer_decode_and_extend():
+    """gpt-oss-style attention sinks passed by SGLang's keyword: the decode step (HIP
+    kernel) and the extend path (explicit attention) against the oracle's sink form."""
+    lens = [5, 130, 700]
+    fb, layers, pool, r2t = make_batch(lens, hq=16, hkv=4, d=64, layers=1, seed=8)
+    rows = fb.req_pool_indices.tolist()
+    layer = layers[0]
+    sinks = (torch.randn(16) * 2).to(DEV).to(torch.bfloat16)    # the model's dtype
+    backend = sglang_backend.SplitKVHipBackend()
+    backend.init_forward_metadata(fb)
+    q = torch.randn(len(lens), 16 * 64, device=DEV).half()
+    print("[case] adapter sinks decode", flush=True)
+    out = backend.forward(q, None, None, layer, fb, True, sinks=sinks)
+    torch.cuda.synchronize()
+    indptr, indices, last = ptab.build_page_table(r2t.numpy(), rows, lens)
+    s32 = sinks.float().cpu().numpy()
+    want = ref.reference_attention_paged(to_np(q.view(-1, 16, 64)).astype(np.float32),
+                                         _pool_as_combined(pool, 0), indptr, indices, last,
+                                         sinks=s32)
+    mx, mean = err_stats(out.view(-1, 16, 64), want)
+    assert mx <= 1e-2 and mean <= 1e-3, ("decode", mx, mean)
+    # extend: the last 3 tokens of each request are new; each sees its prefix and itself
+    print("[case] adapter sinks extend", flush=True)
+    ext = [3, 3, 3]
+    fb.forward_mode = type(fb.forward_mode)(False)
+    fb.extend_seq_lens_cpu = ext
+    qe = torch.randn(sum(ext), 16 * 64, device=DEV).half()
+    oe = backend.forward_extend(qe, None, None, layer, fb, sinks=sinks).view(-1, 16, 64)
+    torch.cuda.synchronize()
+    kb, vb = pool.get_key_buffer(0).float().cpu(), pool.get_value_buffer(0).float().cpu()
+    start = 0
+    for r, n, e in zip(rows, lens, ext):
+        for i in range(e):
+            upto = n - e + i + 1                              # tokens this query sees
+            slots = r2t[r, :upto].long()
+            k, v = kb[slots].numpy(), vb[slots].numpy()      # (upto, Hkv, D)
+            qi = to_np(qe[start + i].view(1, 16, 64)).astype(np.float32)
+            w = ref.reference_attention(qi, k[None], v[None], sinks=s32)[0]
+            got = oe[start + i].float().cpu().numpy()
+            assert np.abs(got - w).max() <= 1e-2, (r, i)
+        start += e
