@@ -137,6 +137,13 @@ def parse_args(argv=None):
                          "1/sqrt(head_dim)")
     ap.add_argument("--no-plan-hint", action="store_true",
                     help="do not pass the host-side max_pages_per_seq plan hint")
+    ap.add_argument("--sinks", action="store_true",
+                    help="attention sinks (an extension, gpt-oss): one seeded N(0, 4) logit "
+                         "per q head; the output is checked against the oracle's sink form "
+                         "and no CPU baseline is timed")
+    ap.add_argument("--window", type=int, default=0, metavar="TOKENS",
+                    help="sliding window (an extension): attend to each sequence's last "
+                         "TOKENS tokens; bytes count the pages read; checked like --sinks")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="default run: leave out the BASELINE configs' headline points")
@@ -151,6 +158,10 @@ def parse_args(argv=None):
         ap.error(f"--ragged-min must be in [1, ctx={a.ctx}], got {a.ragged_min}")
     if a.single_call and a.config:
         ap.error("--single-call times the default workload; it does not combine with --config")
+    if a.window < 0:
+        ap.error(f"--window must be >= 0, got {a.window}")
+    if (a.sinks or a.window) and a.config:
+        ap.error("--sinks and --window apply to the default workload, not to --config sweeps")
     return a
 
 
@@ -410,8 +421,11 @@ def max_abs_err(got, want_rows, seqs):
 
 def make_opts(dk_lib, args, wl, split):
     hint = 0 if args.no_plan_hint else _plan_hint(wl)
+    sinks = getattr(wl, "sinks", None)
     return dk_lib.options(args.qk_path, args.waves, args.waves_per_cu, args.schedule, hint,
-                          kv_dtype=dk_lib.DK_KV_FP8_E4M3 if wl.kv8 else dk_lib.DK_KV_SAME), hint
+                          kv_dtype=dk_lib.DK_KV_FP8_E4M3 if wl.kv8 else dk_lib.DK_KV_SAME,
+                          window=getattr(args, "window", 0) or 0,
+                          sinks=0 if sinks is None else sinks.data_ptr()), hint
 
 
 def _plan_hint(wl):
@@ -425,6 +439,18 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                   "freelist" if args.ragged_min else args.page_table, args.ragged_min,
                   q_scale=args.head_dim ** -0.5 if args.ragged_min else 1.0,
                   kv_dtype=args.kv_dtype)
+    extension = bool(args.sinks or args.window)
+    if args.sinks:
+        g = torch.Generator(device="cpu")
+        g.manual_seed(3)
+        wl.sinks = (torch.randn(wl.hq, generator=g) * 2).to(dev)
+    if args.window:
+        # the pages a windowed call reads: those holding each sequence's last `window` tokens
+        w = args.window
+        first = [max(n - w, 0) // 16 * 16 for n in wl.lens]
+        wl.bytes = layout.attention_bytes(wl.batch, [n - f for n, f in zip(wl.lens, first)],
+                                          wl.hq, wl.hkv, wl.d,
+                                          kv_elem_bytes=1 if wl.kv8 else 0)
     split = attention.resolve_split(args.split)
     opts, hint = make_opts(dk_lib, args, wl, split)
     c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
@@ -458,7 +484,7 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     hq, hkv, d = wl.hq, wl.hkv, wl.d
     mfma_qk = args.qk_path == 1 or (args.qk_path == 0 and (hq // hkv > 4 or (wl.kv8 and d >= 256)))
     metric_workload = ((wl.batch, wl.ctx, hq, hkv, d) == (32, 8192, 32, 8, 128)
-                       and wl.table == "permuted" and not wl.ragged_min)
+                       and wl.table == "permuted" and not wl.ragged_min and not extension)
     rec = {
         "metric": METRIC, "value": round(wl.bytes / (p50 * 1e-6) / 1e12, 4), "unit": "TB/s",
         "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -484,7 +510,21 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     }
     if args.single_call:
         rec["mode"] = "single call (no settling, no warm-up)"
-    if not args.no_cpu_baseline:
+    if extension:
+        # the reference has neither: no CPU baseline of its path; the output against the
+        # oracle's masked form with the same options on the first and last sequences
+        rec["config"].update({"sinks": bool(args.sinks), "window": args.window})
+        from oracle.reference import reference_attention_paged
+        seqs = oracle_sequences(wl)
+        sub = _host_subproblem(wl, seqs)
+        qn, kvn, ipn, idn, ln = (t.float().numpy() if t.is_floating_point() else t.numpy()
+                                 for t in sub)
+        want = reference_attention_paged(
+            qn, kvn, ipn, idn, ln, window=args.window or None,
+            sinks=None if not args.sinks else wl.sinks.cpu().numpy())
+        rec["max_abs_err_vs_fp32"] = max_abs_err(c.out, torch.from_numpy(want), seqs)
+        rec["oracle_sequences"] = seqs
+    elif not args.no_cpu_baseline:
         ncpu, threads, model = host_cpu()
         if wl.ragged_min:
             n = min(args.cpu_sample or 8, wl.batch)

@@ -119,6 +119,26 @@ int explicit_split(const Problem& p, int device) {
                       pl.waves);
 }
 
+// Explicit split that split_kv == 0 runs with a sliding window (whose pages bound every
+// sequence): as many splits of the window's pages as fill the device, down to what
+// `ws_bytes` of workspace holds (1: one pass).
+int window_split(const Problem& p, int cus, size_t ws_bytes) {
+  Problem q = p;
+  q.split = 1;
+  const Plan p1 = make_plan(q);
+  const int64_t avg = p.batch > 0 ? p.num_indices / p.batch : 0;
+  const int64_t win_pages = p.opt.window / kPageSize + 2;
+  int s = choose_split((int64_t)p.batch * p1.pairs_per_seq,
+                       (int64_t)cus * resident_groups(p.dtype, p1, p.head_dim),
+                       std::min(avg, win_pages), p1.waves);
+  for (; s > 1; --s) {
+    size_t o, m, l, total;
+    partials_layout_rows(split_rows(p.batch, p.hq, s), p.head_dim, &o, &m, &l, &total);
+    if (total <= ws_bytes) break;
+  }
+  return s;
+}
+
 // Wavefronts per compute unit the balanced schedule keeps resident. Two measured best on
 // MI355X at every decode shape tried with rows of 256 bytes or more (each wavefront keeps
 // two pages of loads in flight), also with 8-16 heads on the MFMA q.k path; four with
@@ -297,20 +317,7 @@ int run(Problem p, bool do_merge, void* stream) {
     const int dev = current_device(-1);
     const int cus = cu_count(dev);
     if (cus <= 0) return hip_fail(hipErrorNoDevice, "compute-unit count");
-    Problem q = p;
-    q.split = 1;
-    const Plan p1 = make_plan(q);
-    const int64_t avg = p.batch > 0 ? p.num_indices / p.batch : 0;
-    const int64_t win_pages = p.opt.window / kPageSize + 2;
-    int s = choose_split((int64_t)p.batch * p1.pairs_per_seq,
-                         (int64_t)cus * resident_groups(p.dtype, p1, p.head_dim),
-                         std::min(avg, win_pages), p1.waves);
-    for (; s > 1; --s) {
-      size_t o, m, l, total;
-      partials_layout_rows(split_rows(p.batch, p.hq, s), p.head_dim, &o, &m, &l, &total);
-      if (total <= p.workspace_bytes) break;
-    }
-    p.split = s;
+    p.split = window_split(p, cus, p.workspace_bytes);
     pl = make_plan(p);
   }
   if (pl.balanced) {
@@ -607,6 +614,9 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, i
   const int dev = dk::current_device(device);
   const int cus = dk::cu_count(dev);
   if (cus <= 0) return dk::hip_fail(hipErrorNoDevice, "dk_plan_schedule");
+  if (p.opt.window > 0)   // explicit splits of the window, in the default workspace
+    return dk::window_split(p, cus, dk::workspace_bytes(batch, num_q_heads, num_kv_heads,
+                                                        head_dim, 0));
   return dk::auto_one_pass(p, dk::make_plan(p), cus) > 0 ? 1 : 0;
 }
 

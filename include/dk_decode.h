@@ -152,8 +152,10 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
 
 /* The schedule that dk_decode_attention_ex runs for these arguments on `device` (-1 =
  * current): 1 = one pass (one workgroup per (sequence, kv head), no merge), 0 = balanced
- * schedule + merge, > 1 = that explicit split + merge. No counterpart in the reference;
- * for callers that size launches or profile the kernels. Returns < 0 on a bad argument. */
+ * schedule + merge, > 1 = that explicit split + merge (with opts->window, the explicit
+ * split of the window's pages that a workspace of dk_workspace_bytes(..., 0) allows). No
+ * counterpart in the reference; for callers that size launches or profile the kernels.
+ * Returns < 0 on a bad argument. */
 int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                      int32_t head_dim, int64_t num_indices, int32_t dtype, int32_t split_kv,
                      const dk_options* opts, int32_t device);

@@ -63,6 +63,16 @@ def test_single_call_does_not_combine_with_a_config_sweep():
     assert r.returncode == 2 and "--single-call" in r.stderr and r.stdout == ""
 
 
+def test_extension_options_are_checked_while_parsing():
+    """--sinks / --window apply to the default workload only, and a window is >= 0."""
+    assert bench.parse_args(["--sinks", "--window", "128"]).window == 128
+    for argv, needle in ((["--sinks", "--config", "2"], "--sinks"),
+                         (["--window", "-3"], "--window")):
+        r = subprocess.run([sys.executable, str(ROOT / "bench.py"), *argv],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 2 and needle in r.stderr and r.stdout == ""
+
+
 def test_host_cpu_reports_count_threads_and_model():
     n, threads, model = bench.host_cpu()
     assert n >= 1 and 1 <= threads <= min(n, bench.CPU_THREADS_CAP) and model

@@ -756,3 +756,22 @@ def test_balanced_ragged_split_charges_sequence_starts(batch, d):
         _check(out, want, rows=rows, label=f"hint wpg={wpg}")
         assert torch.count_nonzero(out[batch // 2]) == 0
         assert torch.allclose(out.float(), ref.float(), atol=2e-3), wpg
+
+
+@pytest.mark.parametrize("batch,window", [(2, 128), (32, 128), (32, 4096), (256, 64)])
+def test_plan_schedule_names_the_window_split_that_runs(batch, window):
+    """With a window, split_kv 0 runs explicit splits of the window's pages: the count
+    dk_plan_schedule reports (for the default workspace) is the one that runs, shown by a
+    bit-identical output from that explicit split_kv."""
+    import dk_lib
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        batch, 2048, 32, 8, 128, device=DEV, page_table="permuted", seed=batch + window)
+    code = attention._DTYPE_CODE[q.dtype]
+    opts = dk_lib.options(window=window)
+    s = dk_lib.plan_schedule(batch, 32, 8, 128, ids.shape[0], code, 0, opts)
+    assert s >= 1
+    _announce(f"plan_schedule window={window} B={batch}: split {s}")
+    auto = decode_attention(q, kv, indptr, ids, last, split_kv=0, window=window)
+    explicit = decode_attention(q, kv, indptr, ids, last, split_kv=s, window=window)
+    torch.cuda.synchronize()
+    assert torch.equal(auto, explicit)
