@@ -141,6 +141,11 @@ def parse_args(argv=None):
                     help="attention sinks (an extension, gpt-oss): one seeded N(0, 4) logit "
                          "per q head; the output is checked against the oracle's sink form "
                          "and no CPU baseline is timed")
+    ap.add_argument("--page-size", type=int, default=16, metavar="TOKENS",
+                    help="pages of TOKENS tokens (a multiple of 16; an extension): times "
+                         "decode_attention, which reads them as 16-token sub-pages after "
+                         "rewriting the page table on the device, checked against the "
+                         "oracle on the original layout; no CPU baseline")
     ap.add_argument("--window", type=int, default=0, metavar="TOKENS",
                     help="sliding window (an extension): attend to each sequence's last "
                          "TOKENS tokens; bytes count the pages read; checked like --sinks")
@@ -162,6 +167,11 @@ def parse_args(argv=None):
         ap.error(f"--window must be >= 0, got {a.window}")
     if (a.sinks or a.window) and a.config:
         ap.error("--sinks and --window apply to the default workload, not to --config sweeps")
+    if a.page_size <= 0 or a.page_size % 16:
+        ap.error(f"--page-size must be a positive multiple of 16, got {a.page_size}")
+    if a.page_size != 16 and (a.config or a.single_call or a.host_overhead or a.ragged_min or
+                              a.sinks or a.window or a.kv_dtype != "same"):
+        ap.error("--page-size times the default uniform workload alone")
     return a
 
 
@@ -750,6 +760,64 @@ def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
                       "host_us_per_call": res}), flush=True)
 
 
+def wide_pages_run(args, torch, attention, dev, stream):
+    """decode_attention over pages of args.page_size tokens (a multiple of 16): the page
+    table is rewritten over 16-token sub-pages on the device inside every timed call. One
+    JSON line; the output against the oracle on the original layout (first and last
+    sequence)."""
+    import numpy as np
+
+    from oracle.reference import reference_attention_paged
+    P, B, ctx = args.page_size, args.batch, args.ctx
+    hq, hkv, d = args.num_q_heads, args.num_kv_heads, args.head_dim
+    dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    npg = -(-ctx // P)
+    kv = torch.randn(B * npg, 2, P, hkv, d, generator=g, device=dev, dtype=dtype)
+    q = torch.randn(B, hq, d, generator=g, device=dev, dtype=dtype)
+    ids = torch.randperm(B * npg, generator=g, device=dev).to(torch.int32)
+    indptr = torch.arange(B + 1, device=dev, dtype=torch.int32) * npg
+    last = torch.full((B,), ctx - (npg - 1) * P, device=dev, dtype=torch.int32)
+    out = torch.empty_like(q)
+    hint = 0 if args.no_plan_hint else npg
+    split = attention.resolve_split(args.split)
+
+    def call():
+        attention.decode_attention(q, kv, indptr, ids, last, split, out=out,
+                                   max_pages_per_seq=hint, qk_path=args.qk_path,
+                                   waves_per_group=args.waves, waves_per_cu=args.waves_per_cu,
+                                   schedule=args.schedule)
+    timer = Timer(torch, dev, stream, args.flush)
+    call()
+    timer.settle(call)
+    timer.run(call, args.warmup)
+    us = sorted(timer.run(call, args.steps))
+    p50 = statistics.median(us)
+    torch.cuda.synchronize()
+    nbytes = B * ctx * hkv * d * 2 * 2 + 2 * B * hq * d * 2
+    seqs = [0, B - 1] if B > 1 else [0]
+    want = []
+    for b in seqs:
+        pages = ids[b * npg:(b + 1) * npg].long()
+        kvb = kv[pages].float().cpu().numpy()
+        want.append(reference_attention_paged(
+            q[b:b + 1].float().cpu().numpy(), kvb, np.array([0, npg], np.int32),
+            np.arange(npg, dtype=np.int32), last[b:b + 1].cpu().numpy())[0])
+    err = float(np.abs(out[seqs].float().cpu().numpy() - np.stack(want)).max())
+    print(json.dumps({
+        "metric": "us/call of decode_attention over pages of a multiple of 16 tokens",
+        "unit": "us", "value": round(p50, 2), "us_per_call_p95": round(percentile(us, 95), 2),
+        "tb_s": round(nbytes / (p50 * 1e-6) / 1e12, 4),
+        "pct_of_peak": round(100 * nbytes / (p50 * 1e-6) / (PEAK_GBPS * 1e9), 2),
+        "config": {"workload": f"paged decode attention B={B} ctx={ctx} Hq={hq} Hkv={hkv} "
+                               f"D={d} {args.dtype} page_size={P} permuted pages",
+                   "split_kv": split, "plan_hint_max_pages": hint,
+                   "path": "Python decode_attention (page table rewritten per call)"},
+        "steps": args.steps, "warmup": args.warmup, "max_abs_err_vs_fp32": err,
+        "oracle_sequences": seqs}), flush=True)
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -771,6 +839,8 @@ def main(argv=None):
         host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
     elif args.config:
         config_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
+    elif args.page_size != 16:
+        wide_pages_run(args, torch, attention, dev, stream)
     else:
         metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
     return 0

@@ -66,8 +66,11 @@ def test_single_call_does_not_combine_with_a_config_sweep():
 def test_extension_options_are_checked_while_parsing():
     """--sinks / --window apply to the default workload only, and a window is >= 0."""
     assert bench.parse_args(["--sinks", "--window", "128"]).window == 128
+    assert bench.parse_args(["--page-size", "64"]).page_size == 64
     for argv, needle in ((["--sinks", "--config", "2"], "--sinks"),
-                         (["--window", "-3"], "--window")):
+                         (["--window", "-3"], "--window"),
+                         (["--page-size", "24"], "--page-size"),
+                         (["--page-size", "32", "--sinks"], "--page-size")):
         r = subprocess.run([sys.executable, str(ROOT / "bench.py"), *argv],
                            capture_output=True, text=True, timeout=120)
         assert r.returncode == 2 and needle in r.stderr and r.stdout == ""
