@@ -156,6 +156,9 @@ extern "C" int dk_expand_page_table(const int32_t* kv_indptr, const int32_t* kv_
                          "different pages would share ids", pages_mult, sub);
   if (num_indices > INT32_MAX)
     return dk::set_error(DK_EINVAL, "num_indices must be < 2^31");
+  // the rewritten table's offsets (at most num_indices * sub entries) are int32
+  if (num_indices * (int64_t)sub > (int64_t)INT32_MAX)
+    return dk::set_error(DK_EINVAL, "num_indices * page_size / 16 sub-pages exceed 2^31");
   // every valid sub-page id, (num_pages - 1) * pages_mult + sub - 1, must fit in int32
   if (num_pages > 0 && (num_pages - 1) * (int64_t)pages_mult + sub > (int64_t)INT32_MAX)
     return dk::set_error(DK_EINVAL, "num_pages * pages_mult exceeds 2^31 sub-page ids");

@@ -113,6 +113,7 @@ def test_expansion_of_separate_caches_uses_their_page_stride():
     (dict(batch=-1), "negative"),
     (dict(capacity=-1), "negative"),
     (dict(num_pages=2**30, pages_mult=4), "2^31"),
+    (dict(num_indices=2**30, page_size=64, pages_mult=8), "sub-pages exceed"),
 ])
 def test_expand_rejects_bad_arguments_before_launch(kw, needle):
     lib = dk_lib.load()
