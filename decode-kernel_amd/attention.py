@@ -556,13 +556,22 @@ class DecodePlan:
     device would be addressed as if it were on the planned one). `out` may be None (a
     contiguous one is allocated; then the plan must have been made without one) and
     `workspace` must hold at least the planned bytes (the library checks its size on every
-    call). Keyword options are those of decode_attention.
+    call). Keyword options are those of decode_attention. A cache of pages of a multiple
+    of 16 tokens is planned over its 16-token view; each run rewrites its page table.
     """
 
     def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=1, *,
                  out=None, workspace=None, qk_path=0, waves_per_group=0, waves_per_cu=0,
                  schedule=0, max_pages_per_seq=0, sm_scale=None, k_scale=None, v_scale=None,
                  logit_cap=None, window=None, sinks=None):
+        # pages of a multiple of 16 tokens: planned (and run) over the 16-token view, with
+        # the page table rewritten on the device by every run (sixteen_token_pages)
+        ps = _page_size_of(kv_data)
+        self._wide = ps is not None and ps != PAGE_SIZE and ps > 0 and ps % PAGE_SIZE == 0
+        if self._wide:
+            kv_data, kv_indptr, kv_indices, kv_last_page_len = sixteen_token_pages(
+                kv_data, kv_indptr, kv_indices, kv_last_page_len)
+            max_pages_per_seq *= ps // PAGE_SIZE
         self._plan = _CallPlan(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
                                out, workspace, qk_path, waves_per_group, waves_per_cu,
                                schedule, max_pages_per_seq, sm_scale, k_scale, v_scale,
@@ -585,6 +594,9 @@ class DecodePlan:
         """One call with the plan. A plan made with sinks takes each call's sinks (a
         layer's own; same shape, dtype and device as the planned ones); one made without
         takes none."""
+        if getattr(self, "_wide", False):
+            kv_data, kv_indptr, kv_indices, kv_last_page_len = sixteen_token_pages(
+                kv_data, kv_indptr, kv_indices, kv_last_page_len)
         if self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) != self._guard:
             _fail("DecodePlan.run: the tensors differ in shape, strides, dtype or device from "
                   "the planned call")

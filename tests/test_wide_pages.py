@@ -254,3 +254,23 @@ def test_sixteen_token_pages_once_for_many_layers():
         b = attention.decode_attention(qd, layer_kv, *tabs, split_kv=0)
         torch.cuda.synchronize()
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_decode_plan_over_wide_pages():
+    """DecodePlan over 64-token pages (planned over the 16-token view, the table rewritten
+    by each run) gives decode_attention's output, layer after layer."""
+    lens = [300, 65, 1000, 16]
+    q, kv, indptr, ids, last = _wide_inputs(len(lens), lens, 64, 32, 8, 128, torch.bfloat16,
+                                            seed=13)
+    qd, tabs = q.to(DEV), (indptr.to(DEV), ids.to(DEV), last.to(DEV))
+    layers = [kv.to(DEV), (kv * 0.5).to(DEV)]
+    hint = int((indptr[1:] - indptr[:-1]).max())
+    print("[case] DecodePlan over 64-token pages", flush=True)
+    plan = attention.DecodePlan(qd, layers[0], *tabs, split_kv=0, max_pages_per_seq=hint)
+    for layer_kv in layers:
+        got = plan.run(qd, layer_kv, *tabs)
+        want = attention.decode_attention(qd, layer_kv, *tabs, split_kv=0,
+                                          max_pages_per_seq=hint)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
