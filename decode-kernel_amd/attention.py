@@ -72,16 +72,20 @@ def _kv_layout(kv_data):
                            d_stride=kv_data.stride(4))
 
 
-def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len):
+def _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, wide_pages=False):
     """Host-side checks: the reference's TORCH_CHECKs (attention_ext.cu:506-509,549-552)
     plus the layout invariants that need no device read (src/layout.md:171-178).
-    Returns the cache layout."""
+    wide_pages: pages of any multiple of 16 tokens pass (the checks that run before such a
+    table is rewritten over 16-token sub-pages on the device). Returns the cache layout."""
     for name, t in (("q", q), ("kv_indptr", kv_indptr),
                     ("kv_indices", kv_indices), ("kv_last_page_len", kv_last_page_len)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     kv = _kv_layout(kv_data)
-    if kv.page_size != PAGE_SIZE:
+    if wide_pages:
+        if kv.page_size <= 0 or kv.page_size % PAGE_SIZE:
+            _fail(f"pages must hold a multiple of 16 tokens, got {kv.page_size}")
+    elif kv.page_size != PAGE_SIZE:
         _fail(f"page_size must be 16 for the HIP kernel (decode_attention also takes a "
               f"multiple of 16), got {kv.page_size}")
     if not q.is_cuda:
@@ -360,10 +364,13 @@ def sixteen_token_pages(kv_data, kv_indptr=None, kv_indices=None, kv_last_page_l
         view, num_pages = (kv_k, kv_v), k.shape[0]
     if kv_indptr is None:
         return view, None, None, None
+    cache_dev = kv_data.device if isinstance(kv_data, torch.Tensor) else kv_data[0].device
     for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
                     ("kv_last_page_len", kv_last_page_len)):
         if not isinstance(t, torch.Tensor) or t.dtype != torch.int32 or t.dim() != 1:
             _fail(f"{name} must be a 1-D int32 tensor")
+        if t.device != cache_dev:
+            _fail(f"{name} must be on the cache's device {cache_dev}, got {t.device}")
     indptr, indices, last = paging.expand_page_table(
         _contig1d(kv_indptr), _contig1d(kv_indices), _contig1d(kv_last_page_len), page_size,
         mult, num_pages)
@@ -373,7 +380,9 @@ def sixteen_token_pages(kv_data, kv_indptr=None, kv_indices=None, kv_last_page_l
 def _decode_over_sub_pages(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv,
                            page_size, kw):
     """decode_attention over a cache of pages of a multiple of 16 tokens (see
-    sixteen_token_pages); the plan hint scales to sub-pages."""
+    sixteen_token_pages); the plan hint scales to sub-pages. The arguments pass the host
+    checks before the expansion kernel reads the tables."""
+    _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, wide_pages=True)
     view, indptr, indices, last = sixteen_token_pages(kv_data, kv_indptr, kv_indices,
                                                       kv_last_page_len)
     kw = dict(kw)
@@ -469,8 +478,12 @@ def decode_attention(
                  sinks=sinks))
     kvs = _kv_sig(kv_data) if isinstance(q, torch.Tensor) else None
     key = None
-    if kvs is not None and all(isinstance(t, torch.Tensor) for t in
-                               (kv_indptr, kv_indices, kv_last_page_len)):
+    # scalar options given as tensors are read on every call (a cached plan would keep the
+    # value they had when it was made)
+    scalars_plain = not any(isinstance(x, torch.Tensor)
+                            for x in (sm_scale, k_scale, v_scale, logit_cap, window))
+    if kvs is not None and scalars_plain and all(isinstance(t, torch.Tensor) for t in
+                                                 (kv_indptr, kv_indices, kv_last_page_len)):
         key = (_tensor_sig(q), kvs, _tensor_sig(kv_indptr), _tensor_sig(kv_indices),
                _tensor_sig(kv_last_page_len),
                None if out is None else _tensor_sig(out),
@@ -556,8 +569,18 @@ class DecodePlan:
     device would be addressed as if it were on the planned one). `out` may be None (a
     contiguous one is allocated; then the plan must have been made without one) and
     `workspace` must hold at least the planned bytes (the library checks its size on every
-    call). Keyword options are those of decode_attention. A cache of pages of a multiple
-    of 16 tokens is planned over its 16-token view; each run rewrites its page table.
+    call). Keyword options are those of decode_attention.
+
+    A cache of pages of a multiple of 16 tokens is planned over its 16-token view. run()
+    then takes either that cache with its own page table, which it rewrites over the
+    sub-pages on every call (one more small kernel, about 6-8 us per call), or the view
+    and rewritten table that sixteen_token_pages returns: a model whose layers share one
+    page table rewrites it once per step and passes each layer's view,
+
+        _, ip16, ids16, last16 = sixteen_token_pages(kv_0, kv_indptr, kv_indices, last)
+        for layer in layers:
+            view, *_ = sixteen_token_pages(kv_l)
+            out = plan.run(q_l, view, ip16, ids16, last16, out=out_l)
     """
 
     def __init__(self, q, kv_data, kv_indptr, kv_indices, kv_last_page_len, split_kv=1, *,
@@ -569,6 +592,7 @@ class DecodePlan:
         ps = _page_size_of(kv_data)
         self._wide = ps is not None and ps != PAGE_SIZE and ps > 0 and ps % PAGE_SIZE == 0
         if self._wide:
+            _check(q, kv_data, kv_indptr, kv_indices, kv_last_page_len, wide_pages=True)
             kv_data, kv_indptr, kv_indices, kv_last_page_len = sixteen_token_pages(
                 kv_data, kv_indptr, kv_indices, kv_last_page_len)
             max_pages_per_seq *= ps // PAGE_SIZE
@@ -594,7 +618,8 @@ class DecodePlan:
         """One call with the plan. A plan made with sinks takes each call's sinks (a
         layer's own; same shape, dtype and device as the planned ones); one made without
         takes none."""
-        if getattr(self, "_wide", False):
+        if getattr(self, "_wide", False) and _page_size_of(kv_data) != PAGE_SIZE:
+            # the wide cache and its own table: rewritten here, on every run
             kv_data, kv_indptr, kv_indices, kv_last_page_len = sixteen_token_pages(
                 kv_data, kv_indptr, kv_indices, kv_last_page_len)
         if self._layout(q, kv_data, kv_indptr, kv_indices, kv_last_page_len) != self._guard:

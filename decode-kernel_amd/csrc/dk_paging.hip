@@ -40,16 +40,17 @@ __device__ __forceinline__ int pages_of(int32_t len) {
 // One workgroup per request b: its first page index is the sum of the page counts of
 // requests 0..b-1 (recomputed per workgroup: batch is at most a few thousand).
 __global__ __launch_bounds__(kThreads) void dk_page_table(PageTableArgs a) {
-  __shared__ int partial[kThreads / 64];
+  __shared__ int64_t partial[kThreads / 64];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  int sum = 0;
+  // int64: a batch of long requests can hold more than 2^31 pages in total
+  int64_t sum = 0;
   for (int j = tid; j < b; j += kThreads) sum += pages_of(a.seq_lens[j]);
   // workgroup sum: wavefront butterfly, then across the four wavefronts through LDS
   for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
   if ((tid & 63) == 0) partial[tid >> 6] = sum;
   __syncthreads();
-  int start = 0;
+  int64_t start = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) start += partial[w];
 
@@ -57,13 +58,15 @@ __global__ __launch_bounds__(kThreads) void dk_page_table(PageTableArgs a) {
   const int n = pages_of(len);
   if (tid == 0) {
     if (b == 0) a.kv_indptr[0] = 0;
-    a.kv_indptr[b + 1] = start + n;
+    // the true offsets (writes past the capacity are dropped), saturated at int32's range
+    a.kv_indptr[b + 1] = (int32_t)min(start + n, (int64_t)INT32_MAX);
     a.kv_last_page_len[b] = n > 0 ? len - (n - 1) * kPageSize : 0;
   }
   const int32_t* row = a.req_to_token + (int64_t)a.req_pool_indices[b] * a.req_stride;
   for (int p = tid; p < n; p += kThreads) {
-    const int64_t at = (int64_t)start + p;
-    if (at < a.capacity) a.kv_indices[at] = row[(int64_t)p * kPageSize] / kPageSize;
+    const int64_t at = start + p;
+    if (at >= a.capacity) break;
+    a.kv_indices[at] = row[(int64_t)p * kPageSize] / kPageSize;
   }
 }
 
@@ -100,23 +103,27 @@ __device__ __forceinline__ int sub_pages_of(const ExpandArgs& a, int b, int* np_
 // page id p is id p * mult + j; an invalid page id becomes INT32_MAX, which the decode
 // kernels treat as they treat any id past the pool.
 __global__ __launch_bounds__(kThreads) void dk_expand_pages(ExpandArgs a) {
-  __shared__ int partial[kThreads / 64];
+  __shared__ int64_t partial[kThreads / 64];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   int np, last;
-  int sum = 0;
+  // int64: sequences whose kv_indptr ranges overlap (not a valid table, but clamped, not
+  // refused) can add up to more sub-pages than int32 holds
+  int64_t sum = 0;
   for (int j = tid; j < b; j += kThreads) sum += sub_pages_of(a, j, &np, &last);
   for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
   if ((tid & 63) == 0) partial[tid >> 6] = sum;
   __syncthreads();
-  int start = 0;
+  int64_t start = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) start += partial[w];
 
   const int n = sub_pages_of(a, b, &np, &last);
   if (tid == 0) {
     if (b == 0) a.out_indptr[0] = 0;
-    a.out_indptr[b + 1] = start + n;
+    // saturated at the capacity, so that the rewritten table never points past its
+    // entries (a valid table's total is at most the capacity)
+    a.out_indptr[b + 1] = (int32_t)min(start + n, a.capacity);
     // the last sub-page's tokens: the last page's remainder, or a full sub-page when the
     // last page holds none (last_len 0 ends the sequence at the page before)
     const int rem = last - ((last + kPageSize - 1) / kPageSize - 1) * kPageSize;
@@ -124,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void dk_expand_pages(ExpandArgs a) {
   }
   const int s0 = min(max(a.indptr[b], 0), a.num_indices);
   for (int t = tid; t < n; t += kThreads) {
-    const int64_t at = (int64_t)start + t;
+    const int64_t at = start + t;
     if (at >= a.capacity) break;
     const int p = t / a.sub, j = t % a.sub;
     const int32_t pid = a.indices[s0 + p];

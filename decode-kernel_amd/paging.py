@@ -93,11 +93,21 @@ def expand_page_table(kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
     are left uninitialised. No host synchronisation."""
     for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
                     ("kv_last_page_len", kv_last_page_len)):
-        if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous():
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.int32 or t.dim() != 1 or \
+                not t.is_contiguous():
             raise DecodeArgumentError(f"{name} must be a contiguous 1-D int32 tensor")
     if page_size <= 0 or page_size % PAGE_SIZE:
         raise DecodeArgumentError(f"page_size must be a positive multiple of 16, got {page_size}")
+    if kv_indptr.shape[0] < 1 or kv_last_page_len.shape[0] != kv_indptr.shape[0] - 1:
+        raise DecodeArgumentError(
+            f"kv_last_page_len must have one entry per sequence (len(kv_indptr) - 1 = "
+            f"{kv_indptr.shape[0] - 1}); got {kv_last_page_len.shape[0]}")
     dev = kv_indptr.device
+    # the kernel reads all three tables on one GPU: host memory there would fault it
+    if dev.type != "cuda" or kv_indices.device != dev or kv_last_page_len.device != dev:
+        raise DecodeArgumentError(
+            f"kv_indptr, kv_indices and kv_last_page_len must be on one GPU; got "
+            f"{kv_indptr.device}, {kv_indices.device}, {kv_last_page_len.device}")
     batch = int(kv_indptr.shape[0]) - 1
     sub = page_size // PAGE_SIZE
     capacity = int(kv_indices.shape[0]) * sub

@@ -50,14 +50,19 @@ def expand_page_table(kv_indptr, kv_indices, kv_last_page_len, page_size: int,
     is p * pages_mult + j; a sequence of n pages whose last holds `last` tokens (clamped
     to [0, page_size]) has (n - 1) s + ceil(last / 16) sub-pages, the last holding the
     remainder (16 when last is a multiple of 16, 0 included). Ids outside [0, num_pages)
-    become 2^31 - 1. Returns (indptr, indices, last) int32. No counterpart in the
+    become 2^31 - 1. kv_indptr is clamped to [0, len(kv_indices)] entry by entry, so the
+    ranges of an invalid table may overlap; the rewritten table then holds only its first
+    capacity = len(kv_indices) * s entries and its offsets saturate there (a valid table
+    never reaches it). Returns (indptr, indices, last) int32. No counterpart in the
     reference (whose page_size is 16); pinned by token order: the sub-page table must
     describe the same token rows of the cache as the page table it came from."""
     s = page_size // PAGE
     indptr = np.asarray(kv_indptr, np.int64)
     indices = np.asarray(kv_indices, np.int64)
     lastv = np.asarray(kv_last_page_len, np.int64)
+    capacity = len(indices) * s
     out_ptr, out_idx, out_last = [0], [], []
+    total = 0
     for b in range(len(indptr) - 1):
         s0 = min(max(int(indptr[b]), 0), len(indices))
         s1 = min(max(int(indptr[b + 1]), s0), len(indices))
@@ -65,9 +70,12 @@ def expand_page_table(kv_indptr, kv_indices, kv_last_page_len, page_size: int,
         last = min(max(int(lastv[b]), 0), page_size)
         m = (n - 1) * s + -(-last // PAGE) if n > 0 else 0
         for t in range(m):
+            if len(out_idx) >= capacity:
+                break
             pid = int(indices[s0 + t // s])
             out_idx.append(pid * pages_mult + t % s if 0 <= pid < num_pages else 2**31 - 1)
-        out_ptr.append(out_ptr[-1] + m)
+        total += m
+        out_ptr.append(min(total, capacity))
         out_last.append(0 if m == 0 else (PAGE if last % PAGE == 0 else last % PAGE))
     return (np.asarray(out_ptr, np.int32), np.asarray(out_idx, np.int32),
             np.asarray(out_last, np.int32))

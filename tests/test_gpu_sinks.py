@@ -2,9 +2,10 @@
 head's softmax has one more logit, with no value. The HIP path against the fp32 oracle
 (whose sink form is pinned against transformers' gpt-oss eager attention in
 tests/test_oracle.py) on every place that normalises an output: one pass (one and several
-wavefronts per workgroup, VALU and MFMA q.k head layouts), explicit splits (merge kernel),
-the balanced schedule (direct writes and merges), an fp8 cache, a sliding window, empty and
-one-token sequences, and a sink that dominates every score.
+wavefronts per workgroup, VALU and MFMA q.k head layouts, D = 64, 128 and 256), explicit
+splits (merge kernel), the balanced schedule (direct writes and merges), an fp8 cache, a
+sliding window, soft-capped scores (logit_cap) together with sinks, empty and one-token
+sequences, and a sink that dominates every score.
 """
 import numpy as np
 import pytest
@@ -50,6 +51,12 @@ CASES = [
     ("balanced D=64 grouped", 32, 8, 64, 0, {}),
     ("automatic with hint", 32, 8, 128, 0, dict(hint=True)),
     ("window 100", 32, 8, 128, 0, dict(window=100)),
+    ("one pass D=256", 16, 4, 256, 1, {}),
+    ("balanced D=256", 16, 4, 256, 0, {}),
+    ("one pass logit_cap", 32, 8, 128, 1, dict(logit_cap=20.0)),
+    ("balanced logit_cap", 32, 8, 128, 0, dict(logit_cap=20.0)),
+    ("split 3 D=256 logit_cap", 16, 4, 256, 3, dict(logit_cap=15.0)),
+    ("balanced MFMA q.k logit_cap", 64, 8, 128, 0, dict(logit_cap=20.0)),
 ]
 
 
@@ -71,7 +78,8 @@ def test_sinks_match_oracle(label, hq, hkv, d, split, extra, dtype):
     want = ref.reference_attention_paged(to_np(q).astype(np.float32),
                                          to_np(kv).astype(np.float32), to_np(indptr),
                                          to_np(ids), to_np(last), sinks=sinks.numpy(),
-                                         window=extra.get("window"))
+                                         window=extra.get("window"),
+                                         logit_cap=extra.get("logit_cap"))
     _check(out, want, lens, dtype, label)
     assert out[:, 3].abs().max().item() < 1e-6      # the dominant sink leaves ~nothing
 

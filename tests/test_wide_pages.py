@@ -66,6 +66,16 @@ def test_expand_known_answer():
     assert last.tolist() == [1, 0, 16, 0]   # 17 = 16 + 1; empty; 32 = two full; last 0, one page
 
 
+def test_expand_overlapping_indptr_saturates_at_capacity():
+    # kv_indptr [0, 4, 0, 4] is clamped entry by entry: sequence 1 is empty and sequence 2
+    # covers all four pages again, 16 sub-pages for a table of capacity 4 * 2 = 8
+    indptr, indices, last = ptab.expand_page_table([0, 4, 0, 4], [3, 0, 2, 1], [32, 5, 32],
+                                                   32, 2, 4)
+    assert indptr.tolist() == [0, 8, 8, 8]
+    assert indices.tolist() == [6, 7, 0, 1, 4, 5, 2, 3]     # sequence 0's, then full
+    assert last.tolist() == [16, 0, 16]
+
+
 @pytest.mark.parametrize("page_size", [32, 64, 128])
 @pytest.mark.parametrize("seed", range(4))
 def test_expansion_gathers_the_same_tokens(page_size, seed):
@@ -130,6 +140,21 @@ def test_expand_rejects_bad_arguments_before_launch(kw, needle):
                                     None) == 0
 
 
+def test_wide_page_tables_are_checked_before_the_expansion():
+    """The expansion kernel reads the three tables on the GPU: host tables and a
+    kv_last_page_len shorter than the batch are refused on the host, before any launch."""
+    t5, t4, t3 = (torch.zeros(n, dtype=torch.int32) for n in (5, 4, 3))
+    with pytest.raises(dk_lib.DecodeArgumentError, match="one entry per sequence"):
+        paging.expand_page_table(t5, t4, t3, 32, 2, 4)
+    with pytest.raises(dk_lib.DecodeArgumentError, match="on one GPU"):
+        paging.expand_page_table(t5, t4, t4, 32, 2, 4)
+    q = torch.zeros(4, 8, 64, dtype=torch.float16)
+    kv = torch.zeros(4, 2, 32, 2, 64, dtype=torch.float16)
+    for fn in (attention.decode_attention, attention.DecodePlan):
+        with pytest.raises(dk_lib.DecodeArgumentError, match="CUDA"):
+            fn(q, kv, t5, t4, t4)
+
+
 def test_page_sizes_not_a_multiple_of_sixteen_are_refused():
     q = torch.zeros(1, 4, 64, dtype=torch.float16)
     kv = torch.zeros(2, 2, 24, 1, 64, dtype=torch.float16)
@@ -156,6 +181,50 @@ def test_device_expansion_matches_oracle(page_size, mult, seed):
     assert d_ptr.cpu().numpy().tolist() == w_ptr.tolist()
     assert d_last.cpu().numpy().tolist() == w_last.tolist()
     assert d_ids[:int(w_ptr[-1])].cpu().numpy().tolist() == w_ids.tolist()
+
+
+@pytest.mark.gpu
+def test_device_expansion_of_overlapping_ranges_stays_in_its_table():
+    """kv_indptr whose clamped ranges overlap (each of 40 sequences covering the whole
+    index range): the offsets saturate at the capacity and nothing is written past it,
+    as the oracle states."""
+    rng = np.random.default_rng(5)
+    n, batch, num_pages = 64, 40, 80
+    indptr = np.array([0, n] * (batch // 2) + [0], np.int32)
+    ids = rng.permutation(num_pages)[:n].astype(np.int32)
+    last = rng.integers(1, 65, size=batch).astype(np.int32)
+    print("[case] expand overlapping kv_indptr", flush=True)
+    to = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    d_ptr, d_ids, d_last = paging.expand_page_table(to(indptr), to(ids), to(last), 64, 4,
+                                                    num_pages)
+    torch.cuda.synchronize()
+    w_ptr, w_ids, w_last = ptab.expand_page_table(indptr, ids, last, 64, 4, num_pages)
+    assert int(w_ptr[-1]) == n * 4 == d_ids.shape[0]
+    assert d_ptr.cpu().numpy().tolist() == w_ptr.tolist()
+    assert d_last.cpu().numpy().tolist() == w_last.tolist()
+    assert d_ids.cpu().numpy().tolist() == w_ids.tolist()
+
+
+@pytest.mark.gpu
+def test_wide_pages_refuse_host_tables_and_short_last_page_len():
+    """A 32-token cache on the GPU with a host kv_indices, or a kv_last_page_len shorter
+    than the batch: decode_attention and DecodePlan raise before the expansion launches."""
+    lens = [40, 70, 33]
+    q, kv, indptr, ids, last = _wide_inputs(len(lens), lens, 32, 16, 4, 64, torch.float16,
+                                            seed=2)
+    qd, kd, ipd, idd, lad = (t.to(DEV) for t in (q, kv, indptr, ids, last))
+    print("[case] wide pages bad tables", flush=True)
+    for fn in (attention.decode_attention, attention.DecodePlan):
+        with pytest.raises(dk_lib.DecodeArgumentError, match="kv_indices must be on"):
+            fn(qd, kd, ipd, ids, lad)
+        with pytest.raises(dk_lib.DecodeArgumentError, match="one entry per sequence"):
+            fn(qd, kd, ipd, idd, lad[:2])
+    plan = attention.DecodePlan(qd, kd, ipd, idd, lad)
+    with pytest.raises(dk_lib.DecodeArgumentError):
+        plan.run(qd, kd, ipd, idd.cpu(), lad)
+    with pytest.raises(dk_lib.DecodeArgumentError):
+        plan.run(qd, kd, ipd, idd, lad[:2])
+    torch.cuda.synchronize()
 
 
 def _wide_inputs(batch, lens, page_size, hq, hkv, d, dtype, seed):
@@ -268,9 +337,13 @@ def test_decode_plan_over_wide_pages():
     hint = int((indptr[1:] - indptr[:-1]).max())
     print("[case] DecodePlan over 64-token pages", flush=True)
     plan = attention.DecodePlan(qd, layers[0], *tabs, split_kv=0, max_pages_per_seq=hint)
+    # the table rewritten once for all layers, each run over a layer's 16-token view
+    _, *tabs16 = attention.sixteen_token_pages(layers[0], *tabs)
     for layer_kv in layers:
         got = plan.run(qd, layer_kv, *tabs)
+        view, *_ = attention.sixteen_token_pages(layer_kv)
+        got16 = plan.run(qd, view, *tabs16)
         want = attention.decode_attention(qd, layer_kv, *tabs, split_kv=0,
                                           max_pages_per_seq=hint)
         torch.cuda.synchronize()
-        assert torch.equal(got, want)
+        assert torch.equal(got, want) and torch.equal(got16, want)
