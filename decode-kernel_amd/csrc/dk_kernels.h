@@ -489,11 +489,13 @@ struct Wave {
 
   // K and V rows of a page straight into the LDS slot: instruction i writes bytes
   // i*1024.. of the slot's K (V) part, lane L bytes 16L..16L+15, i.e. token
-  // i*TPI + L/(64/TPI), 16-byte chunk L%(64/TPI) of its row (RB >= 256 bytes per row).
+  // i*TPI + L/(64/TPI), 16-byte chunk L%(64/TPI) of its row. Every lane loads 16 bytes and
+  // every instruction reads whole rows: 8 rows of 128 bytes (16-bit D = 64, fp8 D = 128),
+  // 16 of 64 bytes (fp8 D = 64), 4 of 256 or 2 of 512.
   // live == false: a zero-extent descriptor (no memory access; the slot gets zeros).
   __device__ __forceinline__ void lds_load_page(uint8_t* slot, const uint8_t* pg,
                                                 bool live = true) const {
-    static_assert(RB >= 256 && 1024 % RB == 0, "rows of 256, 512 or 1024 bytes");
+    static_assert(RB >= 64 && RB <= 1024 && 1024 % RB == 0, "rows of 64 to 1024 bytes");
     constexpr int TPI = 1024 / RB, LPR = 64 / TPI;   // tokens per instruction, lanes per row
     const u32 ext = live ? extent : 0u;
     const __amdgpu_buffer_rsrc_t rk = page_rsrc(pg, ext);
@@ -512,17 +514,93 @@ struct Wave {
   }
 
   // A page of the LDS slot into the VALU layout's registers (tokens 4*r16 .. 4*r16+3,
-  // bytes c*RB/16 .. of each row): 16 ds_read_b128 and their lgkmcnt wait in one asm
-  // block (outputs early-clobber, so none shares a register with the address). Written in
-  // asm because a compiler-visible LDS read after the LDS-bound buffer loads makes hipcc
-  // wait for all of them (vmcnt(0)), which would serialise the ring; the waits for those
-  // loads are stream_lds's.
+  // bytes c*RB/16 .. of each row) and the lgkmcnt wait, in one asm block (outputs
+  // early-clobber, so none shares a register with the address). Written in asm because a
+  // compiler-visible LDS read after the LDS-bound buffer loads makes hipcc wait for all of
+  // them (vmcnt(0)), which would serialise the ring; the waits for those loads are
+  // stream_lds's. Rows of RB bytes give each lane RB/16 bytes per token: 4 (ds_read_b32),
+  // 8 (b64), 16 (b128) or 32 (two b128).
   __device__ __forceinline__ void lds_read_page(const uint8_t* slot, u32 (&kb)[KB],
                                                 u32 (&vb)[VB]) const {
-    static_assert(KB == 32 && VB == 32 && RB == 512 && LDS_PAGE == 16384,
-                  "LDS pages: 16-bit caches at D = 256 (the offsets below)");
+    static_assert(KB == VB && KB == RB / 16 && LDS_PAGE == 32 * RB,
+                  "a page slot of K rows then V rows, RB / 16 bytes per lane and token");
     const u32 base = (u32)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(
         slot + 4 * r16 * RB + c * (RB / 16));
+    if constexpr (RB == 512) {
+      lds_read_512(base, kb, vb);
+    } else if constexpr (RB == 256) {
+      u32x4 k[4], v[4];
+      asm volatile(
+          "ds_read_b128 %0, %8 offset:0\n\t"
+          "ds_read_b128 %1, %8 offset:256\n\t"
+          "ds_read_b128 %2, %8 offset:512\n\t"
+          "ds_read_b128 %3, %8 offset:768\n\t"
+          "ds_read_b128 %4, %8 offset:4096\n\t"
+          "ds_read_b128 %5, %8 offset:4352\n\t"
+          "ds_read_b128 %6, %8 offset:4608\n\t"
+          "ds_read_b128 %7, %8 offset:4864\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
+            "=&v"(v[2]), "=&v"(v[3])
+          : "v"(base)
+          : "memory");
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kb[4 * i + e] = k[i][e];
+          vb[4 * i + e] = v[i][e];
+        }
+    } else if constexpr (RB == 128) {
+      u32x2 k[4], v[4];
+      asm volatile(
+          "ds_read_b64 %0, %8 offset:0\n\t"
+          "ds_read_b64 %1, %8 offset:128\n\t"
+          "ds_read_b64 %2, %8 offset:256\n\t"
+          "ds_read_b64 %3, %8 offset:384\n\t"
+          "ds_read_b64 %4, %8 offset:2048\n\t"
+          "ds_read_b64 %5, %8 offset:2176\n\t"
+          "ds_read_b64 %6, %8 offset:2304\n\t"
+          "ds_read_b64 %7, %8 offset:2432\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
+            "=&v"(v[2]), "=&v"(v[3])
+          : "v"(base)
+          : "memory");
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          kb[2 * i + e] = k[i][e];
+          vb[2 * i + e] = v[i][e];
+        }
+    } else {
+      static_assert(RB == 64, "rows of 64, 128, 256 or 512 bytes");
+      u32 k[4], v[4];
+      asm volatile(
+          "ds_read_b32 %0, %8 offset:0\n\t"
+          "ds_read_b32 %1, %8 offset:64\n\t"
+          "ds_read_b32 %2, %8 offset:128\n\t"
+          "ds_read_b32 %3, %8 offset:192\n\t"
+          "ds_read_b32 %4, %8 offset:1024\n\t"
+          "ds_read_b32 %5, %8 offset:1088\n\t"
+          "ds_read_b32 %6, %8 offset:1152\n\t"
+          "ds_read_b32 %7, %8 offset:1216\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]),
+            "=&v"(v[2]), "=&v"(v[3])
+          : "v"(base)
+          : "memory");
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kb[i] = k[i];
+        vb[i] = v[i];
+      }
+    }
+  }
+
+  // lds_read_page for 512-byte rows (16-bit caches at D = 256): 16 ds_read_b128
+  __device__ __forceinline__ void lds_read_512(u32 base, u32 (&kb)[KB], u32 (&vb)[VB]) const {
     u32x4 k[8], v[8];
     asm volatile(
         "ds_read_b128 %0, %16 offset:0\n\t"
@@ -1089,16 +1167,35 @@ __device__ __forceinline__ void stream_lds(W& wv, uint8_t* ring, int n, PageFn p
   wait_vmem<0>();
 }
 
-// Whether a kernel streams its pages through LDS (stream_lds): 16-bit caches at D = 256
-// on the VALU q.k path, with at most 2 wavefronts per workgroup (LDS: 64 KB each).
-// (a build may set another depth with DK_LDS_DEPTH; 2 measured the same as 3 at D=256)
+// Whether a kernel streams its pages through LDS (stream_lds), on the VALU q.k path:
+// 16-bit caches at D = 256 (512-byte rows) with at most 2 wavefronts per workgroup (LDS:
+// 64 KB each), and, with DK_LDS_NARROW, rows of at most 128 bytes (16-bit D = 64, fp8
+// D <= 128: 16-byte lane loads instead of 8 or 4) with at most 4 wavefronts.
+// (a build may set another depth with DK_LDS_DEPTH / DK_LDS_DEPTH_NARROW; 2 measured the
+// same as 3 at D=256)
 #ifndef DK_LDS_DEPTH
 #define DK_LDS_DEPTH 3
 #endif
-constexpr int kLdsDepth = DK_LDS_DEPTH;
+#ifndef DK_LDS_DEPTH_NARROW
+#define DK_LDS_DEPTH_NARROW 3
+#endif
+#ifndef DK_LDS_NARROW
+#define DK_LDS_NARROW 0
+#endif
+#ifndef DK_LDS_256
+#define DK_LDS_256 0
+#endif
+template <int D, bool KV8>
+constexpr int lds_depth() {
+  return D * (KV8 ? 1 : 2) <= kNarrowRowBytes ? DK_LDS_DEPTH_NARROW : DK_LDS_DEPTH;
+}
 template <int D, bool KV8, bool MFMA, int NW>
 constexpr bool lds_pages() {
-  return DK_LDS_PAGES && D == 256 && !KV8 && !MFMA && NW <= 2;
+  constexpr int rb = D * (KV8 ? 1 : 2);
+  if (!DK_LDS_PAGES || MFMA) return false;
+  if (rb == 512) return !KV8 && NW <= 2;
+  if (rb == 256) return DK_LDS_256 && NW <= 2;
+  return DK_LDS_NARROW && rb <= kNarrowRowBytes && NW <= 4;
 }
 
 // ---------------------------------------------------------------- workgroup combine
@@ -1200,7 +1297,7 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
     auto vk = [&](int k) { return valid(w + NW * k); };
     constexpr int depth = prefetch_depth<D, KV8>();
     if constexpr (LDS) {
-      stream_lds<kLdsDepth, CAP>(wv, ring, nk, pk, vk);
+      stream_lds<lds_depth<D, KV8>(), CAP>(wv, ring, nk, pk, vk);
     } else if constexpr (depth <= 2) {
       u32 ka[WV::KB], va[WV::VB];
       wv.load_page(ka, va, pk(0));
@@ -1245,7 +1342,7 @@ __global__ __launch_bounds__(NW * 64, (min_waves_per_simd<D, G, KV8>())) void dk
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> sm;
   __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? NW * WV::STAGE_BYTES : 16];
   constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW>();
-  constexpr int RING = (kLdsDepth + 1) * WV::LDS_PAGE;
+  constexpr int RING = (lds_depth<D, KV8>() + 1) * WV::LDS_PAGE;
   __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? NW * RING : 16];
   WV wv;
   wv.init(a);
@@ -1375,7 +1472,7 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> smh[HP];
   __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? HP * NW * WV::STAGE_BYTES : 16];
   constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW * HP>();
-  constexpr int RING = (kLdsDepth + 1) * WV::LDS_PAGE;
+  constexpr int RING = (lds_depth<D, KV8>() + 1) * WV::LDS_PAGE;
   __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? HP * NW * RING : 16];
   WV wv;
   wv.init(a);
