@@ -32,11 +32,22 @@ Modes:
                    the fraction of 8 TB/s and the max-abs error against the CPU oracle on
                    sampled sequences
   --single-call    one flush and one call, no settling or warm-up (for rocprofv3 --pmc
-                   counter runs, which then see exactly the call's dispatches)
+                   counter runs, which then see exactly the call's dispatches); with
+                   --no-check the call is the run's only decode dispatch (no checking call
+                   before it, no correctness call after it)
+  --graph          the latency-bound configs as a model runs them: N back-to-back calls on
+                   N distinct caches (N x bytes >= 1 GiB, so no flush is needed between
+                   calls; config 5's 16-layer step as stated), eager and captured in one
+                   HIP graph and replayed, reported per call beside the flush + events
+                   protocol's figure of the same shape (one JSON line per point)
   --host-overhead  host time per call of the Python entry points (back to back, no
                    flush): attention.decode_attention, DecodePlan.run with a preallocated
                    output, the bare C-ABI call, and a call that validates its arguments
                    afresh (no cached plan)
+
+With the environment variable DK_TRACE set, every timed step is a roctx range ("step i")
+holding a "flush" and a "call" range (rocprofv3 --marker-trace), around the library's own
+ranges of each launch.
 
 `value` is achieved algorithmic HBM bandwidth in TB/s (bytes of the reference's model,
 bench/microbench_cuda.py:114-121, plus page tables, divided by the p50 per-call time);
@@ -54,6 +65,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import math
 import os
@@ -108,6 +120,14 @@ def parse_args(argv=None):
                     help="run BASELINE.json config N's sweep (one JSON line per point)")
     ap.add_argument("--single-call", action="store_true",
                     help="one flush + one call, no settling / warm-up (counter runs)")
+    ap.add_argument("--no-check", action="store_true",
+                    help="--single-call: no checking call before the timed call and no "
+                         "correctness call after it (the run's only decode dispatch)")
+    ap.add_argument("--graph", action="store_true",
+                    help="latency-bound configs as N back-to-back calls on N caches, eager "
+                         "and under HIP-graph replay (see the modes)")
+    ap.add_argument("--graph-point", default="",
+                    help="--graph: only the point of this label (e.g. 'C2 B=1')")
     ap.add_argument("--host-overhead", action="store_true",
                     help="host us per call of attention.decode_attention (see the modes)")
     ap.add_argument("--split", type=int, default=0, help="split_kv (0 = automatic)")
@@ -163,6 +183,11 @@ def parse_args(argv=None):
         ap.error(f"--ragged-min must be in [1, ctx={a.ctx}], got {a.ragged_min}")
     if a.single_call and a.config:
         ap.error("--single-call times the default workload; it does not combine with --config")
+    if a.no_check and not a.single_call:
+        ap.error("--no-check applies to --single-call")
+    if a.graph and (a.config or a.single_call or a.host_overhead or a.page_size != 16):
+        ap.error("--graph runs its own points; it does not combine with --config, "
+                 "--single-call, --host-overhead or --page-size")
     if a.window < 0:
         ap.error(f"--window must be >= 0, got {a.window}")
     if (a.sinks or a.window) and a.config:
@@ -175,18 +200,45 @@ def parse_args(argv=None):
     return a
 
 
+# Sources whose digest stamps a traffic measurement: every file the library is built from.
+KERNEL_SOURCES = ROOT / "decode-kernel_amd" / "csrc"
+
+
+def kernel_source_digest():
+    """sha256 (16 hex digits) over the library's sources (decode-kernel_amd/csrc/*.h, *.hip,
+    *.cpp, by name and content): a traffic figure measured on another digest does not
+    describe the kernel this tree builds."""
+    h = hashlib.sha256()
+    for f in sorted(KERNEL_SOURCES.iterdir()):
+        if f.suffix in (".h", ".hip", ".cpp"):
+            h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()[:16]
+
+
 def read_traffic(kv_dtype="same"):
-    """HBM bytes per pass-1 launch recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE."""
+    """(HBM bytes per pass-1 launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, or None when the
+    profile was measured on other kernel sources; the profile's stamp). The profile file
+    holds `traffic_bytes_per_launch:`, `kernel_source_digest:` and `measured_at_commit:`
+    lines."""
     path = TRAFFIC_FILES[kv_dtype]
     if not path.exists():
-        return None
+        return None, None
+    fields = {}
     for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            try:
-                return int(line.split(":", 1)[1].strip())
-            except ValueError:
-                return None
-    return None
+        key, sep, val = line.partition(":")
+        if sep and key in ("traffic_bytes_per_launch", "kernel_source_digest",
+                           "measured_at_commit"):
+            fields[key] = val.strip()
+    try:
+        traffic = int(fields["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None, None
+    current = kernel_source_digest()
+    stamp = {"file": str(path.relative_to(ROOT)), "commit": fields.get("measured_at_commit"),
+             "kernel_source_digest": fields.get("kernel_source_digest"),
+             "current_digest": current,
+             "matches_build": fields.get("kernel_source_digest") == current}
+    return (traffic if stamp["matches_build"] else None), stamp
 
 
 def host_cpu():
@@ -307,12 +359,31 @@ class Caller:
                                     else f"split {self.schedule} + merge")
 
 
+def roctx_ranges():
+    """(push, pop) of the roctx library when DK_TRACE is set (to anything but "" or "0"),
+    else None: the same library and switch as libdk_decode's launch ranges."""
+    if os.environ.get("DK_TRACE", "") in ("", "0"):
+        return None
+    for name in ("librocprofiler-sdk-roctx.so.1", "libroctx64.so.4"):
+        try:
+            lib = ctypes.CDLL(name)
+        except OSError:
+            continue
+        push, pop = lib.roctxRangePushA, lib.roctxRangePop
+        push.argtypes, push.restype, pop.restype = [ctypes.c_char_p], ctypes.c_int, ctypes.c_int
+        return push, pop
+    return None
+
+
 class Timer:
-    """Flush + events around each call, on the launch stream."""
+    """Flush + events around each call, on the launch stream (each step a roctx range
+    under DK_TRACE)."""
 
     def __init__(self, torch, dev, stream, mode="write"):
         self.torch, self.stream, self.mode = torch, stream, mode
         self.buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+        self.ranges = roctx_ranges()
+        self.nstep = 0
 
     def flush(self):
         # evict the caches: write (fill) or read (sum) a 1 GiB buffer
@@ -325,11 +396,22 @@ class Timer:
         torch = self.torch
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(steps)]
+        rg = self.ranges
         for e0, e1 in evs:
+            if rg:
+                rg[0](f"step {self.nstep}".encode())
+                rg[0](b"flush")
             self.flush()
+            if rg:
+                rg[1]()
+                rg[0](b"call")
             e0.record(self.stream)
             fn()
             e1.record(self.stream)
+            if rg:
+                rg[1]()
+                rg[1]()
+            self.nstep += 1
         torch.cuda.synchronize()
         return [e0.elapsed_time(e1) * 1e3 for e0, e1 in evs]     # microseconds
 
@@ -465,11 +547,12 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     opts, hint = make_opts(dk_lib, args, wl, split)
     c = Caller(lib, dk_lib, attention, wl, split, opts, stream)
     timer = Timer(torch, dev, stream, args.flush)
-    dk_lib.check(c.full(), "decode_attention")
+    if not args.no_check:
+        dk_lib.check(c.full(), "decode_attention")
     if args.single_call:
         steps, warmup = 1, 0
         torch.cuda.synchronize()
-        call_us = timer.run(c.full, 1)
+        call_us = timer.run(lambda: dk_lib.check(c.full(), "decode_attention"), 1)
         pass1_us = call_us if c.schedule == 1 else None
         wall = 0.0
     else:
@@ -487,8 +570,10 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     p95 = percentile(call_us, 95)
     p1_avg = statistics.fmean(pass1_us) if pass1_us else p50
     achieved = wl.bytes / (p1_avg * 1e-6) / 1e9           # GB/s, the dominant kernel alone
-    # final correctness of the timed output
-    dk_lib.check(c.full(), "decode_attention")
+    # final correctness of the timed output (a single call with --no-check keeps the timed
+    # call's output as it is)
+    if not args.no_check:
+        dk_lib.check(c.full(), "decode_attention")
     torch.cuda.synchronize()
     finite = bool(torch.isfinite(c.out).all())
     hq, hkv, d = wl.hq, wl.hkv, wl.d
@@ -514,12 +599,17 @@ def metric_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
         "pass1_us_avg": round(p1_avg, 2), "output_finite": finite,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": read_traffic(args.kv_dtype) if metric_workload else None,
+                     "traffic": None, "traffic_from": None,
                      "kernel": "dk_pass1_balanced" if c.schedule == 0 else "dk_pass1_split"},
         "cpu_baseline": None,
     }
+    if metric_workload:
+        traffic, stamp = read_traffic(args.kv_dtype)
+        rec["roofline"].update(traffic=traffic, traffic_from=stamp)
     if args.single_call:
-        rec["mode"] = "single call (no settling, no warm-up)"
+        rec["mode"] = ("single call (no settling, no warm-up" +
+                       (", no checking calls: the run's only decode dispatch)"
+                        if args.no_check else ")"))
     if extension:
         # the reference has neither: no CPU baseline of its path; the output against the
         # oracle's masked form with the same options on the first and last sequences
@@ -714,6 +804,94 @@ def config_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
         release_device_memory(torch)
 
 
+# --graph points: the latency-bound configs, each as N back-to-back calls on N caches of
+# its shape (label, BASELINE config, shape, split_kv, layers; 0 layers = enough for 1 GiB)
+GRAPH_POINTS = [
+    ("C1", 1, dict(CONFIGS[1][0]), 4, 0),
+    ("C1 auto", 1, dict(CONFIGS[1][0]), 0, 0),
+    ("C2 B=1", 2, dict(batch=1, ctx=4096, dtype="fp16", table="permuted"), 0, 0),
+    ("C2 B=4", 2, dict(batch=4, ctx=4096, dtype="fp16", table="permuted"), 0, 0),
+    ("C5 step", 5, dict(CONFIGS[5][0]), 0, 16),     # the 16 attention layers of the step
+]
+GRAPH_MIN_BYTES = 1 << 30      # the N caches of a point together: > L2 + Infinity Cache
+
+
+def graph_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
+    """Per point: the flush + events protocol's p50 for one call, then N calls on N
+    distinct caches back to back (events around the whole sequence, no flush: the caches
+    together exceed every cache level), eager and as one captured HIP graph replayed, as a
+    model step runs its attention layers. Reports us per call of each; checks that every
+    layer's output of a replay equals its eager output bit for bit."""
+    timer = Timer(torch, dev, stream, args.flush)
+    cap = torch.cuda.Stream(dev)
+    points = [p for p in GRAPH_POINTS if not args.graph_point or p[0] == args.graph_point]
+    if not points:
+        raise SystemExit(f"--graph-point {args.graph_point!r}: no such point "
+                         f"({', '.join(p[0] for p in GRAPH_POINTS)})")
+    for label, cid, shape, split, layers in points:
+        wl0 = config_workload(torch, layout, dev, shape)
+        n = layers or max(16, -(-GRAPH_MIN_BYTES // wl0.bytes))
+        wls = [wl0] + [config_workload(torch, layout, dev, dict(shape, seed=1 + i))
+                       for i in range(1, n)]
+        proto = measure_point(args, dk_lib, attention, lib, timer, wl0, split, stream,
+                              settle=True)
+        opts = [make_opts(dk_lib, args, wl, split)[0] for wl in wls]
+        callers = [Caller(lib, dk_lib, attention, wl, split, o, cap)
+                   for wl, o in zip(wls, opts)]
+
+        def step():
+            for c in callers:
+                dk_lib.check(c.full(), "decode_attention")
+
+        def timed(fn, reps):
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(reps)]
+            with torch.cuda.stream(cap):
+                for e0, e1 in evs:
+                    e0.record(cap)
+                    fn()
+                    e1.record(cap)
+            torch.cuda.synchronize()
+            return sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+
+        # eager, back to back (the first steps also load every kernel before the capture)
+        timed(step, max(args.warmup, 2))
+        eager = timed(step, args.steps)
+        want = [c.out.clone() for c in callers]
+        for c in callers:
+            c.out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            step()
+        timed(g.replay, max(args.warmup, 2))
+        graph = timed(g.replay, args.steps)
+        same = all(torch.equal(c.out, w) for c, w in zip(callers, want))
+        p50e, p50g = statistics.median(eager) / n, statistics.median(graph) / n
+        rec = {
+            "metric": "µs per call of N back-to-back calls on N caches (HIP graph replay)",
+            "value": round(p50g, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": False, "dtype": wl0.dtype_name,
+            "data": "synthetic",
+            "config": {"point": label, "config_id": cid, "workload": wl0.label(),
+                       "split_kv": split, "schedule": proto["schedule"], "layers": n,
+                       "bytes_per_call": wl0.bytes},
+            "us_per_call_graph": round(p50g, 2),
+            "us_per_call_graph_p95": round(percentile(graph, 95) / n, 2),
+            "us_per_call_eager": round(p50e, 2),
+            "us_per_call_protocol": proto["us_per_call"],
+            "tb_s_graph": round(wl0.bytes / (p50g * 1e-6) / 1e12, 4),
+            "frac_graph": round(wl0.bytes / (p50g * 1e-6) / (PEAK_GBPS * 1e9), 4),
+            "us_per_replay": round(statistics.median(graph), 2),
+            "graph_matches_eager": same,
+        }
+        print(json.dumps(rec), flush=True)
+        if not same:
+            raise RuntimeError(f"{label}: a graph replay's output differs from the eager call's")
+        del g, callers, wls, wl0, want
+        release_device_memory(torch)
+
+
 def host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream):
     """Host microseconds per call, issued back to back (no flush, no sync inside the
     timed loop; the GPU runs behind): the bare C-ABI call with prebuilt arguments, the
@@ -839,6 +1017,8 @@ def main(argv=None):
         host_overhead_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
     elif args.config:
         config_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
+    elif args.graph:
+        graph_run(args, torch, lib, dk_lib, attention, layout, dev, stream)
     elif args.page_size != 16:
         wide_pages_run(args, torch, attention, dev, stream)
     else:

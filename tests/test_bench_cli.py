@@ -30,12 +30,86 @@ def test_ragged_lengths_beyond_the_context_are_refused_before_any_gpu_work():
 
 @pytest.mark.parametrize("kv_dtype,algorithmic", [("same", 1_074_331_908),
                                                   ("fp8", 537_460_996)])
-def test_recorded_traffic_is_read_and_close_to_the_algorithmic_bytes(kv_dtype, algorithmic):
-    # profiles/*_hbm_traffic.md hold rocprofv3 FETCH_SIZE + WRITE_SIZE per launch; the bench
-    # line reports them as roofline.traffic. Every cache byte is read once: within 1 %.
-    t = bench.read_traffic(kv_dtype)
-    assert t is not None
-    assert abs(t / algorithmic - 1.0) < 0.01, t
+def test_recorded_traffic_is_stamped_and_close_to_the_algorithmic_bytes(kv_dtype, algorithmic):
+    # profiles/*_hbm_traffic.md hold rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, the commit
+    # and the digest of the kernel sources they were measured on; the bench line reports the
+    # bytes as roofline.traffic (null when the sources have changed since) and the stamp as
+    # roofline.traffic_from. Every cache byte is read once: within 1 %.
+    text = bench.TRAFFIC_FILES[kv_dtype].read_text()
+    raw = int(text.split("traffic_bytes_per_launch:")[1].split()[0])
+    assert abs(raw / algorithmic - 1.0) < 0.01, raw
+    t, stamp = bench.read_traffic(kv_dtype)
+    assert stamp["commit"] and len(stamp["kernel_source_digest"]) == 16
+    assert stamp["current_digest"] == bench.kernel_source_digest()
+    assert t == (raw if stamp["matches_build"] else None)
+
+
+def test_traffic_from_other_kernel_sources_is_not_reported(tmp_path, monkeypatch):
+    prof = tmp_path / "traffic.md"
+    monkeypatch.setitem(bench.TRAFFIC_FILES, "same", prof)
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    body = "traffic_bytes_per_launch: 1075613696\nmeasured_at_commit: 0123abcd\n"
+    prof.write_text(body + f"kernel_source_digest: {bench.kernel_source_digest()}\n")
+    t, stamp = bench.read_traffic("same")
+    assert t == 1075613696 and stamp["matches_build"] and stamp["commit"] == "0123abcd"
+    prof.write_text(body + "kernel_source_digest: 0000000000000000\n")
+    t, stamp = bench.read_traffic("same")
+    assert t is None and not stamp["matches_build"]
+    prof.write_text(body)                                 # no digest recorded: not trusted
+    assert bench.read_traffic("same")[0] is None
+
+
+def test_kernel_source_digest_follows_every_library_source(tmp_path, monkeypatch):
+    src = tmp_path / "csrc"
+    src.mkdir()
+    (src / "a.h").write_text("x")
+    (src / "b.hip").write_text("y")
+    (src / "notes.txt").write_text("not a source")
+    monkeypatch.setattr(bench, "KERNEL_SOURCES", src)
+    d0 = bench.kernel_source_digest()
+    (src / "notes.txt").write_text("changed")
+    assert bench.kernel_source_digest() == d0
+    (src / "b.hip").write_text("y2")
+    assert bench.kernel_source_digest() != d0
+    (src / "b.hip").write_text("y")
+    (src / "c.cpp").write_text("")
+    assert bench.kernel_source_digest() != d0
+
+
+def test_single_call_checks_and_graph_mode_combinations_are_refused():
+    assert bench.parse_args(["--single-call", "--no-check"]).no_check
+    assert bench.parse_args(["--graph", "--graph-point", "C2 B=1"]).graph
+    for argv, needle in ((["--no-check"], "--no-check"),
+                         (["--graph", "--config", "5"], "--graph"),
+                         (["--graph", "--single-call"], "--graph")):
+        r = subprocess.run([sys.executable, str(ROOT / "bench.py"), *argv],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 2 and needle in r.stderr and r.stdout == ""
+
+
+def test_graph_points_cover_the_latency_bound_configs():
+    # config 1 at its stated split and automatic, config 2 at B=1 and B=4, config 5's
+    # 16-layer step; every point's N caches together exceed 1 GiB
+    import torch
+
+    import layout
+    labels = [p[0] for p in bench.GRAPH_POINTS]
+    assert labels == ["C1", "C1 auto", "C2 B=1", "C2 B=4", "C5 step"]
+    (c5,) = [p for p in bench.GRAPH_POINTS if p[1] == 5]
+    assert c5[4] == 16 and c5[2]["d"] == 64 and c5[2]["dtype"] == "bf16"
+    for label, cid, shape, split, layers in bench.GRAPH_POINTS:
+        bytes_ = layout.attention_bytes(shape["batch"], [shape["ctx"]] * shape["batch"], 32, 8,
+                                        shape.get("d", 128))
+        n = layers or max(16, -(-bench.GRAPH_MIN_BYTES // bytes_))
+        assert n * bytes_ >= bench.GRAPH_MIN_BYTES, label
+    del torch
+
+
+def test_roctx_ranges_are_off_without_dk_trace(monkeypatch):
+    monkeypatch.delenv("DK_TRACE", raising=False)
+    assert bench.roctx_ranges() is None
+    monkeypatch.setenv("DK_TRACE", "0")
+    assert bench.roctx_ranges() is None
 
 
 def test_config_sweeps_follow_baseline_json():
