@@ -1167,35 +1167,49 @@ __device__ __forceinline__ void stream_lds(W& wv, uint8_t* ring, int n, PageFn p
   wait_vmem<0>();
 }
 
-// Whether a kernel streams its pages through LDS (stream_lds), on the VALU q.k path:
-// 16-bit caches at D = 256 (512-byte rows) with at most 2 wavefronts per workgroup (LDS:
-// 64 KB each), and, with DK_LDS_NARROW, rows of at most 128 bytes (16-bit D = 64, fp8
-// D <= 128: 16-byte lane loads instead of 8 or 4) with at most 4 wavefronts.
-// (a build may set another depth with DK_LDS_DEPTH / DK_LDS_DEPTH_NARROW; 2 measured the
-// same as 3 at D=256)
+// Whether a kernel streams its pages through LDS (stream_lds), on the VALU q.k path (GROUPED:
+// a balanced kernel serving several kv heads per workgroup; NW: the workgroup's wavefronts):
+//  * 16-bit caches at D = 256 (512-byte rows), at most 2 wavefronts per workgroup (64 KB of
+//    ring each);
+//  * fp8 caches at D = 64 (64-byte rows) in the grouped balanced kernels: 16-byte lane loads
+//    (16 rows per instruction) instead of 4-byte ones, 2 pages in flight, the workgroup's
+//    rings within DK_LDS_NARROW_BUDGET bytes (against the register ring, us: ragged B=128
+//    ctx U[128, 8192] 129.4 -> 123.1, B=32 ctx 2048 28.0 -> 26.9, ctx 8192 63.8 -> 63.3;
+//    depth 1, 3, 5 and 7 measured slower than 2, and the one-pass kernels over short
+//    sequences 3 % slower with the ring).
+// Build switches for comparisons (all measured slower): DK_LDS_NARROW=0 turns the fp8 D = 64
+// case off, DK_LDS_NARROW=2 extends it to every row of at most 128 bytes (16-bit D = 64,
+// fp8 D = 128) in any kernel, DK_LDS_256=1 to 256-byte rows (16-bit D = 128, fp8 D = 256);
+// DK_LDS_DEPTH / DK_LDS_DEPTH_NARROW set the pages in flight (at D = 256, 2 measured the
+// same as 3).
 #ifndef DK_LDS_DEPTH
 #define DK_LDS_DEPTH 3
 #endif
 #ifndef DK_LDS_DEPTH_NARROW
-#define DK_LDS_DEPTH_NARROW 3
+#define DK_LDS_DEPTH_NARROW 2
 #endif
 #ifndef DK_LDS_NARROW
-#define DK_LDS_NARROW 0
+#define DK_LDS_NARROW 1
 #endif
 #ifndef DK_LDS_256
 #define DK_LDS_256 0
+#endif
+#ifndef DK_LDS_NARROW_BUDGET
+#define DK_LDS_NARROW_BUDGET 65536
 #endif
 template <int D, bool KV8>
 constexpr int lds_depth() {
   return D * (KV8 ? 1 : 2) <= kNarrowRowBytes ? DK_LDS_DEPTH_NARROW : DK_LDS_DEPTH;
 }
-template <int D, bool KV8, bool MFMA, int NW>
+template <int D, bool KV8, bool MFMA, int NW, bool GROUPED = false>
 constexpr bool lds_pages() {
   constexpr int rb = D * (KV8 ? 1 : 2);
   if (!DK_LDS_PAGES || MFMA) return false;
   if (rb == 512) return !KV8 && NW <= 2;
   if (rb == 256) return DK_LDS_256 && NW <= 2;
-  return DK_LDS_NARROW && rb <= kNarrowRowBytes && NW <= 4;
+  if (rb > kNarrowRowBytes) return false;
+  const bool on = DK_LDS_NARROW >= 2 || (DK_LDS_NARROW == 1 && rb == 64 && GROUPED);
+  return on && NW * (lds_depth<D, KV8>() + 1) * 2 * kPage * rb <= DK_LDS_NARROW_BUDGET;
 }
 
 // ---------------------------------------------------------------- workgroup combine
@@ -1471,7 +1485,7 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   using WV = Wave<T, D, G, MFMA, KV8>;
   __shared__ CombineSmem<G, D, (NW > 1 ? NW : 1)> smh[HP];
   __shared__ __attribute__((aligned(16))) uint8_t kst[WV::STAGE ? HP * NW * WV::STAGE_BYTES : 16];
-  constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW * HP>();
+  constexpr bool LDSP = lds_pages<D, KV8, MFMA, NW * HP, (HP > 1)>();
   constexpr int RING = (lds_depth<D, KV8>() + 1) * WV::LDS_PAGE;
   __shared__ __attribute__((aligned(16))) uint8_t ring[LDSP ? HP * NW * RING : 16];
   WV wv;
