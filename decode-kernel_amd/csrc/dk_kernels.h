@@ -1197,6 +1197,9 @@ __device__ __forceinline__ void stream_lds(W& wv, uint8_t* ring, int n, PageFn p
 #ifndef DK_LDS_NARROW_BUDGET
 #define DK_LDS_NARROW_BUDGET 65536
 #endif
+#ifndef DK_LDS_GROUPED_ROW          // grouped kernels: the ring over rows of at most this
+#define DK_LDS_GROUPED_ROW 64       // many bytes
+#endif
 template <int D, bool KV8>
 constexpr int lds_depth() {
   return D * (KV8 ? 1 : 2) <= kNarrowRowBytes ? DK_LDS_DEPTH_NARROW : DK_LDS_DEPTH;
@@ -1208,7 +1211,7 @@ constexpr bool lds_pages() {
   if (rb == 512) return !KV8 && NW <= 2;
   if (rb == 256) return DK_LDS_256 && NW <= 2;
   if (rb > kNarrowRowBytes) return false;
-  const bool on = DK_LDS_NARROW >= 2 || (DK_LDS_NARROW == 1 && rb == 64 && GROUPED);
+  const bool on = DK_LDS_NARROW >= 2 || (DK_LDS_NARROW == 1 && GROUPED && rb <= DK_LDS_GROUPED_ROW);
   return on && NW * (lds_depth<D, KV8>() + 1) * 2 * kPage * rb <= DK_LDS_NARROW_BUDGET;
 }
 

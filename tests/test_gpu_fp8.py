@@ -125,6 +125,7 @@ CASES = [
     (3, [513, 1, 64], 16, 4, 64, torch.bfloat16, "freelist"),     # 64-byte rows
     (3, [400, 9, 130], 24, 6, 128, torch.float16, "freelist"),    # 3 groups of 2 kv heads
     (2, [333, 65], 48, 12, 128, torch.bfloat16, "permuted"),      # 3 groups of 4 kv heads
+    (4, [200, 0, 95, 31], 12, 6, 64, torch.float16, "freelist"),  # 64-byte rows, 3 groups of 2
 ]
 
 
@@ -271,16 +272,17 @@ def test_fp8_partials_match_oracle():
         check_partials(po, pm, pl, O, m, l, q.dtype)
 
 
-@pytest.mark.parametrize("batch", [65, 2000])
-def test_ragged_fp8_charged_range_split_matches_oracle(batch):
+@pytest.mark.parametrize("batch,d", [(65, 128), (2000, 128), (65, 64), (2000, 64)])
+def test_ragged_fp8_charged_range_split_matches_oracle(batch, d):
     # a ragged batch over an fp8 cache with the plan hint: the balanced schedule groups
-    # kv heads (128-byte rows) and charges each sequence start in its range split
+    # kv heads (rows of 128 bytes, or 64 read through the LDS page ring) and charges each
+    # sequence start in its range split
     rng = np.random.default_rng(batch + 3)
     hi = 40 if batch > 100 else 2500
     lens = [int(x) for x in rng.integers(0, hi, size=batch)]
     lens[-1] = 3 * hi
     q, kv, indptr, ids, last, _ = layout.synthesize_paged(
-        batch, lens, 32, 8, 128, device=DEV, page_table="permuted", seed=batch)
+        batch, lens, 32, 8, d, device=DEV, page_table="permuted", seed=batch)
     codes = _quantize(kv, 0.5, 0.25)
     deq = _dequantize(codes, 0.5, 0.25)
     rows = list(range(0, batch, max(batch // 50, 1))) + [batch - 1]
@@ -288,7 +290,7 @@ def test_ragged_fp8_charged_range_split_matches_oracle(batch):
                                          to_np(ids), to_np(last), batch_subset=rows)
     kv8 = _codes_to_device(codes)
     hint = attention.plan_hint(indptr.cpu())
-    _announce(f"fp8 ragged charged split batch={batch}")
+    _announce(f"fp8 ragged charged split batch={batch} d={d}")
     out = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=0, schedule=1,
                                      max_pages_per_seq=hint, k_scale=0.5, v_scale=0.25)
     ref_out = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=0, schedule=1,
