@@ -811,6 +811,7 @@ GRAPH_POINTS = [
     ("C1 auto", 1, dict(CONFIGS[1][0]), 0, 0),
     ("C2 B=1", 2, dict(batch=1, ctx=4096, dtype="fp16", table="permuted"), 0, 0),
     ("C2 B=4", 2, dict(batch=4, ctx=4096, dtype="fp16", table="permuted"), 0, 0),
+    ("C3 B=1 ctx 32768", 3, dict(batch=1, ctx=32768, dtype="bf16", table="permuted"), 0, 0),
     ("C5 step", 5, dict(CONFIGS[5][0]), 0, 16),     # the 16 attention layers of the step
 ]
 GRAPH_MIN_BYTES = 1 << 30      # the N caches of a point together: > L2 + Infinity Cache

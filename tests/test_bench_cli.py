@@ -88,13 +88,14 @@ def test_single_call_checks_and_graph_mode_combinations_are_refused():
 
 
 def test_graph_points_cover_the_latency_bound_configs():
-    # config 1 at its stated split and automatic, config 2 at B=1 and B=4, config 5's
-    # 16-layer step; every point's N caches together exceed 1 GiB
+    # config 1 at its stated split and automatic, config 2 at B=1 and B=4, config 3's
+    # shortest single sequence, config 5's 16-layer step; every point's N caches together
+    # exceed 1 GiB
     import torch
 
     import layout
     labels = [p[0] for p in bench.GRAPH_POINTS]
-    assert labels == ["C1", "C1 auto", "C2 B=1", "C2 B=4", "C5 step"]
+    assert labels == ["C1", "C1 auto", "C2 B=1", "C2 B=4", "C3 B=1 ctx 32768", "C5 step"]
     (c5,) = [p for p in bench.GRAPH_POINTS if p[1] == 5]
     assert c5[4] == 16 and c5[2]["d"] == 64 and c5[2]["dtype"] == "bf16"
     for label, cid, shape, split, layers in bench.GRAPH_POINTS:
