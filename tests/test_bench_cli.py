@@ -203,3 +203,16 @@ def test_default_line_carries_every_baseline_config():
         wl = bench.config_workload(torch, layout, "cpu", small, "same")
         assert wl.d == shape.get("d", 128) and wl.dtype_name == shape["dtype"]
         assert bench.oracle_sequences(wl) == [0, 1]
+
+
+def test_timing_events_skip_the_system_fence():
+    # the timed regions' events are created with hipEventDisableSystemFence, whose value is
+    # the HIP header's; earlier lines' default-flag events stay available for comparison
+    import re
+    header = Path("/opt/rocm/include/hip/hip_runtime_api.h")
+    if header.exists():
+        m = re.search(r"#define\s+hipEventDisableSystemFence\s+(0x[0-9a-fA-F]+)", header.read_text())
+        assert m and int(m.group(1), 16) == bench.HIP_EVENT_DISABLE_SYSTEM_FENCE
+    assert bench.HipEvents.__init__.__defaults__ == (bench.HIP_EVENT_DISABLE_SYSTEM_FENCE,)
+    import inspect
+    assert inspect.signature(bench.Timer).parameters["events"].default == "nofence"
