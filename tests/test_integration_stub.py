@@ -1,5 +1,6 @@
 """The reference-side binding a maintainer would paste into src/attention.py (the fenced
-Python block of INTEGRATION.md, "Binding from the reference's Python"), run as written:
+Python block under "Binding from the reference's Python" in the repository's integration
+guide), run as written:
 a bare ctypes stub over the plain dk_decode_attention entry point, which takes no
 options (split_kv 0 is the balanced schedule without a plan hint).
 
@@ -22,12 +23,13 @@ from helpers import err_stats, to_np
 from oracle import reference as ref
 
 ROOT = Path(__file__).resolve().parent.parent
+GUIDE = ROOT / "INTEGRATION.md"     # the integration guide holding the binding stub
 DEV = "cuda"
 
 
 def _stub_source() -> str:
-    """The first fenced Python block after the binding heading of INTEGRATION.md."""
-    text = (ROOT / "INTEGRATION.md").read_text()
+    """The first fenced Python block after the guide's binding heading."""
+    text = GUIDE.read_text()
     at = text.index("## Binding from the reference's Python")
     m = re.search(r"```python\n(.*?)```", text[at:], re.S)
     assert m, "no python block under the binding heading"
@@ -37,7 +39,7 @@ def _stub_source() -> str:
 def _load_stub():
     src = _stub_source().replace("/path/to/libdk_decode.so", str(dk_lib.LIB_PATH))
     ns = {}
-    exec(compile(src, "INTEGRATION.md", "exec"), ns)
+    exec(compile(src, GUIDE.name, "exec"), ns)
     return ns
 
 
@@ -77,7 +79,7 @@ def test_stub_against_oracle(config):
     want = ref.reference_attention_paged(to_np(q), to_np(kv), to_np(indptr), to_np(ids),
                                          to_np(last))
     for split in (1, 4, 0):
-        print(f"[case] INTEGRATION.md stub {config} split_kv={split}", flush=True)
+        print(f"[case] integration stub {config} split_kv={split}", flush=True)
         out = ns["decode_attention"](q, kv, indptr, ids, last, split_kv=split)
         torch.cuda.synchronize()
         mx, mean = err_stats(out, want)
