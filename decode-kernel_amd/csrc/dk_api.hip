@@ -181,6 +181,12 @@ int64_t balanced_groups(const Problem& p, const Plan& pl, int cus, int hp = 1) {
 // Whether one workgroup per (sequence, head chunk) with pl's wavefronts per workgroup fits
 // in the balanced grid of the same shape, and no sequence (plan hint) is longer than a
 // balanced workgroup's share of pages: then one pass finishes no later and needs no merge.
+// The plan hint shows near-uniform lengths: the longest sequence (hint pages) within 1/32 of
+// the mean (num_indices / batch). 128-bit products: the hint is the caller's.
+bool near_uniform(const Problem& p, int64_t hint) {
+  return (__int128)hint * p.batch * 32 <= (__int128)p.num_indices * 33;
+}
+
 bool one_pass_fits(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t groups = balanced_groups(p, pl, cus);
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
@@ -211,7 +217,7 @@ bool one_pass_fits(const Problem& p, const Plan& pl, int cus, int64_t hint) {
 bool short_uniform_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   return hint <= kShortOnePassPages && 4 * pairs >= cus && pairs <= cus &&
-         hint * p.batch * 32 <= p.num_indices * 33;
+         near_uniform(p, hint);
 }
 
 // The same over an fp8 cache at D = 128 (128-byte rows), at any pair count from CUs/4 up:
@@ -226,7 +232,7 @@ bool short_uniform_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint
 // (B=256 105.8 vs 109.2 / 119.9).
 int short_uniform_fp8_waves(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
-  if (hint > kShortOnePassPages || 4 * pairs < cus || hint * p.batch * 32 > p.num_indices * 33)
+  if (hint > kShortOnePassPages || 4 * pairs < cus || !near_uniform(p, hint))
     return 0;
   return pairs < 8 * (int64_t)cus ? 4 : 1;
 }
@@ -242,14 +248,14 @@ int short_uniform_fp8_waves(const Problem& p, const Plan& pl, int cus, int64_t h
 bool short_uniform_d64(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   return hint <= kShortOnePassPages && 4 * pairs >= cus && pairs <= 2 * (int64_t)cus &&
-         hint * p.batch * 32 <= p.num_indices * 33;
+         near_uniform(p, hint);
 }
 
 bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint) {
   const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
   const int64_t unit = (int64_t)kOnePassPairsPerCU * cus;
   return unit > 0 && pairs >= unit && pairs % unit == 0 &&
-         hint * p.batch * 32 <= p.num_indices * 33;
+         near_uniform(p, hint);
 }
 
 // Wavefronts per workgroup of the one-pass kernel that split_kv == 0 runs, or 0 for the
@@ -577,7 +583,8 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, in
   dk::clear_error();
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
       (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
-      (dtype != DK_F16 && dtype != DK_BF16) || avg_pages_per_seq < 0)
+      (dtype != DK_F16 && dtype != DK_BF16) || avg_pages_per_seq < 0 ||
+      avg_pages_per_seq > INT32_MAX || (int64_t)batch * num_q_heads > dk::kMaxRows)
     return dk::set_error(DK_EINVAL, "dk_choose_split: bad argument");
   Problem p;
   p.batch = batch;
@@ -598,7 +605,8 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, i
   dk::clear_error();
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
       (head_dim != 64 && head_dim != 128 && head_dim != 256) || split_kv < 0 ||
-      split_kv > 4096 || num_indices < 0 || (dtype != DK_F16 && dtype != DK_BF16))
+      split_kv > dk::kMaxSplit || num_indices < 0 || (dtype != DK_F16 && dtype != DK_BF16) ||
+      (int64_t)batch * num_q_heads > dk::kMaxRows)
     return dk::set_error(DK_EINVAL, "dk_plan_schedule: bad argument");
   if (split_kv != 0) return split_kv;
   Problem p;
@@ -722,7 +730,7 @@ int dk_merge_partials(const void* workspace, size_t workspace_bytes, void* out, 
                       int32_t num_q_heads, int32_t head_dim, int32_t dtype, int64_t o_b,
                       int64_t o_h, int32_t split_kv, void* hip_stream) {
   dk::clear_error();
-  if (batch < 0 || num_q_heads <= 0 || split_kv < 1 || split_kv > 4096 ||
+  if (batch < 0 || num_q_heads <= 0 || split_kv < 1 || split_kv > dk::kMaxSplit ||
       (head_dim != 64 && head_dim != 128 && head_dim != 256) ||
       (dtype != DK_F16 && dtype != DK_BF16) || o_b < 0 || o_h < 0)
     return dk::set_error(DK_EINVAL, "dk_merge_partials: bad argument");
@@ -731,8 +739,12 @@ int dk_merge_partials(const void* workspace, size_t workspace_bytes, void* out, 
   // the partials are read as float vectors from 256-byte aligned arrays
   if (((uintptr_t)workspace % 256) != 0)
     return dk::set_error(DK_EWORKSPACE, "workspace must be 256-byte aligned");
-  if ((int64_t)batch * num_q_heads > INT32_MAX / 4)
+  if ((int64_t)batch * num_q_heads > dk::kMaxRows)
     return dk::set_error(DK_EINVAL, "dk_merge_partials: batch*num_q_heads too large");
+  if (!dk::extent_ok(batch, o_b, num_q_heads, o_h, head_dim, 2))
+    return dk::set_error(DK_EUNSUPPORTED,
+                         "dk_merge_partials: out strides must be below 2^40 elements and span "
+                         "less than 2^62 bytes");
   size_t off_o, off_m, off_l, need;
   dk::partials_layout_rows(dk::split_rows(batch, num_q_heads, split_kv), head_dim, &off_o,
                            &off_m, &off_l, &need);

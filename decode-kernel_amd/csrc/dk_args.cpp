@@ -64,6 +64,14 @@ HeadChunks head_chunks(int group, int head_dim, bool mfma) {
   return h;
 }
 
+bool extent_ok(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t last, int64_t esize) {
+  // 128-bit products, so that no stride can wrap the bound
+  if (s0 < 0 || s1 < 0 || s0 >= kMaxStride || s1 >= kMaxStride) return false;
+  const __int128 ext = ((__int128)std::max<int64_t>(n0, 1) - 1) * s0 +
+                       ((__int128)std::max<int64_t>(n1, 1) - 1) * s1 + last;
+  return ext * esize < ((__int128)1 << 62);
+}
+
 void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,
                           size_t* off_l, size_t* total) {
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -93,7 +101,9 @@ int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim) 
 }
 
 size_t workspace_bytes(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim, int32_t split) {
-  if (!valid_shape(batch, hq, hkv, head_dim) || split < 0 || batch == 0 || split == 1) return 0;
+  if (!valid_shape(batch, hq, hkv, head_dim) || split < 0 || split > kMaxSplit || batch == 0 ||
+      split == 1 || (int64_t)batch * hq > kMaxRows)
+    return 0;
   const int64_t rows = split == 0 ? balanced_rows(batch, hq, hkv, head_dim)
                                   : split_rows(batch, hq, split);
   size_t o, m, l, total;
@@ -156,7 +166,8 @@ int validate(const Problem& p) {
   if (p.dtype != DK_F16 && p.dtype != DK_BF16)
     return set_error(DK_EINVAL, "dtype must be DK_F16 (0) or DK_BF16 (1); got %d", p.dtype);
   if (p.split < 0) return set_error(DK_EINVAL, "split_kv must be >= 0; got %d", p.split);
-  if (p.split > 4096) return set_error(DK_EINVAL, "split_kv must be <= 4096; got %d", p.split);
+  if (p.split > kMaxSplit)
+    return set_error(DK_EINVAL, "split_kv must be <= %d; got %d", kMaxSplit, p.split);
   if (p.num_indices < 0 || p.num_indices > INT32_MAX)
     return set_error(DK_EINVAL, "num_indices must be in [0, 2^31); got %lld",
                      (long long)p.num_indices);
@@ -216,6 +227,20 @@ int validate(const Problem& p) {
   const int64_t all[] = {s.q_b, s.q_h, s.kv_p, kv_r, s.kv_s, s.kv_h, s.o_b, s.o_h};
   for (int64_t v : all)
     if (v < 0) return set_error(DK_EINVAL, "strides must be non-negative");
+  // Every byte offset formed from the strides (here, in the launch arguments and in the
+  // kernels) must fit int64: strides below kMaxStride elements, and the last element of q,
+  // out and the page pool below 2^62 bytes, bounded in 128-bit arithmetic.
+  for (int64_t v : all)
+    if (v >= kMaxStride)
+      return set_error(DK_EUNSUPPORTED, "strides must be below 2^40 elements; got %lld",
+                       (long long)v);
+  const __int128 pool = ((__int128)std::max<int64_t>(p.num_pages, 1) - 1) * s.kv_p + kv_r +
+                        (__int128)(kPageSize - 1) * s.kv_s + (__int128)(p.hkv - 1) * s.kv_h +
+                        p.head_dim;
+  if (!extent_ok(p.batch, s.q_b, p.hq, s.q_h, p.head_dim, 2) ||
+      (p.need_out && !extent_ok(p.batch, s.o_b, p.hq, s.o_h, p.head_dim, 2)) ||
+      pool * p.kv_esize() >= ((__int128)1 << 62))
+    return set_error(DK_EUNSUPPORTED, "q, out or kv_data spans 2^62 bytes or more");
   const int64_t esize = p.kv_esize();
   auto aligned16 = [](int64_t elems, int64_t es) { return (elems * es) % 16 == 0; };
   if (!aligned16(s.q_b, 2) || !aligned16(s.q_h, 2) || !aligned16(s.kv_p, esize) ||
@@ -232,12 +257,13 @@ int validate(const Problem& p) {
   if (in_page >= ((int64_t)1 << 31))
     return set_error(DK_EUNSUPPORTED, "kv_data page extent exceeds 2 GiB");
 
+  // bounds the products below (grid, partial rows) well inside int64
+  if ((int64_t)p.batch * p.hq > kMaxRows)
+    return set_error(DK_EINVAL, "batch*num_q_heads too large");
   const Plan plan = make_plan(p);
   if (plan.grid > INT32_MAX)
     return set_error(DK_EINVAL, "grid too large: batch*kv_heads*split = %lld workgroups",
                      (long long)plan.grid);
-  if ((int64_t)p.batch * p.hq > INT32_MAX / 4)
-    return set_error(DK_EINVAL, "batch*num_q_heads too large");
   // Two passes and the pass-1-only entry point write fp32 partials.
   if (p.split != 1 || !p.need_out) {
     size_t req, o, m, l;

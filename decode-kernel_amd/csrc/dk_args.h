@@ -12,6 +12,9 @@ namespace dk {
 
 constexpr int kPageSize = 16;        // tokens per page (reference: PAGE_SIZE=16, attention_ext.cu:509)
 constexpr int kMaxWaves = 2048;      // upper bound on the balanced pass-1 grid (wavefronts)
+constexpr int64_t kMaxStride = (int64_t)1 << 40;   // element strides accepted (exclusive)
+constexpr int kMaxSplit = 4096;                      // split_kv accepted (inclusive)
+constexpr int64_t kMaxRows = INT32_MAX / 4;          // batch * num_q_heads accepted
 constexpr int kXcds = 8;             // MI355X: the dispatcher deals workgroups to 8 XCDs in turn
 constexpr int kDefaultWavesPerCU = 2;
 constexpr int kDefaultWavesPerGroup = 2;
@@ -143,6 +146,9 @@ void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t*
 // Rows of partials each mode writes: explicit split S -> batch*hq*S; balanced ->
 // (max(kMaxWaves, pairs_per_seq) + batch*pairs_per_seq) * heads.
 int64_t split_rows(int32_t batch, int32_t hq, int32_t split);
+// Whether the last element of an array of n0 x n1 rows (strides s0, s1 elements, `last`
+// elements in the final row) lies below 2^62 bytes, the strides below kMaxStride.
+bool extent_ok(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t last, int64_t esize);
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim);
 // Workspace of dk_decode_attention: split 1 -> 0, split > 1 -> explicit partials,
 // split 0 -> balanced partials. 0 on invalid shapes.

@@ -127,6 +127,19 @@ def _call(lib, **kw):
     (dict(opts=dk_lib.options(kv_dtype=dk_lib.DK_KV_FP8_E4M3),
           strides=dk_lib.DkStrides(32 * 128, 128, 2 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128 + 8,
                                    128, 32 * 128, 128)), dk_lib.DK_EUNSUPPORTED, "strides"),
+    # strides whose byte products would wrap int64: refused, not wrapped past the checks
+    (dict(strides=dk_lib.DkStrides(32 * 128, 128, 2 * 16 * 8 * 128, 16 * 8 * 128, 1 << 62,
+                                   128, 32 * 128, 128)), dk_lib.DK_EUNSUPPORTED, "2^40"),
+    (dict(strides=dk_lib.DkStrides(1 << 40, 128, 2 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128,
+                                   128, 32 * 128, 128)), dk_lib.DK_EUNSUPPORTED, "2^40"),
+    # each stride in range, but the pool they address spans more than 2^62 bytes
+    (dict(num_pages=1 << 31, strides=dk_lib.DkStrides(32 * 128, 128, (1 << 40) - 8,
+                                                      16 * 8 * 128, 8 * 128, 128, 32 * 128,
+                                                      128)), dk_lib.DK_EUNSUPPORTED, "2^62"),
+    (dict(batch=1 << 24, hq=32, strides=dk_lib.DkStrides((1 << 40) - 8, 128,
+                                                         2 * 16 * 8 * 128, 16 * 8 * 128,
+                                                         8 * 128, 128, 32 * 128, 128)),
+     dk_lib.DK_EUNSUPPORTED, "2^62"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(kw, code, needle):
     lib = dk_lib.load()
@@ -267,3 +280,13 @@ def test_python_merge_partials_refuses_cpu_partials_and_bad_shapes():
         attention.merge_partials(po, pm[:, :3], pl)
     with pytest.raises(dk_lib.DecodeArgumentError, match=r"\(B, Hq, S, D\)"):
         attention.merge_partials(po[0], pm, pl)
+
+
+def test_merge_partials_refuses_out_strides_that_would_wrap():
+    lib = dk_lib.load()
+    rc = lib.dk_merge_partials(0x70000, 1 << 30, 0x60000, 2, 32, 128, dk_lib.DK_F16,
+                               1 << 62, 128, 4, None)
+    assert rc == dk_lib.DK_EUNSUPPORTED and "2^40" in lib.dk_last_error().decode()
+    rc = lib.dk_merge_partials(0x70000, 1 << 30, 0x60000, 1 << 22, 32, 128, dk_lib.DK_F16,
+                               (1 << 40) - 8, 128, 1, None)
+    assert rc == dk_lib.DK_EUNSUPPORTED and "2^62" in lib.dk_last_error().decode()
