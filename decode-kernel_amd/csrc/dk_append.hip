@@ -178,6 +178,14 @@ static int append_impl(void* q, const void* k_new, const void* v_new, int64_t ne
   if (new_b < 0 || new_h < 0 || s.q_b < 0 || s.q_h < 0 || s.kv_p < 0 || s.kv_s < 0 ||
       s.kv_h < 0 || (!v_cache && s.kv_r < 0))
     return dk::set_error(DK_EINVAL, "strides must be non-negative");
+  // every byte offset formed from the strides must fit int64 (bounded in 128-bit arithmetic)
+  const int64_t kes_ = kv8 ? 1 : 2;
+  if (!dk::extent_ok(batch, s.q_b, num_q_heads, s.q_h, head_dim, 2) ||
+      !dk::extent_ok(batch, new_b, num_kv_heads, new_h, head_dim, 2) ||
+      !dk::pool_ok(num_pages, s, v_cache ? 0 : s.kv_r, num_kv_heads, head_dim, kes_))
+    return dk::set_error(DK_EUNSUPPORTED,
+                         "strides must be below 2^40 elements and q, the new rows and the cache "
+                         "must span less than 2^62 bytes");
   if (batch == 0) return DK_OK;
   if (!k_new || !v_new || !k_cache || !kv_indptr || !kv_last_page_len ||
       (num_indices > 0 && !kv_indices))

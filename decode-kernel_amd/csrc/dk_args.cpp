@@ -72,6 +72,17 @@ bool extent_ok(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t last, int
   return ext * esize < ((__int128)1 << 62);
 }
 
+bool pool_ok(int64_t num_pages, const dk_strides& s, int64_t kv_r, int32_t hkv, int32_t head_dim,
+             int64_t esize) {
+  const int64_t st[] = {s.kv_p, kv_r, s.kv_s, s.kv_h};
+  for (int64_t v : st)
+    if (v < 0 || v >= kMaxStride) return false;
+  const __int128 last = ((__int128)std::max<int64_t>(num_pages, 1) - 1) * s.kv_p + kv_r +
+                        (__int128)(kPageSize - 1) * s.kv_s + (__int128)(hkv - 1) * s.kv_h +
+                        head_dim;
+  return last * esize < ((__int128)1 << 62);
+}
+
 void partials_layout_rows(int64_t rows, int32_t head_dim, size_t* off_o, size_t* off_m,
                           size_t* off_l, size_t* total) {
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -234,12 +245,9 @@ int validate(const Problem& p) {
     if (v >= kMaxStride)
       return set_error(DK_EUNSUPPORTED, "strides must be below 2^40 elements; got %lld",
                        (long long)v);
-  const __int128 pool = ((__int128)std::max<int64_t>(p.num_pages, 1) - 1) * s.kv_p + kv_r +
-                        (__int128)(kPageSize - 1) * s.kv_s + (__int128)(p.hkv - 1) * s.kv_h +
-                        p.head_dim;
   if (!extent_ok(p.batch, s.q_b, p.hq, s.q_h, p.head_dim, 2) ||
       (p.need_out && !extent_ok(p.batch, s.o_b, p.hq, s.o_h, p.head_dim, 2)) ||
-      pool * p.kv_esize() >= ((__int128)1 << 62))
+      !pool_ok(p.num_pages, s, kv_r, p.hkv, p.head_dim, p.kv_esize()))
     return set_error(DK_EUNSUPPORTED, "q, out or kv_data spans 2^62 bytes or more");
   const int64_t esize = p.kv_esize();
   auto aligned16 = [](int64_t elems, int64_t es) { return (elems * es) % 16 == 0; };

@@ -149,6 +149,11 @@ int64_t split_rows(int32_t batch, int32_t hq, int32_t split);
 // Whether the last element of an array of n0 x n1 rows (strides s0, s1 elements, `last`
 // elements in the final row) lies below 2^62 bytes, the strides below kMaxStride.
 bool extent_ok(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t last, int64_t esize);
+// The same for a page pool: the last element of its last page (num_pages pages kv_p apart,
+// V kv_r after K, 16 token rows kv_s apart, hkv heads kv_h apart, head_dim elements) below
+// 2^62 bytes, every stride below kMaxStride.
+bool pool_ok(int64_t num_pages, const dk_strides& s, int64_t kv_r, int32_t hkv, int32_t head_dim,
+             int64_t esize);
 int64_t balanced_rows(int32_t batch, int32_t hq, int32_t hkv, int32_t head_dim);
 // Workspace of dk_decode_attention: split 1 -> 0, split > 1 -> explicit partials,
 // split 0 -> balanced partials. 0 on invalid shapes.

@@ -163,6 +163,8 @@ extern "C" int dk_expand_page_table(const int32_t* kv_indptr, const int32_t* kv_
                          "different pages would share ids", pages_mult, sub);
   if (num_indices > INT32_MAX)
     return dk::set_error(DK_EINVAL, "num_indices must be < 2^31");
+  if (num_pages > INT32_MAX)
+    return dk::set_error(DK_EINVAL, "num_pages must be < 2^31 (page ids are int32)");
   // the rewritten table's offsets (at most num_indices * sub entries) are int32
   if (num_indices * (int64_t)sub > (int64_t)INT32_MAX)
     return dk::set_error(DK_EINVAL, "num_indices * page_size / 16 sub-pages exceed 2^31");
@@ -193,6 +195,10 @@ extern "C" int dk_build_page_table(const int32_t* req_to_token, int64_t req_stri
   dk::clear_error();
   if (batch < 0 || req_stride < 0 || capacity < 0)
     return dk::set_error(DK_EINVAL, "dk_build_page_table: negative batch, stride or capacity");
+  // row offsets req_pool_indices[b] * req_stride (int32 index) must fit int64
+  if (req_stride >= dk::kMaxStride)
+    return dk::set_error(DK_EUNSUPPORTED, "req_stride must be below 2^40 elements; got %lld",
+                         (long long)req_stride);
   if (page_size != dk::kPageSize)
     return dk::set_error(DK_EINVAL, "page_size must be 16; got %d", page_size);
   if (batch == 0) return DK_OK;

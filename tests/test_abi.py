@@ -290,3 +290,23 @@ def test_merge_partials_refuses_out_strides_that_would_wrap():
     rc = lib.dk_merge_partials(0x70000, 1 << 30, 0x60000, 1 << 22, 32, 128, dk_lib.DK_F16,
                                (1 << 40) - 8, 128, 1, None)
     assert rc == dk_lib.DK_EUNSUPPORTED and "2^62" in lib.dk_last_error().decode()
+
+
+def test_build_page_table_refuses_a_stride_that_would_wrap():
+    lib = dk_lib.load()
+    fake = ctypes.c_void_p(256)
+    rc = lib.dk_build_page_table(fake, 1 << 62, fake, fake, 2, 16, fake, fake, 64, fake, None)
+    assert rc == dk_lib.DK_EUNSUPPORTED and "req_stride" in lib.dk_last_error().decode()
+
+
+@pytest.mark.parametrize("q_b,kv_p,num_pages", [(1 << 62, 8192, 64), (4096, 1 << 45, 64),
+                                                 (4096, (1 << 40) - 8, 1 << 31)])
+def test_append_refuses_strides_that_would_wrap(q_b, kv_p, num_pages):
+    # the checks come before any pointer is used; every call is refused on the host
+    lib = dk_lib.load()
+    fake = ctypes.c_void_p(256)
+    st = dk_lib.DkStrides(q_b, 128, kv_p, 4096, 1024, 128, 0, 0)
+    rc = lib.dk_append_kv(fake, fake, fake, 1024, 128, fake, None, fake, fake, fake, None,
+                          None, 0, 2, 32, 8, 128, 16, num_pages, 64, dk_lib.DK_F16,
+                          ctypes.byref(st), None)
+    assert rc == dk_lib.DK_EUNSUPPORTED and "2^62" in lib.dk_last_error().decode()

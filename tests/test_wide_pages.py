@@ -124,6 +124,7 @@ def test_expansion_of_separate_caches_uses_their_page_stride():
     (dict(capacity=-1), "negative"),
     (dict(num_pages=2**30, pages_mult=4), "2^31"),
     (dict(num_indices=2**30, page_size=64, pages_mult=8), "sub-pages exceed"),
+    (dict(num_pages=2**62, pages_mult=4), "num_pages must be < 2^31"),   # no wrapped product
 ])
 def test_expand_rejects_bad_arguments_before_launch(kw, needle):
     lib = dk_lib.load()
