@@ -151,20 +151,31 @@ int waves_per_cu(const Problem& p, const Plan& pl, int hp = 1) {
                                                         : kDefaultWavesPerCU;
 }
 
+// 64-byte kv-head rows (fp8 at D = 64)
+bool row64(const Problem& p) { return (int64_t)p.head_dim * p.kv_esize() == 64; }
+
 // Kv heads per workgroup of the balanced schedule (1 = one). Rows of at most
 // kNarrowRowBytes per kv head and token: the workgroup serves kGroupedKvHeads neighbouring
 // kv heads of the same pages (2 if the kv-head count is not a multiple of it), two
-// wavefronts each, so their row segments of each token are fetched together. Not with
+// wavefronts each, so their row segments of each token are fetched together; 64-byte rows
+// take kGroupedKvHeadsRow64 of one wavefront each when the kv-head count allows. Not with
 // user-set wave counts, nor for problems the plan hint shows to be small (fewer than
 // kGroupedMinUnitsPerCU (page, head chunk) units per CU), where it measured slower.
+
 int grouped_kv_heads(const Problem& p, const Plan& pl, int cus) {
   if (p.split != 0 || !p.narrow_rows() || p.opt.waves_per_group || p.opt.waves_per_cu) return 1;
   const int64_t hint = p.opt.max_pages_per_seq;
   if (hint > 0 &&
       (int64_t)p.batch * hint * pl.pairs_per_seq < (int64_t)kGroupedMinUnitsPerCU * cus)
     return 1;
+  if (row64(p) && p.hkv % kGroupedKvHeadsRow64 == 0) return kGroupedKvHeadsRow64;
   if (p.hkv % kGroupedKvHeads == 0) return kGroupedKvHeads;
   return p.hkv % 2 == 0 ? 2 : 1;
+}
+
+// Wavefronts per kv head of a grouped workgroup of hp kv heads.
+int grouped_waves(const Problem& p, int hp) {
+  return row64(p) && hp == kGroupedKvHeadsRow64 ? kGroupedWavesRow64 : kGroupedWavesPerKvHead;
 }
 
 // Workgroups of the balanced grid: about waves_per_cu wavefronts per compute unit, a
@@ -340,7 +351,7 @@ int run(Problem p, bool do_merge, void* stream) {
       const int64_t hint = p.opt.max_pages_per_seq;
       const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
       if (hp > 1) {
-        pl.waves = kGroupedWavesPerKvHead;
+        pl.waves = grouped_waves(p, hp);
       } else if (hint > 0 && auto_waves && pl.waves < kDefaultWavesPerGroupNarrow &&
                  (int64_t)p.batch * hint * pl.pairs_per_seq <= (int64_t)kSmallUnitsPerCU * cus) {
         pl.waves = kDefaultWavesPerGroupNarrow;

@@ -65,8 +65,29 @@ constexpr int kSegmentCostPerWave = DK_SEGMENT_COST_PER_WAVE;
 // kGroupedMinUnitsPerCU). With rows of at most kGroupedAlwaysRowBytes the automatic
 // schedule takes it over one pass (fp8 D=64: 64 vs 94 us); wider narrow rows keep the
 // one-pass choice (fp8 D=128 95 vs 94, D=64 bf16 ctx 2048 29 vs 33 us).
-constexpr int kGroupedKvHeads = 4;
-constexpr int kGroupedWavesPerKvHead = 2;
+// 64-byte rows (fp8 D=64) with a multiple of 8 kv heads: all 8 heads of a token row (512
+// contiguous bytes) per workgroup, one wavefront each (same wavefronts per CU). Against 4
+// heads x 2 wavefronts, us: B=32 ctx 8192 61.1 -> 59.7, ragged B=128 121.0 -> 118.6, B=64
+// ctx 4096 61.6 -> 60.2, 16/8 58.7 -> 56.7, B=4 ctx 32768 36.8 -> 37.0; over 128-byte rows
+// 8 x 1 measured no faster or slower (fp16 D=64 ctx 8192 88.3 -> 89.4, fp8 D=128 ragged
+// 192.6-199.7 -> 202.8-203.3). A build may set other groupings with the macros below (2, 4
+// or 8 kv heads, 1 or 2 wavefronts each).
+#ifndef DK_GROUPED_KV_HEADS
+#define DK_GROUPED_KV_HEADS 4
+#endif
+#ifndef DK_GROUPED_WAVES_PER_KV_HEAD
+#define DK_GROUPED_WAVES_PER_KV_HEAD 2
+#endif
+#ifndef DK_GROUPED_KV_HEADS_ROW64
+#define DK_GROUPED_KV_HEADS_ROW64 8
+#endif
+#ifndef DK_GROUPED_WAVES_ROW64
+#define DK_GROUPED_WAVES_ROW64 1
+#endif
+constexpr int kGroupedKvHeads = DK_GROUPED_KV_HEADS;
+constexpr int kGroupedWavesPerKvHead = DK_GROUPED_WAVES_PER_KV_HEAD;
+constexpr int kGroupedKvHeadsRow64 = DK_GROUPED_KV_HEADS_ROW64;
+constexpr int kGroupedWavesRow64 = DK_GROUPED_WAVES_ROW64;
 constexpr int kGroupedWavesPerCU = 8;
 constexpr int kGroupedMinUnitsPerCU = 128;
 constexpr int kGroupedAlwaysRowBytes = 64;

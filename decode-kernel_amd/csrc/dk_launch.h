@@ -68,14 +68,28 @@ const void* pass1_sym(bool balanced, int hp, bool cost) {
   if (hp == 1)
     return cost ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 1, true>)
                 : reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 1>);
-  // several kv heads per workgroup: rows of at most kNarrowRowBytes, two wavefronts each
-  if constexpr (D * (KV8 ? 1 : 2) <= kNarrowRowBytes && NW == 2) {
+  // several kv heads per workgroup: rows of at most kNarrowRowBytes, kGroupedWavesPerKvHead
+  // wavefronts each (2 kv heads when the kv-head count is no multiple of kGroupedKvHeads);
+  // 64-byte rows: kGroupedKvHeadsRow64 kv heads of kGroupedWavesRow64 wavefronts
+  constexpr int rb = D * (KV8 ? 1 : 2);
+  if constexpr (rb <= kNarrowRowBytes && NW == kGroupedWavesPerKvHead) {
     if (hp == 2)
       return cost ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 2, true>)
                   : reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 2>);
-    if (hp == 4)
-      return cost ? reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 4, true>)
-                  : reinterpret_cast<const void*>(&dk_pass1_balanced<T, D, G, NW, M, KV8, 4>);
+    if constexpr (kGroupedKvHeads != 2) {
+      if (hp == kGroupedKvHeads)
+        return cost ? reinterpret_cast<const void*>(
+                          &dk_pass1_balanced<T, D, G, NW, M, KV8, kGroupedKvHeads, true>)
+                    : reinterpret_cast<const void*>(
+                          &dk_pass1_balanced<T, D, G, NW, M, KV8, kGroupedKvHeads>);
+    }
+  }
+  if constexpr (rb == 64 && NW == kGroupedWavesRow64) {
+    if (hp == kGroupedKvHeadsRow64)
+      return cost ? reinterpret_cast<const void*>(
+                        &dk_pass1_balanced<T, D, G, NW, M, KV8, kGroupedKvHeadsRow64, true>)
+                  : reinterpret_cast<const void*>(
+                        &dk_pass1_balanced<T, D, G, NW, M, KV8, kGroupedKvHeadsRow64>);
   }
   return nullptr;
 }
