@@ -192,12 +192,14 @@ def test_fp8_arguments_are_checked():
         attention.decode_attention(q, kv, indptr, ids, last, k_scale=2.0)
 
 
-@pytest.fixture(scope="module")
-def metric_fp8():
-    """Benchmark shape (B=32, ctx 8192, 32/8/128): random finite E4M3 codes of moderate
-    magnitude (|value| <= 3.75) and the same values as an fp16 cache."""
-    q, kv, indptr, ids, last, _ = layout.synthesize_paged(32, 8192, 32, 8, 128, device=DEV,
-                                                          page_table="permuted", seed=9)
+@pytest.fixture(scope="module", params=[128, 64])
+def metric_fp8(request):
+    """Benchmark shape (B=32, ctx 8192, 32/8/128) and its D=64 form (64-byte rows: the LDS
+    page ring and whole-row kv-head groups of the balanced schedule): random finite E4M3
+    codes of moderate magnitude (|value| <= 3.75) and the same values as an fp16 cache."""
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(32, 8192, 32, 8, request.param,
+                                                          device=DEV, page_table="permuted",
+                                                          seed=9)
     g = torch.Generator(device=DEV)
     g.manual_seed(9)
     mag = torch.randint(0, 0x48, kv.shape, generator=g, device=DEV, dtype=torch.int32)
@@ -222,8 +224,8 @@ def test_full_size_fp8_equals_fp16_on_the_same_values(metric_fp8, scales):
     for qk, split, sched, h in ((2, 1, 0, 0), (2, 0, 0, hint), (2, 0, 1, 0), (2, 8, 0, 0),
                                 (1, 1, 0, 0), (1, 0, 1, 0)):
         knobs = dict(waves_per_group=4, waves_per_cu=4, qk_path=qk)
-        _announce(f"full size fp8 vs fp16 scales={scales} qk_path={qk} split={split} "
-                  f"schedule={sched}")
+        _announce(f"full size fp8 vs fp16 D={q.shape[-1]} scales={scales} qk_path={qk} "
+                  f"split={split} schedule={sched}")
         a = attention.decode_attention(q, kv8, indptr, ids, last, split_kv=split,
                                        schedule=sched, max_pages_per_seq=h, k_scale=k_scale,
                                        v_scale=v_scale, **knobs)
