@@ -1037,18 +1037,21 @@ struct Wave {
 #endif
 // Pages in flight per wavefront. An fp8 page is half the bytes of a 16-bit one, so the
 // fp8 path keeps twice the pages in flight for the same bytes (and the same registers).
-// (A 16-bit cache at D = 64 measured no faster with 4 pages than with 2.) GROUPED: a
-// balanced kernel serving several kv heads per workgroup (8 wavefronts per CU); there an
-// fp8 cache with at most 4 q heads per kv head keeps 2 pages in flight, like a 16-bit one,
-// and loads its first page before the sequence search (fp8 32/8/128, ctx 8192 unless
-// noted, us, 4 -> 2 pages: B=16 54.6 -> 51.3, B=4 ctx 32768 54.6 -> 51.1, B=256 ctx 1024
-// 103.3 -> 96.4, B=128 ctx 2048 92.7 -> 90.5, B=64 171.2 -> 168.3, ragged B=128 199.6-200.4
-// -> 193.4-199.0; 8 q heads on the VALU path spill with it).
-template <int D, bool KV8, bool GROUPED = false, int G = 1>
+// (A 16-bit cache at D = 64 measured no faster with 4 pages than with 2.) BAL: the
+// balanced kernel; there an fp8 cache with at most 4 q heads per kv head keeps 2 pages in
+// flight, like a 16-bit one, and loads its first page before the sequence search (fp8
+// 32/8/128, ctx 8192 unless noted, us, 4 -> 2 pages; kv heads grouped per workgroup: B=16
+// 54.6 -> 51.3, B=4 ctx 32768 54.6 -> 51.1, B=256 ctx 1024 103.3 -> 96.4, B=128 ctx 2048
+// 92.7 -> 90.5, B=64 171.2 -> 168.3, ragged B=128 199.6-200.4 -> 193.4-199.0; one kv head
+// per workgroup: B=4 24.4 -> 22.8, B=1 ctx 32768 24.3 -> 22.8, B=1 ctx 4096 14.0 -> 12.3,
+// D=64 B=2 ctx 16384 21.9 -> 20.7;
+// 8 q heads on the VALU path spill with it). The one-pass / explicit-split kernel keeps 4
+// (metric shape 92.2 vs 93.0 with 2).
+template <int D, bool KV8, bool BAL = false, int G = 1>
 constexpr int prefetch_depth() {
   if constexpr (KV8) {
     if constexpr (DK_PREFETCH_DEPTH_KV8 != 0) return DK_PREFETCH_DEPTH_KV8;
-    else if constexpr (GROUPED && G <= 4 && D <= 128) return 2;
+    else if constexpr (BAL && G <= 4 && D <= 128) return 2;
     else return D <= 128 ? 4 : 2;
   } else {
     return DK_PREFETCH_DEPTH ? DK_PREFETCH_DEPTH : (D <= 128 ? 2 : 1);
@@ -1315,7 +1318,7 @@ __device__ __forceinline__ void combine_store(WV& wv, CombineSmem<G, D, (NW > 1 
 
 // Wavefront w of NW streams pages first + w, first + w + NW, ... of a run of n pages
 // (through its LDS ring when LDS is set; GATED: see stream_pages).
-template <int D, bool KV8, bool CAP, bool LDS, bool GATED, bool GROUPED = false, class WV,
+template <int D, bool KV8, bool CAP, bool LDS, bool GATED, bool BAL = false, class WV,
           class PageFn, class ValidFn>
 __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n, PageFn page,
                                                    ValidFn valid, uint8_t* ring = nullptr) {
@@ -1323,7 +1326,7 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
-    constexpr int depth = prefetch_depth<D, KV8, GROUPED, WV::HEADS>();
+    constexpr int depth = prefetch_depth<D, KV8, BAL, WV::HEADS>();
     if constexpr (LDS) {
       stream_lds<lds_depth<D, KV8>(), CAP>(wv, ring, nk, pk, vk);
     } else if constexpr (depth <= 2) {
@@ -1341,16 +1344,16 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
 // (stream_loaded below): the register ring of depth <= 2 on the VALU q.k path (16-bit
 // caches at D <= 128). (The MFMA q.k path stages K through LDS and has no registers to
 // spare for it: two of its kernels spilled.)
-template <int D, bool KV8, bool LDS, bool MFMA, bool GROUPED = false, int G = 1>
+template <int D, bool KV8, bool LDS, bool MFMA, bool BAL = false, int G = 1>
 constexpr bool first_page_by_caller() {
-  return !LDS && !MFMA && prefetch_depth<D, KV8, GROUPED, G>() <= 2;
+  return !LDS && !MFMA && prefetch_depth<D, KV8, BAL, G>() <= 2;
 }
 
 // stream_interleaved with this wavefront's first page (page w of the run) already loading
 // into ka / va; the balanced kernel issues that load before it has found the sequence of
 // its first segment, and before the previous segment's combine for the others
 // (first_page_by_caller kernels only).
-template <int D, bool KV8, bool CAP, bool GROUPED = false, class WV, class PageFn,
+template <int D, bool KV8, bool CAP, bool BAL = false, class WV, class PageFn,
           class ValidFn>
 __device__ __forceinline__ void stream_loaded(WV& wv, int NW, int w, int n, PageFn page,
                                               ValidFn valid, u32 (&ka)[WV::KB],
@@ -1359,8 +1362,7 @@ __device__ __forceinline__ void stream_loaded(WV& wv, int NW, int w, int n, Page
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
-    stream_pages<prefetch_depth<D, KV8, GROUPED, WV::HEADS>(), CAP, false>(wv, ka, va, nk, pk,
-                                                                         vk);
+    stream_pages<prefetch_depth<D, KV8, BAL, WV::HEADS>(), CAP, false>(wv, ka, va, nk, pk, vk);
   }
 }
 
@@ -1566,8 +1568,7 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
   // binary search and the sequence's bounds (dependent memory trips) run while it is in
   // flight. A range shorter than the wavefront index loads nothing (zero extent); a page
   // loaded for a segment too short to have a page w is not used.
-  constexpr bool GRP = HP > 1;
-  constexpr bool PRE = first_page_by_caller<D, KV8, LDSP, MFMA, GRP, G>();
+  constexpr bool PRE = first_page_by_caller<D, KV8, LDSP, MFMA, true, G>();
   u32 ka[WV::KB], va[WV::VB];   // unused (and allocated no registers) unless PRE
   if constexpr (PRE) wv.load_page(ka, va, page_at(base + min(u + w, u_end - 1)), u + w < u_end);
 
@@ -1611,14 +1612,14 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
     if constexpr (PRE) {
       // ka / va hold (or are loading) this segment's page w, the range's unit u + w
       if (a.cap_out != 0.f)
-        stream_loaded<D, KV8, true, GRP>(wv, NW, w, n, page, valid, ka, va);
+        stream_loaded<D, KV8, true, true>(wv, NW, w, n, page, valid, ka, va);
       else
-        stream_loaded<D, KV8, false, GRP>(wv, NW, w, n, page, valid, ka, va);
+        stream_loaded<D, KV8, false, true>(wv, NW, w, n, page, valid, ka, va);
     } else {
       if (a.cap_out != 0.f)
-        stream_interleaved<D, KV8, true, LDSP, false, GRP>(wv, NW, w, n, page, valid, wring);
+        stream_interleaved<D, KV8, true, LDSP, false, true>(wv, NW, w, n, page, valid, wring);
       else
-        stream_interleaved<D, KV8, false, LDSP, false, GRP>(wv, NW, w, n, page, valid, wring);
+        stream_interleaved<D, KV8, false, LDSP, false, true>(wv, NW, w, n, page, valid, wring);
     }
 
     // the next non-empty sequence of the range, if any
