@@ -48,6 +48,19 @@ constexpr int kOnePassPairsPerCU = 4;
 // ... and uniform batches of sequences of at most this many pages with CUs/4 to CUs pairs
 // run one pass at 4 wavefronts per workgroup (dk_api.hip, short_uniform_pairs)
 constexpr int kShortOnePassPages = 32;
+// An fp8 cache at D = 128 with up to 4 q heads per kv head (VALU q.k) takes the balanced
+// schedule with grouped kv heads (an even kv-head count) for sequences longer than this
+// many pages even where one pass fits: grouped kv heads with 2 pages in flight outrun one
+// pass there. Uniform B=32 (B=16 at 32/16, B=8 at 32/32), 32/8/128 fp16 q unless noted,
+// us, one pass vs balanced: ctx 4096 50.7-51.0 vs 51.4-51.5, 5120 60.9-61.0 vs 61.6-61.9,
+// 6144 71.9-72.1 vs 70.3-70.4, 8192 92.2 vs 90.3-90.9 (bf16 q 92.4-92.5 vs 90.6-91.1; 8/8
+// 93.3 vs 88.1; 16/8 92.9 vs 88.8-89.0; 24/8 92.1 vs 90.2-90.3; 32/16 91.1-91.3 vs
+// 88.6-88.7; 32/32 91.2-91.4 vs 86.9-87.6; 8/2 B=128 96.4 vs 93.3-93.6; 24/6 B=42
+// 91.9-92.3 vs 91.4-91.7), 12288 133.5-134.2 vs 129.0-129.5, 16384 175.1 vs 166.8-167.3,
+// 32768 339.2-342.0 vs 337.0-337.3. 8 q heads per kv head stay one pass (64/8 ctx 8192
+// 91.8-92.1 vs 92.2-92.3), and so does an odd kv-head count, which the balanced schedule
+// does not group (12/3 B=85 ctx 8192 93.1-93.5 vs 94.0-94.3).
+constexpr int kFp8OnePassMaxPages = 352;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5
