@@ -281,9 +281,9 @@ bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint)
 // narrow rows, e.g. fp8 96.1 vs 157.7). With the same rows and wave counts, uniform
 // batches of short sequences (short_uniform_pairs) and of many pairs (uniform_many_pairs)
 // run one pass too, and over an fp8 cache at D = 128 (short_uniform_fp8_waves) or at
-// D = 64 (short_uniform_d64) uniform batches of short sequences. An fp8 cache at D = 128
-// with up to 4 q heads per kv head and sequences of more than kFp8OnePassMaxPages pages
-// stays balanced where that groups kv heads. Pass-1-only calls always take the balanced schedule (they return
+// D = 64 (short_uniform_d64) uniform batches of short sequences. Rows of 128 bytes (fp8
+// D = 128 up to 4 q heads per kv head, 16-bit D = 64 up to 8) with sequences of more than
+// kNarrowOnePassMaxPages pages stay balanced where that groups kv heads. Pass-1-only calls always take the balanced schedule (they return
 // partials).
 int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return 0;
@@ -299,10 +299,12 @@ int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
       grouped_kv_heads(p, pl, cus) > 1)
     return 0;
   if (hint <= 0) return 0;
-  // fp8 cache at D = 128, up to 4 q heads per kv head on the VALU path, sequences of more
-  // than kFp8OnePassMaxPages pages: balanced with grouped kv heads even where one pass fits
-  if (auto_waves && p.head_dim == 128 && p.kv_esize() == 1 && !pl.mfma && pl.heads <= 4 &&
-      hint > kFp8OnePassMaxPages && grouped_kv_heads(p, pl, cus) > 1)
+  // 128-byte rows (16-bit up to 8 q heads per kv head, fp8 up to 4 on the VALU q.k path),
+  // sequences of more than kNarrowOnePassMaxPages pages: balanced with grouped kv heads
+  // even where one pass fits
+  if (auto_waves && (int64_t)p.head_dim * p.kv_esize() == kNarrowRowBytes &&
+      (p.kv_esize() == 2 ? pl.heads <= 8 : !pl.mfma && pl.heads <= 4) &&
+      hint > kNarrowOnePassMaxPages && grouped_kv_heads(p, pl, cus) > 1)
     return 0;
   if (one_pass_fits(p, pl, cus, hint)) return pl.waves;
   if (auto_waves && pl.waves == kDefaultWavesPerGroup &&

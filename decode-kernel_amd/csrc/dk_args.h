@@ -48,19 +48,27 @@ constexpr int kOnePassPairsPerCU = 4;
 // ... and uniform batches of sequences of at most this many pages with CUs/4 to CUs pairs
 // run one pass at 4 wavefronts per workgroup (dk_api.hip, short_uniform_pairs)
 constexpr int kShortOnePassPages = 32;
-// An fp8 cache at D = 128 with up to 4 q heads per kv head (VALU q.k) takes the balanced
-// schedule with grouped kv heads (an even kv-head count) for sequences longer than this
-// many pages even where one pass fits: grouped kv heads with 2 pages in flight outrun one
-// pass there. Uniform B=32 (B=16 at 32/16, B=8 at 32/32), 32/8/128 fp16 q unless noted,
-// us, one pass vs balanced: ctx 4096 50.7-51.0 vs 51.4-51.5, 5120 60.9-61.0 vs 61.6-61.9,
-// 6144 71.9-72.1 vs 70.3-70.4, 8192 92.2 vs 90.3-90.9 (bf16 q 92.4-92.5 vs 90.6-91.1; 8/8
-// 93.3 vs 88.1; 16/8 92.9 vs 88.8-89.0; 24/8 92.1 vs 90.2-90.3; 32/16 91.1-91.3 vs
-// 88.6-88.7; 32/32 91.2-91.4 vs 86.9-87.6; 8/2 B=128 96.4 vs 93.3-93.6; 24/6 B=42
-// 91.9-92.3 vs 91.4-91.7), 12288 133.5-134.2 vs 129.0-129.5, 16384 175.1 vs 166.8-167.3,
-// 32768 339.2-342.0 vs 337.0-337.3. 8 q heads per kv head stay one pass (64/8 ctx 8192
-// 91.8-92.1 vs 92.2-92.3), and so does an odd kv-head count, which the balanced schedule
-// does not group (12/3 B=85 ctx 8192 93.1-93.5 vs 94.0-94.3).
-constexpr int kFp8OnePassMaxPages = 352;
+// Rows of 128 bytes (an fp8 cache at D = 128 up to 4 q heads per kv head, on the VALU q.k
+// path; a 16-bit one at D = 64 up to 8, 64/8 on the MFMA path) take the balanced schedule
+// with grouped kv heads (an even kv-head count) for sequences longer than this many pages
+// even where one pass fits: grouped kv heads with 2 pages in flight outrun one pass there
+// (fp8 at 8 q heads per kv head, on the MFMA path with 4 pages in flight, does not: 64/8
+// ctx 8192 one pass 91.8-92.1 vs balanced 92.2-92.3). Uniform B=32 (B=16 at
+// 32/16, B=8 at 32/32), 32/8, fp16 q unless noted, us, one pass vs balanced:
+//   fp8 D=128: ctx 4096 50.7-51.0 vs 51.4-51.5, 5120 60.9-61.0 vs 61.6-61.9, 6144
+//   71.9-72.1 vs 70.3-70.4, 8192 92.2 vs 90.3-90.9 (bf16 q 92.4-92.5 vs 90.6-91.1; 8/8
+//   93.3 vs 88.1; 16/8 92.9 vs 88.8-89.0; 24/8 92.1 vs 90.2-90.3; 32/16 91.1-91.3 vs
+//   88.6-88.7; 32/32 91.2-91.4 vs 86.9-87.6; 8/2 B=128 96.4 vs 93.3-93.6; 24/6 B=42
+//   91.9-92.3 vs 91.4-91.7), 12288 133.5-134.2 vs 129.0-129.5, 16384 175.1 vs
+//   166.8-167.3, 32768 339.2-342.0 vs 337.0-337.3;
+//   16-bit D=64: ctx 4096 49.0-49.3 vs 48.9, 5120 59.0-59.1 vs 59.3-59.4, 6144 70.2-70.5
+//   vs 68.0-68.1, 8192 91.3-91.4 vs 88.1 (bf16 91.1-91.4 vs 87.8-87.9; 8/8 90.7-91.2 vs
+//   86.8-86.9; 16/8 92.0-92.4 vs 87.1-87.3; 64/8 92.5-92.6 vs 89.1-89.2; 32/16 91.7-92.2
+//   vs 86.8; 32/32 89.8-90.8 vs 85.8-86.0), 12288 134.4-134.9 vs 126.7-126.9, 16384
+//   177.9 vs 164.1-164.3.
+// An odd kv-head count, which the balanced schedule does not group, stays one pass (fp8
+// 12/3 B=85 ctx 8192 93.1-93.5 vs 94.0-94.3).
+constexpr int kNarrowOnePassMaxPages = 352;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5

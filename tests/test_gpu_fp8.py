@@ -303,27 +303,6 @@ def test_ragged_fp8_charged_range_split_matches_oracle(batch, d):
     assert torch.allclose(out.float(), ref_out.float(), atol=2e-3)
 
 
-@pytest.mark.parametrize("hq,hkv,batch,pages,want", [
-    (32, 8, 32, 512, 0), (32, 8, 32, 353, 0), (32, 8, 32, 352, 1), (32, 8, 32, 256, 1),
-    (8, 8, 32, 512, 0), (32, 32, 8, 512, 0), (8, 2, 128, 512, 0), (32, 8, 32, 2048, 0),
-    (64, 8, 32, 512, 1), (12, 3, 85, 512, 1)])
-def test_fp8_d128_long_uniform_plans_balanced(hq, hkv, batch, pages, want):
-    # about one (sequence, kv head) pair per CU of the MI355X's 256, uniform lengths: one
-    # pass fits, and it is what the automatic schedule runs for 16-bit caches; over an fp8
-    # cache at D=128 with up to 4 q heads per kv head and an even kv-head count, sequences
-    # longer than 352 pages take the balanced schedule with grouped kv heads (0); 8 q heads
-    # per kv head, an odd kv-head count and shorter sequences keep one pass (1)
-    import dk_lib
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if cus != 256:
-        pytest.skip(f"the cases are sized for 256 CUs, not {cus}")
-    code = attention._DTYPE_CODE[torch.float16]
-    opts = dk_lib.options(max_pages_per_seq=pages, kv_dtype=dk_lib.DK_KV_FP8_E4M3)
-    got = dk_lib.plan_schedule(batch, hq, hkv, 128, batch * pages, code, 0, opts)
-    _announce(f"fp8 plan {hq}/{hkv} B={batch} pages={pages}: {got}")
-    assert got == want
-
-
 @pytest.mark.parametrize("batch,ctx,d", [(8, 500, 128), (64, 256, 128), (512, 200, 128),
                                          (16, 512, 64), (64, 200, 64)])
 def test_short_uniform_fp8_one_pass_matches_oracle(batch, ctx, d):

@@ -577,6 +577,58 @@ def test_schedules_agree_and_reuse_a_dirty_workspace(batch):
         assert torch.allclose(o.float(), outs[0].float(), atol=2e-3)
 
 
+@pytest.mark.parametrize("kv8,d,hq,hkv,batch,pages,want", [
+    (True, 128, 32, 8, 32, 512, 0), (True, 128, 32, 8, 32, 353, 0),
+    (True, 128, 32, 8, 32, 352, 1), (True, 128, 32, 8, 32, 256, 1),
+    (True, 128, 8, 8, 32, 512, 0), (True, 128, 32, 32, 8, 512, 0),
+    (True, 128, 8, 2, 128, 512, 0), (True, 128, 32, 8, 32, 2048, 0),
+    (True, 128, 64, 8, 32, 512, 1), (True, 128, 12, 3, 85, 512, 1),
+    (False, 64, 32, 8, 32, 512, 0), (False, 64, 32, 8, 32, 352, 1),
+    (False, 64, 64, 8, 32, 512, 0), (False, 64, 32, 32, 8, 1024, 0),
+    (False, 64, 12, 3, 85, 512, 1), (False, 128, 32, 8, 32, 512, 1)])
+def test_narrow_rows_long_uniform_plans_balanced(kv8, d, hq, hkv, batch, pages, want):
+    # about one (sequence, kv head) pair per CU of the MI355X's 256, uniform lengths: one
+    # pass fits, and it is what the automatic schedule runs over 256-byte rows (16-bit
+    # D=128); over 128-byte rows (fp8 D=128 with up to 4 q heads per kv head, 16-bit D=64
+    # with up to 8) with an even kv-head count, sequences longer than 352 pages take the
+    # balanced schedule with grouped kv heads (0); fp8 with 8 q heads per kv head, an odd
+    # kv-head count and shorter sequences keep one pass (1)
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip(f"the cases are sized for 256 CUs, not {cus}")
+    code = attention._DTYPE_CODE[torch.float16]
+    opts = dk_lib.options(max_pages_per_seq=pages,
+                          kv_dtype=dk_lib.DK_KV_FP8_E4M3 if kv8 else dk_lib.DK_KV_SAME)
+    got = dk_lib.plan_schedule(batch, hq, hkv, d, batch * pages, code, 0, opts)
+    _announce(f"plan {'fp8' if kv8 else 'fp16'} D={d} {hq}/{hkv} B={batch} pages={pages}: "
+              f"{got}")
+    assert got == want
+
+
+def test_d64_long_uniform_balanced_matches_oracle():
+    # 16-bit D=64, uniform B=32 sequences of 400 pages with the plan hint: the automatic
+    # schedule is the balanced one with grouped kv heads; checked against the oracle and
+    # against the forced one pass
+    import dk_lib
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        32, 400 * 16 - 5, 32, 8, 64, dtype=torch.bfloat16, device=DEV, page_table="permuted",
+        seed=33)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[torch.bfloat16]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus == 256:
+        assert dk_lib.plan_schedule(32, 32, 8, 64, ids.shape[0], code, 0,
+                                    dk_lib.options(max_pages_per_seq=hint)) == 0
+    rows = [0, 13, 31]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0, schedule=2)
+    torch.cuda.synchronize()
+    _check(a, want, rows=rows, label="balanced D=64")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_plan_hint_one_pass_on_uniform_batch(dtype):
     # uniform batch that fills the balanced grid: with the hint the automatic schedule is
