@@ -1662,17 +1662,23 @@ __global__ __launch_bounds__(NW * HP * 64, (min_waves_per_simd<D, G, KV8>())) vo
 // Partial k of a row: O at po + k * stride_rows * D, m and l at pm / pl + k * stride_rows.
 // One wavefront per row, lanes over the D dims (E = D/64 each). The O loads of the first
 // kU slots are issued before the m / l loads and the max, so a row with up to kU slots
-// costs one memory round trip; more slots are loaded kU at a time.
+// costs one memory round trip; more slots are loaded kV at a time.
 template <class T, int D>
 __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const float* po,
                                           const float* pm, const float* pl, int nslots,
                                           int64_t stride_rows) {
   constexpr int E = D / 64;
   constexpr int kU = E <= 2 ? 32 : 16;
+  constexpr int kV = 8;   // slots per later batch (rows of more than kU slots)
   typedef float vecE __attribute__((ext_vector_type(E)));
   const int lane = threadIdx.x & 63;
-  const float* o = po + lane * E;
-  auto o_at = [&](int k) { return *reinterpret_cast<const vecE*>(o + (int64_t)k * stride_rows * D); };
+  // slot k's row starts at a wave-uniform address (scalar registers); each lane adds its
+  // own 32-bit byte offset, so no slot needs a 64-bit vector address
+  const uint32_t lane_off = (uint32_t)(lane * E) * 4u;
+  auto o_at = [&](int k) {
+    const char* base = reinterpret_cast<const char*>(po + (int64_t)k * stride_rows * D);
+    return *reinterpret_cast<const vecE*>(base + lane_off);
+  };
   // first batch of O (uniform guards: no load past the row's last slot)
   const int cnt0 = min(nslots, kU);
   vecE v0[kU];
@@ -1708,12 +1714,12 @@ __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const flo
       for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, u) * v0[u];   // zero past cnt0
       j = cnt0;
     }
-    for (; j + kU <= cnt; j += kU) {
-      vecE v[kU];
+    for (; j + kV <= cnt; j += kV) {
+      vecE v[kV];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) v[u] = o_at(k0 + j + u);
+      for (int u = 0; u < kV; ++u) v[u] = o_at(k0 + j + u);
 #pragma unroll
-      for (int u = 0; u < kU; ++u) acc += readlane_f(wgt, j + u) * v[u];
+      for (int u = 0; u < kV; ++u) acc += readlane_f(wgt, j + u) * v[u];
     }
     for (; j < cnt; ++j) acc += readlane_f(wgt, j) * o_at(k0 + j);
   }
@@ -1729,7 +1735,7 @@ __device__ __forceinline__ void merge_row(const MergeArgs& m, int row, const flo
 
 template <class T, int D>
 __global__ __launch_bounds__(256) void dk_merge_split(MergeArgs m) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
   if (row >= m.batch * m.hq) return;
   const int64_t r0 = (int64_t)row * m.split;
   merge_row<T, D>(m, row, m.po + r0 * D, m.pm + r0, m.pl + r0, m.split, 1);
@@ -1738,7 +1744,7 @@ __global__ __launch_bounds__(256) void dk_merge_split(MergeArgs m) {
 // COST: pass 1 ran the charged range split (m.seg_cost); the other build carries none of it.
 template <class T, int D, bool COST = false>
 __global__ __launch_bounds__(256) void dk_merge_balanced(MergeArgs m) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
   if (row >= m.batch * m.hq) return;
   const int b = row / m.hq, qh = row % m.hq;
   const int G = m.heads, Wg = m.waves_per_pair;
