@@ -348,8 +348,11 @@ class Caller:
                                                self.stream.cuda_stream)
 
     def pass1(self):
+        # split_kv 0 resolved to an explicit split: that split's pass 1 (the pass-1-only
+        # entry point would take the balanced schedule)
+        split = self.schedule if self.split == 0 and self.schedule > 1 else self.split
         return self.lib.dk_decode_partials(*self.common, self.ws.data_ptr(), self.ws.numel(),
-                                           *self.shape, self.split, ctypes.byref(self.opts),
+                                           *self.shape, split, ctypes.byref(self.opts),
                                            self.stream.cuda_stream)
 
     def dominant(self):

@@ -323,6 +323,27 @@ int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   return 0;
 }
 
+// The explicit split that split_kv == 0 runs for a uniform batch over 256-byte rows whose
+// (sequence, kv head) pairs divide the balanced grid into S >= 2 ranges of at least
+// kSplitFillMinPages pages (0: not such a batch, or its partials would not fit ws_bytes).
+// Full calls only: the pass-1-only entry point returns the balanced schedule's partials.
+int auto_split_fill(const Problem& p, const Plan& pl, int cus, size_t ws_bytes) {
+  const int64_t hint = p.opt.max_pages_per_seq;
+  const bool auto_waves = !p.opt.waves_per_group && !p.opt.waves_per_cu;
+  if (!p.need_out || p.opt.schedule != 0 || hint <= 0 || !auto_waves || pl.mfma ||
+      (int64_t)p.head_dim * p.kv_esize() != 256 || pl.waves != kDefaultWavesPerGroup ||
+      waves_per_cu(p, pl) != kDefaultWavesPerCU || !near_uniform(p, hint))
+    return 0;
+  const int64_t pairs = (int64_t)p.batch * pl.pairs_per_seq;
+  const int64_t groups = balanced_groups(p, pl, cus);
+  if (pairs <= 0 || groups % pairs != 0) return 0;
+  const int64_t s = groups / pairs;
+  if (s < 2 || s > kMaxSplit || (hint + s - 1) / s < kSplitFillMinPages) return 0;
+  size_t o, m, l, total;
+  partials_layout_rows(split_rows(p.batch, p.hq, (int)s), p.head_dim, &o, &m, &l, &total);
+  return total <= ws_bytes ? (int)s : 0;
+}
+
 }  // namespace
 
 // Validation, planning and both passes; shared by the extern "C" entry points.
@@ -355,6 +376,9 @@ int run(Problem p, bool do_merge, void* stream) {
       pl.balanced = false;
       pl.waves = one_pass_waves;
       pl.grid = split_grid(p.batch, p.hkv, 1, pl.chunks);
+    } else if (const int s = auto_split_fill(p, pl, cus, p.workspace_bytes)) {
+      p.split = s;
+      pl = make_plan(p);
     } else {
       hp = grouped_kv_heads(p, pl, cus);
       const int64_t hint = p.opt.max_pages_per_seq;
@@ -645,7 +669,10 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, i
   if (p.opt.window > 0)   // explicit splits of the window, in the default workspace
     return dk::window_split(p, cus, dk::workspace_bytes(batch, num_q_heads, num_kv_heads,
                                                         head_dim, 0));
-  return dk::auto_one_pass(p, dk::make_plan(p), cus) > 0 ? 1 : 0;
+  const dk::Plan pl = dk::make_plan(p);
+  if (dk::auto_one_pass(p, pl, cus) > 0) return 1;
+  return dk::auto_split_fill(p, pl, cus,
+                             dk::workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, 0));
 }
 
 int dk_decode_attention_ex(const void* q, const void* kv_data, const int32_t* kv_indptr,

@@ -69,6 +69,15 @@ constexpr int kShortOnePassPages = 32;
 // An odd kv-head count, which the balanced schedule does not group, stays one pass (fp8
 // 12/3 B=85 ctx 8192 93.1-93.5 vs 94.0-94.3).
 constexpr int kNarrowOnePassMaxPages = 352;
+// A uniform batch over 256-byte rows (16-bit D = 128, VALU q.k, default wave counts) whose
+// (sequence, kv head) pairs divide the balanced grid into S >= 2 equal page ranges of at
+// least this many pages runs the explicit split S instead: the same ranges on a grid of the
+// same size, streamed faster over such long runs (32/8/128, us, balanced vs split S: B=16
+// ctx 65536 (S=2, 2048 pages) 631.9-634.0 vs 609.8-611.3, B=4 ctx 131072 bf16 (S=8, 1024)
+// 314.5-315.8 vs 308.7-308.8; shorter ranges stay balanced: B=16 ctx 16384 (512)
+// 158.5-160.5 vs 159.6-160.0, B=8 ctx 32768 (512) 158.3-159.2 vs 159.5-160.4, B=1 ctx
+// 131072 bf16 (256) 84.3-84.5 vs 85.1-85.2, B=2 ctx 65536 (256) 84.4-84.7 vs 84.8-84.9).
+constexpr int kSplitFillMinPages = 1024;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5

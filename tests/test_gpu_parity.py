@@ -606,6 +606,60 @@ def test_narrow_rows_long_uniform_plans_balanced(kv8, d, hq, hkv, batch, pages, 
     assert got == want
 
 
+@pytest.mark.parametrize("batch,pages,dtype,want", [
+    (16, 4096, torch.float16, 2), (4, 8192, torch.bfloat16, 8), (16, 2048, torch.float16, 2),
+    (8, 4096, torch.float16, 4), (16, 1024, torch.float16, 0), (1, 8192, torch.bfloat16, 0),
+    (2, 4096, torch.float16, 0)])
+def test_long_uniform_plans_explicit_split(batch, pages, dtype, want):
+    # 16-bit D=128, uniform lengths: when the (sequence, kv head) pairs divide the balanced
+    # grid of the MI355X's 256 CUs into S >= 2 ranges of at least 1024 pages, split_kv 0
+    # runs the explicit split S (the plan names it); shorter ranges stay balanced (0)
+    import dk_lib
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip(f"the cases are sized for 256 CUs, not {cus}")
+    code = attention._DTYPE_CODE[dtype]
+    got = dk_lib.plan_schedule(batch, 32, 8, 128, batch * pages, code, 0,
+                               dk_lib.options(max_pages_per_seq=pages))
+    _announce(f"plan B={batch} pages={pages} {dtype}: {got}")
+    assert got == want
+    # an fp8 cache, or a ragged batch, of the same size stays balanced
+    assert dk_lib.plan_schedule(batch, 32, 8, 128, batch * pages, code, 0,
+                                dk_lib.options(max_pages_per_seq=pages,
+                                               kv_dtype=dk_lib.DK_KV_FP8_E4M3)) == 0
+    if batch > 1:
+        assert dk_lib.plan_schedule(batch, 32, 8, 128, batch * pages // 2, code, 0,
+                                    dk_lib.options(max_pages_per_seq=pages)) == 0
+
+
+def test_long_uniform_split_fill_matches_oracle():
+    # B=16 uniform sequences of 2048 pages with the plan hint: split_kv 0 runs the explicit
+    # split 2 (on 256 CUs); checked against the oracle on three sequences and against the
+    # forced balanced schedule on all of them
+    import dk_lib
+    q, kv, indptr, ids, last, _ = layout.synthesize_paged(
+        16, 2048 * 16 - 7, 32, 8, 128, dtype=torch.float16, device=DEV,
+        page_table="permuted", seed=41)
+    hint = attention.plan_hint(indptr.cpu())
+    code = attention._DTYPE_CODE[torch.float16]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    s = dk_lib.plan_schedule(16, 32, 8, 128, ids.shape[0], code, 0,
+                             dk_lib.options(max_pages_per_seq=hint))
+    _announce(f"split fill B=16 pages=2048: plan {s}")
+    if cus == 256:
+        assert s == 2
+    rows = [0, 7, 15]
+    want = _oracle(q, kv, indptr, ids, last, batch_subset=rows)
+    a = decode_attention(q, kv, indptr, ids, last, split_kv=0, max_pages_per_seq=hint)
+    b = decode_attention(q, kv, indptr, ids, last, split_kv=0, schedule=1)
+    c = decode_attention(q, kv, indptr, ids, last, split_kv=2)
+    torch.cuda.synchronize()
+    _check(a, want, rows=rows, label="split fill")
+    assert torch.allclose(a.float(), b.float(), atol=2e-3)
+    if s == 2:
+        assert torch.equal(a, c)   # the same kernel and partition as split_kv=2
+
+
 def test_d64_long_uniform_balanced_matches_oracle():
     # 16-bit D=64, uniform B=32 sequences of 400 pages with the plan hint: the automatic
     # schedule is the balanced one with grouped kv heads; checked against the oracle and
