@@ -344,6 +344,21 @@ int auto_split_fill(const Problem& p, const Plan& pl, int cus, size_t ws_bytes) 
   return total <= ws_bytes ? (int)s : 0;
 }
 
+// Whether a caller's explicit split over 256-byte rows runs 4 wavefronts per workgroup
+// (kShortSplitPages): its workgroups are fewer than the CUs, or stream short runs of pages
+// (the mean sequence's pages per split).
+bool short_split_runs(const Problem& p, const Plan& pl, int cus) {
+  if (p.split < 1 || pl.balanced || p.opt.waves_per_group || p.opt.waves_per_cu ||
+      p.opt.window > 0 || pl.mfma || pl.waves != kDefaultWavesPerGroup ||
+      (int64_t)p.head_dim * p.kv_esize() != 256)
+    return false;
+  const int64_t groups = (int64_t)p.batch * p.hkv * pl.chunks * p.split;
+  const int64_t avg = p.num_indices / p.batch;
+  const int64_t pps = (avg + p.split - 1) / p.split;
+  return groups < cus || pps <= kShortSplitPages ||
+         (groups >= 2 * (int64_t)cus && pps <= 2 * kShortSplitPages);
+}
+
 }  // namespace
 
 // Validation, planning and both passes; shared by the extern "C" entry points.
@@ -352,6 +367,10 @@ int run(Problem p, bool do_merge, void* stream) {
   const int rc = validate(p);
   if (rc != DK_OK || p.batch == 0) return rc;
   Plan pl = make_plan(p);
+  if (!pl.balanced) {
+    const int cus = cu_count(current_device(-1));
+    if (cus > 0 && short_split_runs(p, pl, cus)) pl.waves = kDefaultWavesPerGroupNarrow;
+  }
   int waves_per_pair = 0;   // balanced: workgroups per head chunk
   int seg_cost = 0;         // balanced: pages charged per change of sequence
   int hp = 1;               // balanced: kv heads per workgroup

@@ -78,6 +78,21 @@ constexpr int kNarrowOnePassMaxPages = 352;
 // 158.5-160.5 vs 159.6-160.0, B=8 ctx 32768 (512) 158.3-159.2 vs 159.5-160.4, B=1 ctx
 // 131072 bf16 (256) 84.3-84.5 vs 85.1-85.2, B=2 ctx 65536 (256) 84.4-84.7 vs 84.8-84.9).
 constexpr int kSplitFillMinPages = 1024;
+// An explicit split_kv over 256-byte rows (16-bit D = 128, VALU q.k, default wave counts)
+// runs 4 wavefronts per workgroup instead of 2 when its workgroups are fewer than the CUs,
+// or stream at most this many pages each (twice as many with at least two workgroups per
+// CU): each wavefront's chain of pages is half as long. 32/8/128 fp16 unless noted, us, 2 vs
+// 4 wavefronts (workgroups, pages per split): B=2 ctx 512 split 4 (64, 8) 12.4-12.5 vs 11.2
+// (bf16 the same; 8/8 heads 10.7 vs 9.9), split 1 (16, 32) 15.7 vs 11.8; B=8 ctx 512 split
+// 1 (64, 32) 15.9 vs 12.3; B=1 ctx 4096 split 1 (8, 256) 73.7 vs 49.1, split 8 (64, 32)
+// 18.9 vs 15.2-15.3, split 16 (128, 16) 14.1 vs 13.8; B=4 ctx 4096 split 4 (128, 64) 27.0
+// vs 23.2, split 8 (256, 32) 20.4-20.5 vs 19.6, split 16 (512, 16) 21.6 vs 20.8; B=8 ctx
+// 1024 split 2 (128, 32) 19.3 vs 16.1; B=32 ctx 1024 split 2 (512, 32) 33.4 vs 29.8; B=16
+// ctx 1024 split 4 (512, 16) 21.6 vs 20.6; B=32 ctx 2048 split 2 (512, 64) 53.5 vs 50.3;
+// B=64 ctx 512 split 1 (512, 32) 30.5 vs 26.7. Two stay faster with as many workgroups as
+// CUs and longer runs: B=16 ctx 4096 split 2 (256, 128) 48.4 vs 49.2-49.3, B=1 ctx 32768
+// bf16 split 32 (256, 64) 29.3-29.4 vs 30.6, and the metric shape's one pass (256, 512).
+constexpr int kShortSplitPages = 32;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
 // workgroup is the time of ~10 pages (C4, B=128 ctx U[128, 8192]: workgroups crossing 3 / 5
