@@ -345,8 +345,9 @@ int auto_split_fill(const Problem& p, const Plan& pl, int cus, size_t ws_bytes) 
 }
 
 // Whether a caller's explicit split over 256-byte rows runs 4 wavefronts per workgroup
-// (kShortSplitPages): its workgroups are fewer than the CUs, or stream short runs of pages
-// (the mean sequence's pages per split).
+// (kShortSplitPages): its workgroups are fewer than the CUs; as many as the CUs, streaming
+// short runs of pages (the mean sequence's pages per split); or up to twice as many, so
+// that all their wavefronts are resident at once (2 per SIMD).
 bool short_split_runs(const Problem& p, const Plan& pl, int cus) {
   if (p.split < 1 || pl.balanced || p.opt.waves_per_group || p.opt.waves_per_cu ||
       p.opt.window > 0 || pl.mfma || pl.waves != kDefaultWavesPerGroup ||
@@ -355,8 +356,8 @@ bool short_split_runs(const Problem& p, const Plan& pl, int cus) {
   const int64_t groups = (int64_t)p.batch * p.hkv * pl.chunks * p.split;
   const int64_t avg = p.num_indices / p.batch;
   const int64_t pps = (avg + p.split - 1) / p.split;
-  return groups < cus || pps <= kShortSplitPages ||
-         (groups >= 2 * (int64_t)cus && pps <= 2 * kShortSplitPages);
+  if (groups > 2 * (int64_t)cus) return false;
+  return groups != cus || pps <= kShortSplitPages;
 }
 
 }  // namespace

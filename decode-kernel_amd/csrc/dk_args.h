@@ -80,18 +80,22 @@ constexpr int kNarrowOnePassMaxPages = 352;
 constexpr int kSplitFillMinPages = 1024;
 // An explicit split_kv over 256-byte rows (16-bit D = 128, VALU q.k, default wave counts)
 // runs 4 wavefronts per workgroup instead of 2 when its workgroups are fewer than the CUs,
-// or stream at most this many pages each (twice as many with at least two workgroups per
-// CU): each wavefront's chain of pages is half as long. 32/8/128 fp16 unless noted, us, 2 vs
-// 4 wavefronts (workgroups, pages per split): B=2 ctx 512 split 4 (64, 8) 12.4-12.5 vs 11.2
-// (bf16 the same; 8/8 heads 10.7 vs 9.9), split 1 (16, 32) 15.7 vs 11.8; B=8 ctx 512 split
-// 1 (64, 32) 15.9 vs 12.3; B=1 ctx 4096 split 1 (8, 256) 73.7 vs 49.1, split 8 (64, 32)
-// 18.9 vs 15.2-15.3, split 16 (128, 16) 14.1 vs 13.8; B=4 ctx 4096 split 4 (128, 64) 27.0
-// vs 23.2, split 8 (256, 32) 20.4-20.5 vs 19.6, split 16 (512, 16) 21.6 vs 20.8; B=8 ctx
-// 1024 split 2 (128, 32) 19.3 vs 16.1; B=32 ctx 1024 split 2 (512, 32) 33.4 vs 29.8; B=16
-// ctx 1024 split 4 (512, 16) 21.6 vs 20.6; B=32 ctx 2048 split 2 (512, 64) 53.5 vs 50.3;
-// B=64 ctx 512 split 1 (512, 32) 30.5 vs 26.7. Two stay faster with as many workgroups as
-// CUs and longer runs: B=16 ctx 4096 split 2 (256, 128) 48.4 vs 49.2-49.3, B=1 ctx 32768
-// bf16 split 32 (256, 64) 29.3-29.4 vs 30.6, and the metric shape's one pass (256, 512).
+// up to twice as many (all 4-wavefront workgroups then resident at once, 2 per SIMD), or
+// exactly as many and streaming at most this many pages each: each wavefront's chain of
+// pages is half as long. 32/8/128 fp16 unless noted, us, 2 vs 4 wavefronts (workgroups,
+// pages per split): fewer than the CUs: B=2 ctx 512 split 4 (64, 8) 12.4-12.5 vs 11.2 (bf16
+// the same; 8/8 heads 10.7 vs 9.9), split 1 (16, 32) 15.7 vs 11.8; B=8 ctx 512 split 1 (64,
+// 32) 15.9 vs 12.3; B=1 ctx 4096 split 1 (8, 256) 73.7 vs 49.1, split 8 (64, 32) 18.9 vs
+// 15.2-15.3, split 16 (128, 16) 14.1 vs 13.8; B=4 ctx 4096 split 4 (128, 64) 27.0 vs 23.2;
+// B=8 ctx 1024 split 2 (128, 32) 19.3 vs 16.1; as many: B=4 ctx 4096 split 8 (256, 32)
+// 20.4-20.5 vs 19.6, but B=16 ctx 4096 split 2 (256, 128) 48.4 vs 49.2-49.3, B=1 ctx 32768
+// bf16 split 32 (256, 64) 29.3-29.4 vs 30.6 and the metric shape's one pass (256, 512) stay
+// at 2; twice as many: B=4 ctx 4096 split 16 (512, 16) 21.6 vs 20.8, B=16 ctx 1024 split 4
+// (512, 16) 21.6 vs 20.6, B=32 ctx 1024 split 2 (512, 32) 33.4 vs 29.8, B=32 ctx 2048
+// split 2 (512, 64) 53.5 vs 50.3, ctx 4096 (512, 128) 98.9-99.3 vs 91.3-91.5, ctx 8192
+// (512, 256) 184.5-184.7 vs 171.6-172.0, B=64 ctx 512 split 1 (512, 32) 30.5 vs 26.7;
+// more (a second round of workgroups at 4): B=64 ctx 2048 split 2 (1024, 64) 92.0-92.8 vs
+// 94.5, ctx 4096 (1024, 128) 173.3-173.7 vs 175.1-175.9.
 constexpr int kShortSplitPages = 32;
 // Balanced schedule over a ragged batch: a change of sequence costs a workgroup about 3 us
 // (its reduction, combine, stores and pipeline refill), which at two wavefronts per
