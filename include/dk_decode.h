@@ -78,8 +78,11 @@ typedef struct {
                               the balanced schedule over such narrow rows serves 4 (or
                               2) neighbouring kv heads per workgroup with 2 wavefronts
                               each, over small problems (plan hint) uses 4, and over many
-                              short sequences (plan hint) 1; else 1, 2 or 4 (then one kv
-                              head per workgroup)                                         */
+                              short sequences (plan hint) 1; an explicit split_kv over
+                              256-byte rows uses 4 when its workgroups are fewer than the
+                              compute units, up to twice as many, or as many with at most
+                              32 pages each; else 1, 2 or 4 (then one kv head per
+                              workgroup)                                                  */
   int32_t waves_per_cu;    /* wavefronts per compute unit the automatic and balanced
                               schedules aim for (0 = default: 2, or 4 as above, 8 with
                               grouped kv heads)                                           */
@@ -153,7 +156,8 @@ int dk_choose_split(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
 /* The schedule that dk_decode_attention_ex runs for these arguments on `device` (-1 =
  * current): 1 = one pass (one workgroup per (sequence, kv head), no merge), 0 = balanced
  * schedule + merge, > 1 = that explicit split + merge (with opts->window, the explicit
- * split of the window's pages that a workspace of dk_workspace_bytes(..., 0) allows). No
+ * split of the window's pages that a workspace of dk_workspace_bytes(..., 0) allows; for a
+ * long uniform batch over 256-byte rows, the split that fills the balanced grid). No
  * counterpart in the reference; for callers that size launches or profile the kernels.
  * Returns < 0 on a bad argument. */
 int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
@@ -179,7 +183,11 @@ int dk_plan_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
  *                  fp8 cache at D = 128: CUs/4 pairs or more; at D = 64: CUs/4 to
  *                  2 * CUs pairs, either cache) (otherwise never for kv-head rows
  *                  of <= 64 bytes, which stream faster with grouped kv heads in the
- *                  balanced schedule).
+ *                  balanced schedule, nor for 128-byte rows with an even kv-head count
+ *                  and sequences of more than 352 pages); or, for a uniform batch over
+ *                  256-byte rows whose pairs divide the balanced grid into S >= 2
+ *                  ranges of at least 1024 pages, the explicit split S
+ *                  (dk_plan_schedule returns S).
  * Replaces decode_attention_split_kv_cuda (src/cuda_/attention_ext.cu:541-609) and
  * decode_attention_naive_cuda (src/cuda_/attention_ext.cu:499-539), i.e. the two
  * functions behind src/attention.py:50-58. Differences: the caller allocates `out`
