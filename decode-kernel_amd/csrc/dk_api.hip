@@ -283,8 +283,8 @@ bool uniform_many_pairs(const Problem& p, const Plan& pl, int cus, int64_t hint)
 // run one pass too, and over an fp8 cache at D = 128 (short_uniform_fp8_waves) or at
 // D = 64 (short_uniform_d64) uniform batches of short sequences. Rows of 128 bytes (fp8
 // D = 128 up to 4 q heads per kv head, 16-bit D = 64 up to 8) with sequences of more than
-// kNarrowOnePassMaxPages pages stay balanced where that groups kv heads. Pass-1-only calls always take the balanced schedule (they return
-// partials).
+// kNarrowOnePassMaxPages pages stay balanced where that groups kv heads. Pass-1-only calls
+// always take the balanced schedule (they return partials).
 int auto_one_pass(const Problem& p, const Plan& pl, int cus) {
   if (!p.need_out || p.opt.schedule == 1) return 0;
   if (p.opt.schedule == 2) return pl.waves;
