@@ -364,6 +364,7 @@ struct Wave {
   static constexpr int NS = WIDE ? 1 : G / GQ;             // column sets (G = 8 -> 2)
   static constexpr int AH = WIDE ? 4 : G;                  // heads held in acc
   static constexpr int HEADS = G;                          // q heads per wavefront
+  static constexpr bool MF = MFMA;                         // q.k on the matrix cores
   static constexpr int DPL = D / 16;         // V (and VALU-path K) dims per lane
   static constexpr int VWT = DPL / 2;        // words per token per lane
   static constexpr int KW = D / 8;           // K words per lane per page (both paths)
@@ -1046,12 +1047,16 @@ struct Wave {
 // per workgroup: B=4 24.4 -> 22.8, B=1 ctx 32768 24.3 -> 22.8, B=1 ctx 4096 14.0 -> 12.3,
 // D=64 B=2 ctx 16384 21.9 -> 20.7;
 // 8 q heads on the VALU path spill with it). The one-pass / explicit-split kernel keeps 4
-// (metric shape 92.2 vs 93.0 with 2).
-template <int D, bool KV8, bool BAL = false, int G = 1>
+// on the VALU q.k path (metric shape 92.2 vs 93.0 with 2). MF: q.k on the matrix cores
+// (more than 4 q heads per kv head), where an fp8 cache keeps 2 pages in flight in either
+// kernel (32/8/128 B=32 ctx 8192 but for the heads, us, 4 -> 2 pages: 64/8 one pass 92.2
+// -> 91.5, balanced 92.1 -> 90.7-90.8; 128/8 one pass 93.1-93.3 -> 92.3-92.5, balanced
+// 95.1 -> 93.5-93.7; 64/8 ragged B=128 198.1-203.5 -> 201.9-202.2).
+template <int D, bool KV8, bool BAL = false, int G = 1, bool MF = false>
 constexpr int prefetch_depth() {
   if constexpr (KV8) {
     if constexpr (DK_PREFETCH_DEPTH_KV8 != 0) return DK_PREFETCH_DEPTH_KV8;
-    else if constexpr (BAL && G <= 4 && D <= 128) return 2;
+    else if constexpr (D <= 128 && (MF || (BAL && G <= 4))) return 2;
     else return D <= 128 ? 4 : 2;
   } else {
     return DK_PREFETCH_DEPTH ? DK_PREFETCH_DEPTH : (D <= 128 ? 2 : 1);
@@ -1326,7 +1331,7 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
-    constexpr int depth = prefetch_depth<D, KV8, BAL, WV::HEADS>();
+    constexpr int depth = prefetch_depth<D, KV8, BAL, WV::HEADS, WV::MF>();
     if constexpr (LDS) {
       stream_lds<lds_depth<D, KV8>(), CAP>(wv, ring, nk, pk, vk);
     } else if constexpr (depth <= 2) {
@@ -1346,7 +1351,7 @@ __device__ __forceinline__ void stream_interleaved(WV& wv, int NW, int w, int n,
 // spare for it: two of its kernels spilled.)
 template <int D, bool KV8, bool LDS, bool MFMA, bool BAL = false, int G = 1>
 constexpr bool first_page_by_caller() {
-  return !LDS && !MFMA && prefetch_depth<D, KV8, BAL, G>() <= 2;
+  return !LDS && !MFMA && prefetch_depth<D, KV8, BAL, G, MFMA>() <= 2;
 }
 
 // stream_interleaved with this wavefront's first page (page w of the run) already loading
@@ -1362,7 +1367,8 @@ __device__ __forceinline__ void stream_loaded(WV& wv, int NW, int w, int n, Page
   if (nk > 0) {
     auto pk = [&](int k) { return page(w + NW * k); };
     auto vk = [&](int k) { return valid(w + NW * k); };
-    stream_pages<prefetch_depth<D, KV8, BAL, WV::HEADS>(), CAP, false>(wv, ka, va, nk, pk, vk);
+    stream_pages<prefetch_depth<D, KV8, BAL, WV::HEADS, WV::MF>(), CAP, false>(wv, ka, va, nk,
+                                                                               pk, vk);
   }
 }
 
